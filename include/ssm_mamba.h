@@ -1,0 +1,118 @@
+/*
+ * ssm_mamba.h -- C ABI of the MI355X (gfx950) selective-scan library
+ * (libssm_mamba_hip.so).
+ *
+ * Plain pointers and sizes only.  Every pointer is a device pointer on the
+ * current HIP device unless stated otherwise; tensors are dense row-major.
+ * Every call is asynchronous on `stream` (a hipStream_t; NULL = the default
+ * stream) and returns SSM_OK or an error code, with a message available from
+ * ssm_last_error() (per calling thread).
+ *
+ * Element types (`dtype`): SSM_F32 or SSM_BF16 for the streamed tensors
+ * (u, delta, z, out, dout, du, ddelta, dz, B, C, dB, dC, x, dt); parameters
+ * (A, D, delta_bias), states and their gradients are always fp32.  Arithmetic
+ * is fp32 throughout.
+ *
+ * Shapes: u/delta/z/out/dout/du/ddelta/dz (batch, dim, seqlen);
+ * B/C/dB/dC (batch, nstate, seqlen); A/dA (dim, nstate); D/delta_bias/dD/
+ * ddelta_bias (dim); h_init/h_last/dh_last/dh_init (batch, dim, nstate);
+ * h_chunks (batch, dim, ssm_scan_nchunks(seqlen), nstate): the state after
+ * each SSM_CHUNK steps (the last entry is the final state); length (batch)
+ * int64.
+ */
+#ifndef SSM_MAMBA_H_
+#define SSM_MAMBA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { SSM_F32 = 0, SSM_BF16 = 1 };
+enum { SSM_OK = 0, SSM_ERR_INVALID = 1, SSM_ERR_UNSUPPORTED = 2, SSM_ERR_HIP = 3 };
+enum { SSM_CHUNK = 16 };
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* ssm_last_error(void);
+
+/* Library ABI version (bumped on any signature change). */
+int ssm_abi_version(void);
+
+/* Number of saved states per row: ceil(seqlen / SSM_CHUNK). */
+int64_t ssm_scan_nchunks(int64_t seqlen);
+
+/* Device workspace (bytes) for ssm_selective_scan_fwd / _bwd. */
+size_t ssm_scan_fwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate);
+size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate);
+
+/*
+ * Selective-scan forward.  Replaces selective_scan_forward
+ * (csrc/selective_scan/selective_scan.cpp:212-292, declared at
+ * csrc/selective_scan/selective_scan.h:73-84) behind the pybind binding
+ * selective_scan.forward (csrc/selective_scan/bindings.cpp:6).
+ *
+ *   out      = (D*u + sum_n C*h) [* silu(z)]  with h_t = exp(delta_t*A) h_{t-1}
+ *              + delta_t*u_t*B_t, delta = softplus(delta_raw + delta_bias)
+ *              (no softplus when delta_softplus == 0)
+ *   h_chunks = states after each SSM_CHUNK steps, or NULL (inference); then
+ *              h_last (nullable) receives the final state.
+ * D, delta_bias, h_init, length, z are nullable.  padding_right: 1 = valid
+ * positions are t < length[b], 0 = t >= seqlen - length[b] (lengths are
+ * clamped to [0, seqlen]); padded steps leave the state unchanged.
+ * nstate <= 256.  workspace: ssm_scan_fwd_workspace_bytes() bytes.
+ */
+int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
+                           const void* u, const void* delta, const float* A, const void* B,
+                           const void* C, const float* D, const float* delta_bias,
+                           const float* h_init, const int64_t* length, int padding_right,
+                           const void* z, int delta_softplus, void* out, float* h_chunks,
+                           float* h_last, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Selective-scan backward.  Replaces selective_scan_backward
+ * (csrc/selective_scan/selective_scan.cpp:294-380, declared at
+ * csrc/selective_scan/selective_scan.h:86-99) behind selective_scan.backward
+ * (csrc/selective_scan/bindings.cpp:7).
+ *
+ * Inputs as for the forward plus h_chunks (from the forward), dout (the
+ * upstream gradient of out; ignored at padded positions) and dh_last
+ * (nullable = zero).  Writes du, ddelta, dA, dB, dC (all overwritten), and
+ * when non-NULL dD, ddelta_bias, dh_init (requires h_init) and dz (requires z).
+ * nstate <= 64.  workspace: ssm_scan_bwd_workspace_bytes() bytes.  The result
+ * is deterministic (fixed-order reductions, no atomics on global memory).
+ */
+int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
+                           const void* u, const void* delta, const float* A, const void* B,
+                           const void* C, const float* D, const float* delta_bias,
+                           const float* h_init, const int64_t* length, int padding_right,
+                           const void* z, int delta_softplus, const float* h_chunks,
+                           const void* dout, const float* dh_last, void* du, void* ddelta,
+                           float* dA, void* dB, void* dC, float* dD, float* ddelta_bias,
+                           float* dh_init, void* dz, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/*
+ * One decode step.  Replaces selective_update
+ * (csrc/selective_update/selective_update.cpp:78-130, declared at
+ * csrc/selective_update/selective_update.h:32-41) behind
+ * selective_update.apply (csrc/selective_update/bindings.cpp:6).
+ *
+ *   new_state = exp(delta*A)*state + delta*x*B,  delta = softplus(dt + dt_bias)
+ *   out       = (D*x + sum_n C*new_state) [* silu(z)]
+ * state, new_state (batch, dim, nstate) fp32 -- new_state may equal state for
+ * an in-place update; x, dt, z, out (batch, dim); B, C (batch, nstate).
+ * D, dt_bias, z nullable.  nstate <= 256.
+ */
+int ssm_selective_state_update(int64_t batch, int64_t dim, int64_t nstate, int dtype,
+                               const float* state, float* new_state, const void* x,
+                               const void* dt, const float* A, const void* B, const void* C,
+                               const float* D, const float* dt_bias, const void* z,
+                               int dt_softplus, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SSM_MAMBA_H_ */

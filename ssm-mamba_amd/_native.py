@@ -1,0 +1,84 @@
+"""ctypes binding of the C ABI in include/ssm_mamba.h (libssm_mamba_hip.so).
+
+The library must have been built (``__graft_entry__.build()`` or
+``python ssm-mamba_amd/_build.py``); there is no fallback implementation, so a
+missing library raises immediately.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from ._build import LIB_PATH
+
+_lock = threading.Lock()
+_lib = None
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_sz = ctypes.c_size_t
+
+SSM_F32 = 0
+SSM_BF16 = 1
+SSM_CHUNK = 16
+
+# exported symbol -> (restype, argtypes)
+SIGNATURES = {
+    "ssm_last_error": (ctypes.c_char_p, []),
+    "ssm_abi_version": (_i32, []),
+    "ssm_scan_nchunks": (_i64, [_i64]),
+    "ssm_scan_fwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "ssm_scan_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "ssm_selective_scan_fwd": (_i32, [
+        _i64, _i64, _i64, _i64, _i32,          # batch, dim, seqlen, nstate, dtype
+        _p, _p, _p, _p, _p, _p, _p, _p, _p,    # u, delta, A, B, C, D, delta_bias, h_init, length
+        _i32, _p, _i32,                        # padding_right, z, delta_softplus
+        _p, _p, _p,                            # out, h_chunks, h_last
+        _p, _sz, _p,                           # workspace, bytes, stream
+    ]),
+    "ssm_selective_scan_bwd": (_i32, [
+        _i64, _i64, _i64, _i64, _i32,
+        _p, _p, _p, _p, _p, _p, _p, _p, _p,    # u, delta, A, B, C, D, delta_bias, h_init, length
+        _i32, _p, _i32,                        # padding_right, z, delta_softplus
+        _p, _p, _p,                            # h_chunks, dout, dh_last
+        _p, _p, _p, _p, _p, _p, _p, _p, _p,    # du, ddelta, dA, dB, dC, dD, ddelta_bias, dh_init, dz
+        _p, _sz, _p,                           # workspace, bytes, stream
+    ]),
+    "ssm_selective_state_update": (_i32, [
+        _i64, _i64, _i64, _i32,                # batch, dim, nstate, dtype
+        _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,  # state, new_state, x, dt, A, B, C, D, dt_bias, z
+        _i32, _p, _p,                          # dt_softplus, out, stream
+    ]),
+}
+
+ABI_VERSION = 1
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"ssm_mamba_amd: HIP library not found at {LIB_PATH}; build it with "
+                    "`python -c 'import __graft_entry__ as g; g.build()'`")
+            l = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                f = getattr(l, name)
+                f.restype = res
+                f.argtypes = args
+            if l.ssm_abi_version() != ABI_VERSION:
+                raise RuntimeError("ssm_mamba_amd: HIP library ABI version mismatch; rebuild it")
+            _lib = l
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = lib().ssm_last_error().decode(errors="replace")
+        raise RuntimeError(msg or f"ssm_mamba_amd: error code {rc}")

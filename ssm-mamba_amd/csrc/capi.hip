@@ -1,0 +1,229 @@
+// C ABI of the selective-scan library: argument validation, workspace
+// carving, dispatch to the gfx950 kernels.  See include/ssm_mamba.h.
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/ssm_mamba.h"
+#include "ss_io.cuh"
+#include "ss_params.h"
+
+namespace ssm {
+hipError_t launch_scan_fwd(const ScanParams& p, int dtype, bool aligned, float* bc, hipStream_t st);
+hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* bc, hipStream_t st);
+hipError_t launch_state_update(const UpdateParams& p, int dtype, bool vecN, hipStream_t st);
+size_t bc_prep_floats(int batch, int nstate, int seqlen);
+size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen);
+}  // namespace ssm
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return SSM_OK;
+  return fail(SSM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+size_t round256(size_t bytes) { return (bytes + 255) & ~(size_t)255; }
+
+int check_common(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
+                 int max_nstate) {
+  if (dtype != SSM_F32 && dtype != SSM_BF16)
+    return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16 (got %d)", dtype);
+  if (batch < 1 || dim < 1 || seqlen < 1 || nstate < 1)
+    return fail(SSM_ERR_INVALID, "batch, dim, seqlen and nstate must be >= 1 (got %lld, %lld, %lld, %lld)",
+                (long long)batch, (long long)dim, (long long)seqlen, (long long)nstate);
+  if (nstate > max_nstate)
+    return fail(SSM_ERR_UNSUPPORTED, "selective_scan only supports state_dim <= %d (got %lld)",
+                max_nstate, (long long)nstate);
+  if (batch > 65535) return fail(SSM_ERR_UNSUPPORTED, "batch must be <= 65535 (got %lld)", (long long)batch);
+  if (dim > INT_MAX / 2 || seqlen > INT_MAX / 2)
+    return fail(SSM_ERR_UNSUPPORTED, "dim and seqlen must be < 2^30");
+  return SSM_OK;
+}
+
+ssm::ScanParams make_scan_params(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate,
+                                 const void* u, const void* delta, const float* A, const void* B,
+                                 const void* C, const float* D, const float* delta_bias,
+                                 const float* h_init, const int64_t* length, int padding_right,
+                                 const void* z, int delta_softplus) {
+  ssm::ScanParams p{};
+  p.batch = (int)batch;
+  p.dim = (int)dim;
+  p.seqlen = (int)seqlen;
+  p.nstate = (int)nstate;
+  p.nchunks = (int)((seqlen + ssm::kChunk - 1) / ssm::kChunk);
+  p.nblk = (int)((dim + ssm::kBlockCh - 1) / ssm::kBlockCh);
+  p.pad_right = padding_right ? 1 : 0;
+  p.softplus = delta_softplus ? 1 : 0;
+  p.u = u;
+  p.delta = delta;
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.D = D;
+  p.bias = delta_bias;
+  p.h_init = h_init;
+  p.length = length;
+  p.z = z;
+  return p;
+}
+
+bool scan_aligned(int dtype, int64_t seqlen, std::initializer_list<const void*> ptrs) {
+  const int vec = dtype == SSM_BF16 ? 8 : 4;
+  if (seqlen % vec) return false;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return false;
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ssm_last_error(void) { return g_err.c_str(); }
+
+int ssm_abi_version(void) { return 1; }
+
+int64_t ssm_scan_nchunks(int64_t seqlen) { return seqlen <= 0 ? 0 : (seqlen + SSM_CHUNK - 1) / SSM_CHUNK; }
+
+size_t ssm_scan_fwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate) {
+  (void)dim;
+  if (batch < 1 || seqlen < 1 || nstate < 1) return 0;
+  return round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
+}
+
+size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate) {
+  if (batch < 1 || dim < 1 || seqlen < 1 || nstate < 1) return 0;
+  const size_t nblk = (dim + ssm::kBlockCh - 1) / ssm::kBlockCh;
+  return round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float)) +
+         round256(2 * nblk * batch * nstate * seqlen * sizeof(float)) +
+         round256((size_t)batch * dim * nstate * sizeof(float)) +
+         2 * round256((size_t)batch * dim * sizeof(float));
+}
+
+int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
+                           const void* u, const void* delta, const float* A, const void* B,
+                           const void* C, const float* D, const float* delta_bias,
+                           const float* h_init, const int64_t* length, int padding_right,
+                           const void* z, int delta_softplus, void* out, float* h_chunks,
+                           float* h_last, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  if (int e = check_common(batch, dim, seqlen, nstate, dtype, 256)) return e;
+  if (!u || !delta || !A || !B || !C || !out)
+    return fail(SSM_ERR_INVALID, "u, delta, A, B, C and out must be non-NULL");
+  const size_t need = ssm_scan_fwd_workspace_bytes(batch, dim, seqlen, nstate);
+  if (!workspace || workspace_bytes < need)
+    return fail(SSM_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+  ssm::ScanParams p = make_scan_params(batch, dim, seqlen, nstate, u, delta, A, B, C, D, delta_bias,
+                                       h_init, length, padding_right, z, delta_softplus);
+  p.out = out;
+  p.h_chunks = h_chunks;
+  p.h_last = h_last;
+  const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out});
+  return hip_status(ssm::launch_scan_fwd(p, dtype, aligned, static_cast<float*>(workspace),
+                                         static_cast<hipStream_t>(stream)),
+                    "selective_scan forward launch");
+}
+
+int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
+                           const void* u, const void* delta, const float* A, const void* B,
+                           const void* C, const float* D, const float* delta_bias,
+                           const float* h_init, const int64_t* length, int padding_right,
+                           const void* z, int delta_softplus, const float* h_chunks,
+                           const void* dout, const float* dh_last, void* du, void* ddelta,
+                           float* dA, void* dB, void* dC, float* dD, float* ddelta_bias,
+                           float* dh_init, void* dz, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  g_err.clear();
+  if (int e = check_common(batch, dim, seqlen, nstate, dtype, 64)) return e;
+  if (!u || !delta || !A || !B || !C || !h_chunks || !dout || !du || !ddelta || !dA || !dB || !dC)
+    return fail(SSM_ERR_INVALID,
+                "u, delta, A, B, C, h_chunks, dout, du, ddelta, dA, dB and dC must be non-NULL");
+  if (dh_init && !h_init) return fail(SSM_ERR_INVALID, "dh_init requires h_init");
+  if (dz && !z) return fail(SSM_ERR_INVALID, "dz requires z");
+  const size_t need = ssm_scan_bwd_workspace_bytes(batch, dim, seqlen, nstate);
+  if (!workspace || workspace_bytes < need)
+    return fail(SSM_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+  ssm::ScanParams p = make_scan_params(batch, dim, seqlen, nstate, u, delta, A, B, C, D, delta_bias,
+                                       h_init, length, padding_right, z, delta_softplus);
+  p.h_chunks_in = h_chunks;
+  p.dout = dout;
+  p.dh_last = dh_last;
+  p.du = du;
+  p.ddelta = ddelta;
+  p.dz = dz;
+  p.dh_init = dh_init;
+  p.dA = dA;
+  p.dB = dB;
+  p.dC = dC;
+  p.dD = dD;
+  p.dbias = ddelta_bias;
+  // workspace: [prepped B/C][dB/dC partials][dA partials][dD partials][dbias partials]
+  char* ws = static_cast<char*>(workspace);
+  float* bc = reinterpret_cast<float*>(ws);
+  ws += round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
+  p.ws_bc = reinterpret_cast<float*>(ws);
+  ws += round256(2 * (size_t)p.nblk * batch * nstate * seqlen * sizeof(float));
+  p.ws_A = reinterpret_cast<float*>(ws);
+  ws += round256((size_t)batch * dim * nstate * sizeof(float));
+  p.ws_D = reinterpret_cast<float*>(ws);
+  ws += round256((size_t)batch * dim * sizeof(float));
+  p.ws_bias = reinterpret_cast<float*>(ws);
+  const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, dout, du, ddelta, dz});
+  return hip_status(ssm::launch_scan_bwd(p, dtype, aligned, bc, static_cast<hipStream_t>(stream)),
+                    "selective_scan backward launch");
+}
+
+int ssm_selective_state_update(int64_t batch, int64_t dim, int64_t nstate, int dtype,
+                               const float* state, float* new_state, const void* x,
+                               const void* dt, const float* A, const void* B, const void* C,
+                               const float* D, const float* dt_bias, const void* z,
+                               int dt_softplus, void* out, void* stream) {
+  g_err.clear();
+  if (int e = check_common(batch, dim, 1, nstate, dtype, 256)) return e;
+  if ((uint64_t)batch * (uint64_t)dim * 64 > (uint64_t)UINT_MAX * 256)
+    return fail(SSM_ERR_UNSUPPORTED, "batch * dim too large");
+  if (!state || !new_state || !x || !dt || !A || !B || !C || !out)
+    return fail(SSM_ERR_INVALID, "state, new_state, x, dt, A, B, C and out must be non-NULL");
+  ssm::UpdateParams p{};
+  p.batch = (int)batch;
+  p.dim = (int)dim;
+  p.nstate = (int)nstate;
+  p.softplus = dt_softplus ? 1 : 0;
+  p.state = state;
+  p.new_state = new_state;
+  p.x = x;
+  p.dt = dt;
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.D = D;
+  p.bias = dt_bias;
+  p.z = z;
+  p.out = out;
+  // 128-bit path: whole float4 groups and a power-of-two lane count per (b, d)
+  const int nq = (int)((nstate + 3) / 4);
+  const bool pow2 = (nq & (nq - 1)) == 0;
+  const bool vecN = nstate % 4 == 0 && pow2 && aligned16(state) && aligned16(new_state) &&
+                    aligned16(A) && (dtype == SSM_F32 ? aligned16(B) && aligned16(C)
+                                                      : (((uintptr_t)B | (uintptr_t)C) & 7) == 0);
+  return hip_status(ssm::launch_state_update(p, dtype, vecN, static_cast<hipStream_t>(stream)),
+                    "selective_state_update launch");
+}
+
+}  // extern "C"

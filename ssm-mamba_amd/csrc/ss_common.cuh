@@ -1,0 +1,176 @@
+#include <algorithm>
+// Device helpers shared by the selective-scan and state-update kernels (gfx950).
+//
+// Element types: the streamed tensors (u, delta, z, out, dout, du, ddelta, dz,
+// B, C, dB, dC) are either fp32 or bf16; all arithmetic is fp32.  Parameters
+// (A, D, delta_bias), states and state gradients are fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+namespace ssm {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------- bf16 / fp32 I/O
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  // round-to-nearest-even; lowers to v_cvt_pk_bf16_f32 on gfx950
+  __hip_bfloat16 a = __float2bfloat16(lo);
+  __hip_bfloat16 b = __float2bfloat16(hi);
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+template <typename T> struct Elem;
+
+template <> struct Elem<float> {
+  static constexpr int kVec = 4;  // elements per 128-bit access
+  __device__ static __forceinline__ float load1(const float* p) { return *p; }
+  __device__ static __forceinline__ void store1(float* p, float v) { *p = v; }
+  // 128-bit load of kVec elements
+  __device__ static __forceinline__ void loadv(const float* p, float (&v)[4]) {
+    float4 x = *reinterpret_cast<const float4*>(p);
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+  }
+  __device__ static __forceinline__ void storev(float* p, const float (&v)[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+  // 4 consecutive elements (16 B for fp32)
+  __device__ static __forceinline__ void load4(const float* p, float (&v)[4]) { loadv(p, v); }
+};
+
+template <> struct Elem<__hip_bfloat16> {
+  static constexpr int kVec = 8;
+  using T = __hip_bfloat16;
+  __device__ static __forceinline__ float load1(const T* p) {
+    return __uint_as_float((uint32_t)(*reinterpret_cast<const uint16_t*>(p)) << 16);
+  }
+  __device__ static __forceinline__ void store1(T* p, float v) { *p = __float2bfloat16(v); }
+  __device__ static __forceinline__ void loadv(const T* p, float (&v)[8]) {
+    uint4 x = *reinterpret_cast<const uint4*>(p);
+    v[0] = bf16_lo(x.x); v[1] = bf16_hi(x.x); v[2] = bf16_lo(x.y); v[3] = bf16_hi(x.y);
+    v[4] = bf16_lo(x.z); v[5] = bf16_hi(x.z); v[6] = bf16_lo(x.w); v[7] = bf16_hi(x.w);
+  }
+  __device__ static __forceinline__ void storev(T* p, const float (&v)[8]) {
+    uint4 x;
+    x.x = pack_bf16x2(v[0], v[1]); x.y = pack_bf16x2(v[2], v[3]);
+    x.z = pack_bf16x2(v[4], v[5]); x.w = pack_bf16x2(v[6], v[7]);
+    *reinterpret_cast<uint4*>(p) = x;
+  }
+  // 4 consecutive elements (8 B for bf16)
+  __device__ static __forceinline__ void load4(const T* p, float (&v)[4]) {
+    uint2 x = *reinterpret_cast<const uint2*>(p);
+    v[0] = bf16_lo(x.x); v[1] = bf16_hi(x.x); v[2] = bf16_lo(x.y); v[3] = bf16_hi(x.y);
+  }
+};
+
+// ---------------------------------------------------------------- math
+
+// 2^x on the transcendental unit (v_exp_f32).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// log1p(e) for e >= 0 by Goldberg's correction: w = 1 + e rounded; when w != 1,
+// log(w) * e / (w - 1) recovers the digits lost in forming w (D. Goldberg,
+// "What every computer scientist should know about floating-point
+// arithmetic", 1991, Theorem 4).
+__device__ __forceinline__ float log1p_pos(float e) {
+  float w = 1.0f + e;
+  float lw = fast_log2(w) * kLn2;
+  float r = lw * e * fast_rcp(w - 1.0f);
+  return (w == 1.0f) ? e : r;
+}
+
+// softplus with the reference threshold: x <= 20 ? log1p(exp(x)) : x.
+// Evaluated as max(x,0) + log1p(exp(-|x|)), which is the same function and keeps
+// exp's argument non-positive.
+__device__ __forceinline__ float softplus_t20(float x) {
+  float e = fast_exp2(-fabsf(x) * kLog2e);
+  float v = fmaxf(x, 0.0f) + log1p_pos(e);
+  return x > 20.0f ? x : v;
+}
+
+__device__ __forceinline__ float sigmoidf_fast(float x) {
+  return fast_rcp(1.0f + fast_exp2(-x * kLog2e));
+}
+
+// d softplus/dx with the reference threshold (sigmoid below 20, 1 above).
+__device__ __forceinline__ float softplus_grad_t20(float x) {
+  return x > 20.0f ? 1.0f : sigmoidf_fast(x);
+}
+
+// ---------------------------------------------------------------- wave64 primitives
+
+// DPP controls (GCN/CDNA encoding)
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xF, 0xF, true));
+}
+
+// One reduce-scatter level that folds lane bit `kBit` using a DPP pattern whose
+// partner differs from the lane in that bit.  p, q are the two halves of a
+// pair of values; the lane keeps the half selected by its bit and receives the
+// partner's copy of the same half.
+template <int kCtrl>
+__device__ __forceinline__ float rs_fold(float p, float q, bool bit) {
+  float keep = bit ? q : p;
+  float send = bit ? p : q;
+  return keep + dpp_mov<kCtrl>(send);
+}
+
+// Reduce-scatter of K values held by every lane of a wave64: afterwards the
+// sum over the 64 lanes of value index (lane * K/64 + j) is in v[j] of `lane`,
+// for j < K/64.  Cost ~2.2 VALU per input value (permlane32/16 swaps for the
+// two upper levels, DPP for the four lower ones).
+template <int K>
+__device__ __forceinline__ void wave_reduce_scatter(float (&v)[K], int lane) {
+  static_assert(K >= 64 && (K & (K - 1)) == 0, "K must be a power of two >= 64");
+#pragma unroll
+  for (int i = 0; i < K / 2; ++i) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + K / 2]),
+                                              false, false);
+    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < K / 4; ++i) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + K / 4]),
+                                              false, false);
+    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  const bool b3 = lane & 8, b2 = lane & 4, b1 = lane & 2, b0 = lane & 1;
+#pragma unroll
+  for (int i = 0; i < K / 8; ++i) v[i] = rs_fold<kDppRowRor8>(v[i], v[i + K / 8], b3);
+#pragma unroll
+  for (int i = 0; i < K / 16; ++i) v[i] = rs_fold<kDppRowHalfMirror>(v[i], v[i + K / 16], b2);
+#pragma unroll
+  for (int i = 0; i < K / 32; ++i) v[i] = rs_fold<kDppQuadXor2>(v[i], v[i + K / 32], b1);
+#pragma unroll
+  for (int i = 0; i < K / 64; ++i) v[i] = rs_fold<kDppQuadXor1>(v[i], v[i + K / 64], b0);
+}
+
+// Sum over groups of kW consecutive lanes (kW power of two <= 64); every lane
+// of a group gets the group sum.
+template <int kW>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < kW; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+__device__ __forceinline__ int wave_id_uniform() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
+}  // namespace ssm

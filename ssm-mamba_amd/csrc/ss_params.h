@@ -1,0 +1,88 @@
+// Kernel argument blocks for the selective-scan and state-update kernels.
+// All tensors are dense and row-major:
+//   u, delta, z, out, dout, du, ddelta, dz : (batch, dim, seqlen)
+//   B, C, dB, dC                           : (batch, nstate, seqlen)
+//   A, dA                                  : (dim, nstate)          fp32
+//   D, delta_bias, dD, ddelta_bias         : (dim,)                 fp32
+//   h_init, h_last, dh_last, dh_init       : (batch, dim, nstate)   fp32
+//   h_chunks                               : (batch, dim, nchunks, nstate) fp32,
+//                                            state after each kChunk steps
+//   length                                 : (batch,) int64
+#pragma once
+
+#include <stdint.h>
+
+namespace ssm {
+
+constexpr int kChunk = 16;    // steps between saved states
+constexpr int kTileT = 64;    // steps staged through LDS per tile
+constexpr int kBlockCh = 64;  // channels per workgroup (one per lane)
+
+// Scalar shape/flag block passed to the scan kernels (pointers travel as
+// separate __restrict__ kernel arguments).
+struct ScanDims {
+  int batch, dim, seqlen, nstate, nchunks, nblk;
+  int pad_right;
+  int softplus;
+};
+
+struct ScanParams {
+  int batch, dim, seqlen, nstate, nchunks, nblk;
+  int pad_right;  // 1: valid t < len; 0: valid t >= seqlen - len
+  int softplus;   // 1: delta = softplus(delta + bias); 0: delta + bias
+
+  const void* u;
+  const void* delta;
+  const float* A;
+  const void* B;
+  const void* C;
+  const float* D;      // nullable
+  const float* bias;   // nullable
+  const float* h_init; // nullable
+  const int64_t* length;  // nullable
+  const void* z;       // nullable
+
+  // forward outputs
+  void* out;
+  float* h_chunks;  // nullable (then h_last)
+  float* h_last;    // nullable
+
+  // backward
+  const float* h_chunks_in;
+  const void* dout;
+  const float* dh_last;  // nullable
+  void* du;
+  void* ddelta;
+  void* dz;          // nullable (needs z)
+  float* dh_init;    // nullable (needs h_init)
+  float* ws_bc;      // (2, nblk, batch, nstate, seqlen) dB/dC partial sums per channel block
+  float* ws_A;       // (batch, dim, nstate) dA partial sums per batch row
+  float* ws_D;       // (batch, dim)
+  float* ws_bias;    // (batch, dim)
+  float* dA;
+  void* dB;
+  void* dC;
+  float* dD;      // nullable
+  float* dbias;   // nullable
+};
+
+struct UpdateParams {
+  int batch, dim, nstate, softplus;
+  const float* state;
+  float* new_state;  // may alias state
+  const void* x;
+  const void* dt;
+  const float* A;
+  const void* B;
+  const void* C;
+  const float* D;      // nullable
+  const float* bias;   // nullable
+  const void* z;       // nullable
+  void* out;
+};
+
+inline ScanDims dims_of(const ScanParams& p) {
+  return ScanDims{p.batch, p.dim, p.seqlen, p.nstate, p.nchunks, p.nblk, p.pad_right, p.softplus};
+}
+
+}  // namespace ssm

@@ -1,0 +1,213 @@
+"""GPU parity of the HIP selective scan (forward + backward) against the CPU
+oracle on the same seeded, dtype-rounded inputs, through the C ABI."""
+import pytest
+import torch
+
+from oracle import scan_ref as R
+from tests.helpers import assert_close, make_case, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _ss():
+    from ssm_mamba_amd import selective_scan
+    return selective_scan
+
+
+def run_case(cuda, batch, dim, seqlen, nstate, dtype, *, seed=0, with_z=True, h_init=False,
+             length=None, padding_side="right", softplus=True, dlast=False, delta_shift=0.0,
+             bwd=True, with_D=True, with_bias=True):
+    ss = _ss()
+    c = make_case(batch, dim, seqlen, nstate, dtype, seed=seed, with_z=with_z, h_init=h_init,
+                  delta_shift=delta_shift)
+    if not with_D:
+        c["D"] = None
+    if not with_bias:
+        c["delta_bias"] = None
+    d = to_dev(c, cuda)
+    ln_dev = None if length is None else length.to(cuda)
+    pr = (padding_side or "right") == "right"
+    out, h = ss.forward(d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"],
+                        d["h_init"], ln_dev, padding_side, z=d["z"], delta_softplus=softplus)
+    ref = R.scan_fwd(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["delta_bias"],
+                     c["h_init"], length, pr, c["z"], softplus)
+    torch.cuda.synchronize()
+    assert_close(out, ref["y"], dtype, "out")
+    assert_close(h, ref["h_chunks"], torch.float32 if dtype == torch.float32 else dtype, "h_chunks",
+                 scale_atol=True)
+    if not bwd:
+        return
+    g = torch.Generator().manual_seed(seed + 100)
+    dy = torch.randn(batch, dim, seqlen, generator=g).to(dtype)
+    dl = torch.randn(batch, dim, nstate, generator=g) if dlast else None
+    res = ss.backward(d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"], h,
+                      d["h_init"], dy.to(cuda), None if dl is None else dl.to(cuda), ln_dev,
+                      padding_side, z=d["z"], delta_softplus=softplus)
+    rb = R.scan_bwd(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["delta_bias"],
+                    c["h_init"], length, pr, c["z"], softplus, dy=dy, dh_last=dl)
+    torch.cuda.synchronize()
+    names = ["du", "dA", "dB", "dC", "dD", "ddelta", "ddelta_bias", "dh_init"]
+    for nm, got in zip(names, res[:8]):
+        if rb[nm] is None or got is None:
+            assert (nm == "dh_init" and not h_init) or (nm == "dD" and not with_D) or \
+                (nm == "ddelta_bias" and not with_bias), nm
+            continue
+        assert_close(got, rb[nm], dtype, nm, scale_atol=nm in ("dA", "dB", "dC", "dD", "ddelta_bias"))
+    if with_z:
+        assert_close(res[8], rb["dz"], dtype, "dz")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_small_aligned(cuda, dtype):
+    run_case(cuda, 2, 96, 200, 16, dtype, seed=1, h_init=True, dlast=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("seqlen", [1, 5, 16, 37, 64, 65, 129])
+def test_ragged_lengths(cuda, dtype, seqlen):
+    run_case(cuda, 1, 70, seqlen, 16, dtype, seed=seqlen, h_init=True, dlast=True)
+
+
+@pytest.mark.parametrize("nstate", [1, 4, 8, 12, 16, 20, 32, 64])
+def test_state_dims(cuda, nstate):
+    run_case(cuda, 2, 64, 80, nstate, torch.float32, seed=nstate, h_init=True, dlast=True)
+
+
+@pytest.mark.parametrize("nstate", [128, 200, 256])
+def test_state_dims_forward_large(cuda, nstate):
+    run_case(cuda, 1, 64, 48, nstate, torch.float32, seed=nstate, bwd=False)
+
+
+@pytest.mark.parametrize("padding_side", ["right", "left"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lengths(cuda, padding_side, dtype):
+    length = torch.tensor([150, 0, 1, 200], dtype=torch.int64)
+    run_case(cuda, 4, 64, 200, 16, dtype, seed=7, length=length, padding_side=padding_side,
+             h_init=True, dlast=True)
+
+
+def test_no_softplus_no_z_no_D(cuda):
+    run_case(cuda, 2, 64, 96, 16, torch.float32, seed=8, with_z=False, softplus=False,
+             with_D=False, with_bias=False)
+
+
+def test_config0(cuda):
+    """B=2, D=1536, N=16, L=512, fp32, z."""
+    run_case(cuda, 2, 1536, 512, 16, torch.float32, seed=0)
+
+
+def test_config1_reduced_channels(cuda):
+    """Config 1 dtypes and sequence length (bf16 I/O, L=2048) on 256 channels."""
+    run_case(cuda, 2, 256, 2048, 16, torch.bfloat16, seed=1)
+
+
+def test_config3_reduced_channels(cuda):
+    """Config 3 (fp32, L=16384, delta shifted by +2) on 64 channels."""
+    run_case(cuda, 1, 64, 16384, 16, torch.float32, seed=3, delta_shift=2.0)
+
+
+def test_config1_full_size_properties(cuda):
+    """Full config-1 size: forward on a channel subset against the oracle,
+    bitwise determinism, and dB/dC additivity over channel halves."""
+    ss = _ss()
+    batch, dim, seqlen, nstate = 8, 2048, 2048, 16
+    c = make_case(batch, dim, seqlen, nstate, torch.bfloat16, seed=1)
+    d = to_dev(c, cuda)
+    out, h = ss.forward(d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"],
+                        None, None, None, z=d["z"])
+    sub = slice(0, 2048, 97)  # 22 channels spread over the channel blocks
+    cs = {k: (v[:, sub] if k in ("u", "delta", "z") else v) for k, v in c.items()}
+    cs["A"], cs["D"], cs["delta_bias"] = c["A"][sub], c["D"][sub], c["delta_bias"][sub]
+    ref = R.scan_fwd(cs["u"], cs["delta"], cs["A"], cs["B"], cs["C"], cs["D"], cs["delta_bias"],
+                     None, None, True, cs["z"], True, dtype=torch.float64)
+    assert_close(out[:, sub], ref["y"], torch.bfloat16, "out[subset]")
+    assert_close(h[:, sub], ref["h_chunks"], torch.bfloat16, "h[subset]", scale_atol=True)
+    g = torch.Generator().manual_seed(5)
+    dy = torch.randn(batch, dim, seqlen, generator=g).to(torch.bfloat16).to(cuda)
+    args = (d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"], h, None, dy, None)
+    r1 = ss.backward(*args, z=d["z"])
+    r2 = ss.backward(*args, z=d["z"])
+    for a, b_ in zip(r1, r2):
+        if a is not None:
+            assert torch.equal(a, b_), "backward is not deterministic"
+    # dB over all channels == sum of dB over two channel halves (fp32 partials)
+    halves = []
+    for lo, hi in ((0, 1024), (1024, 2048)):
+        dh = {k: (v[:, lo:hi].contiguous() if k in ("u", "delta", "z") else v) for k, v in d.items()}
+        dh["A"], dh["D"], dh["delta_bias"] = d["A"][lo:hi].contiguous(), d["D"][lo:hi].contiguous(), \
+            d["delta_bias"][lo:hi].contiguous()
+        _, hh = ss.forward(dh["u"], dh["A"], dh["B"], dh["C"], dh["D"], dh["delta"],
+                           dh["delta_bias"], None, None, None, z=dh["z"])
+        halves.append(ss.backward(dh["u"], dh["A"], dh["B"], dh["C"], dh["D"], dh["delta"],
+                                  dh["delta_bias"], hh, None, dy[:, lo:hi].contiguous(), None,
+                                  z=dh["z"]))
+    for idx, nm in ((2, "dB"), (3, "dC")):
+        tot = halves[0][idx].float() + halves[1][idx].float()
+        assert_close(r1[idx].float(), tot, torch.bfloat16, nm + " additivity")
+    # per-channel gradients of the subset against the oracle
+    rb = R.scan_bwd(cs["u"], cs["delta"], cs["A"], cs["B"], cs["C"], cs["D"], cs["delta_bias"],
+                    None, None, True, cs["z"], True, dy=dy.cpu()[:, sub], dh_last=None)
+    assert_close(r1[0][:, sub], rb["du"], torch.bfloat16, "du[subset]")
+    assert_close(r1[5][:, sub], rb["ddelta"], torch.bfloat16, "ddelta[subset]")
+    assert_close(r1[8][:, sub], rb["dz"], torch.bfloat16, "dz[subset]")
+    assert_close(r1[1][sub], rb["dA"], torch.bfloat16, "dA[subset]", scale_atol=True)
+    assert_close(r1[4][sub], rb["dD"], torch.bfloat16, "dD[subset]", scale_atol=True)
+    assert_close(r1[6][sub], rb["ddelta_bias"], torch.bfloat16, "dbias[subset]", scale_atol=True)
+
+
+def test_split_sequence_on_gpu(cuda):
+    """scan(x) == scan(x[:k]) then scan(x[k:], h_init=h_last), on the GPU."""
+    ss = _ss()
+    c = to_dev(make_case(2, 128, 256, 16, torch.float32, seed=9), cuda)
+    out, h = ss.forward(c["u"], c["A"], c["B"], c["C"], c["D"], c["delta"], c["delta_bias"],
+                        None, None, None, z=c["z"])
+    k = 96
+    p1 = {n: c[n][..., :k].contiguous() for n in ("u", "delta", "B", "C", "z")}
+    p2 = {n: c[n][..., k:].contiguous() for n in ("u", "delta", "B", "C", "z")}
+    o1, h1 = ss.forward(p1["u"], c["A"], p1["B"], p1["C"], c["D"], p1["delta"], c["delta_bias"],
+                        None, None, None, z=p1["z"])
+    o2, h2 = ss.forward(p2["u"], c["A"], p2["B"], p2["C"], c["D"], p2["delta"], c["delta_bias"],
+                        h1[:, :, -1].contiguous(), None, None, z=p2["z"])
+    torch.testing.assert_close(torch.cat([o1, o2], -1), out, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(h2[:, :, -1], h[:, :, -1], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_reference_api_autograd(cuda, dtype):
+    """SelectiveScanFn (the reference's class and argument order) through autograd."""
+    from ssm_mamba_amd.ops import SelectiveScanFn
+    batch, dim, seqlen, nstate = 2, 64, 100, 16
+    c = make_case(batch, dim, seqlen, nstate, dtype, seed=11, with_z=False, h_init=True)
+    d = to_dev(c, cuda)
+    leaves = {k: d[k].clone().requires_grad_(True)
+              for k in ("u", "A", "B", "C", "D", "delta", "delta_bias", "h_init")}
+    length = torch.tensor([100, 60])
+    out, hl = SelectiveScanFn.apply(leaves["u"], leaves["A"], leaves["B"], leaves["C"],
+                                    leaves["D"], leaves["delta"], leaves["delta_bias"],
+                                    leaves["h_init"], length.to(cuda))
+    g = torch.Generator().manual_seed(12)
+    dy = torch.randn(batch, dim, seqlen, generator=g).to(dtype)
+    dl = torch.randn(batch, dim, nstate, generator=g)
+    ((out.float() * dy.to(cuda).float()).sum() + (hl * dl.to(cuda)).sum()).backward()
+    # the reference's default padding is "left" (ops/selective_scan_interface.py:20)
+    ref = R.scan_fwd(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["delta_bias"],
+                     c["h_init"], length, False, None, True)
+    assert_close(out, ref["y"], dtype, "out")
+    assert_close(hl, ref["h_last"], dtype, "h_last", scale_atol=True)
+    rb = R.scan_bwd(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["delta_bias"],
+                    c["h_init"], length, False, None, True, dy=dy, dh_last=dl)
+    for k, nm in (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC"),
+                  ("D", "dD"), ("delta_bias", "ddelta_bias"), ("h_init", "dh_init")):
+        assert_close(leaves[k].grad, rb[nm], dtype, nm, scale_atol=nm in ("dA", "dB", "dC", "dD", "ddelta_bias"))
+
+
+def test_functional_alias(cuda):
+    from ssm_mamba_amd.ops import selective_scan_fn
+    c = make_case(1, 64, 64, 16, torch.float32, seed=13)
+    d = to_dev(c, cuda)
+    out, last = selective_scan_fn(d["u"], d["delta"], d["A"], d["B"], d["C"], d["D"], z=d["z"],
+                                  delta_bias=d["delta_bias"], return_last_state=True)
+    ref = R.scan_fwd(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["delta_bias"], None,
+                     None, True, c["z"], True)
+    assert_close(out, ref["y"], torch.float32, "out")
+    assert_close(last, ref["h_last"], torch.float32, "last", scale_atol=True)
