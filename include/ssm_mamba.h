@@ -40,6 +40,18 @@ const char* ssm_last_error(void);
 /* Library ABI version (bumped on any signature change). */
 int ssm_abi_version(void);
 
+/*
+ * Kernel timing (measurement hook; no counterpart in the reference, whose
+ * launches are untimed).  Between ssm_profile_begin() and ssm_profile_end()
+ * every kernel this library launches is bracketed by HIP events recorded on
+ * its launch stream.  ssm_profile_end() waits for them and writes one line
+ * "<kernel> <launches> <total_ms>" per kernel into buf (NUL-terminated,
+ * truncated to buf_bytes); it returns the number of timed launches (< 0 on
+ * error).  At most 4096 launches are timed per session.
+ */
+int ssm_profile_begin(void);
+int ssm_profile_end(char* buf, size_t buf_bytes);
+
 /* Number of saved states per row: ceil(seqlen / SSM_CHUNK). */
 int64_t ssm_scan_nchunks(int64_t seqlen);
 

@@ -28,6 +28,8 @@ SSM_CHUNK = 16
 SIGNATURES = {
     "ssm_last_error": (ctypes.c_char_p, []),
     "ssm_abi_version": (_i32, []),
+    "ssm_profile_begin": (_i32, []),
+    "ssm_profile_end": (_i32, [ctypes.c_char_p, _sz]),
     "ssm_scan_nchunks": (_i64, [_i64]),
     "ssm_scan_fwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "ssm_scan_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
@@ -76,6 +78,24 @@ def lib() -> ctypes.CDLL:
                 raise RuntimeError("ssm_mamba_amd: HIP library ABI version mismatch; rebuild it")
             _lib = l
     return _lib
+
+
+def profile_begin() -> None:
+    check(lib().ssm_profile_begin())
+
+
+def profile_end() -> dict:
+    """Returns {kernel: (launches, total_ms)} for the launches timed since
+    profile_begin()."""
+    buf = ctypes.create_string_buffer(8192)
+    n = lib().ssm_profile_end(buf, len(buf))
+    if n < 0:
+        check(n)
+    res = {}
+    for line in buf.value.decode().splitlines():
+        name, cnt, ms = line.split()
+        res[name] = (int(cnt), float(ms))
+    return res
 
 
 def check(rc: int) -> None:

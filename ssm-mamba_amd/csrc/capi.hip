@@ -3,11 +3,15 @@
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
 #include <string>
 
 #include "../../include/ssm_mamba.h"
 #include "ss_io.cuh"
 #include "ss_params.h"
+#include "ss_prof.h"
+#include <mutex>
+#include <vector>
 
 namespace ssm {
 hipError_t launch_scan_fwd(const ScanParams& p, int dtype, bool aligned, float* bc, hipStream_t st);
@@ -15,6 +19,40 @@ hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* 
 hipError_t launch_state_update(const UpdateParams& p, int dtype, bool vecN, hipStream_t st);
 size_t bc_prep_floats(int batch, int nstate, int seqlen);
 size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen);
+}  // namespace ssm
+
+namespace ssm {
+
+// ---- kernel timing (see ss_prof.h)
+namespace {
+struct ProfRec {
+  const char* name;
+  hipEvent_t a, b;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<hipEvent_t> g_prof_pool;
+std::vector<ProfRec> g_prof_recs;
+constexpr size_t kProfPool = 8192;
+}  // namespace
+
+ProfScope::ProfScope(const char* name, hipStream_t st) : slot_(-1), st_(st) {
+  if (!g_prof_on) return;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  const size_t used = g_prof_recs.size() * 2;
+  if (!g_prof_on || used + 2 > g_prof_pool.size()) return;
+  ProfRec r{name, g_prof_pool[used], g_prof_pool[used + 1]};
+  if (hipEventRecord(r.a, st) != hipSuccess) return;
+  slot_ = (int)g_prof_recs.size();
+  g_prof_recs.push_back(r);
+}
+
+ProfScope::~ProfScope() {
+  if (slot_ < 0) return;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  (void)hipEventRecord(g_prof_recs[slot_].b, st_);
+}
+
 }  // namespace ssm
 
 namespace {
@@ -98,6 +136,54 @@ extern "C" {
 const char* ssm_last_error(void) { return g_err.c_str(); }
 
 int ssm_abi_version(void) { return 1; }
+
+int ssm_profile_begin(void) {
+  g_err.clear();
+  std::lock_guard<std::mutex> lk(ssm::g_prof_mu);
+  while (ssm::g_prof_pool.size() < ssm::kProfPool) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return fail(SSM_ERR_HIP, "hipEventCreate failed");
+    ssm::g_prof_pool.push_back(e);
+  }
+  ssm::g_prof_recs.clear();
+  ssm::g_prof_on = true;
+  return SSM_OK;
+}
+
+int ssm_profile_end(char* buf, size_t buf_bytes) {
+  g_err.clear();
+  std::lock_guard<std::mutex> lk(ssm::g_prof_mu);
+  ssm::g_prof_on = false;
+  std::vector<std::pair<std::string, std::pair<int, double>>> agg;
+  for (const auto& r : ssm::g_prof_recs) {
+    if (hipEventSynchronize(r.b) != hipSuccess) return fail(SSM_ERR_HIP, "hipEventSynchronize failed");
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess)
+      return fail(SSM_ERR_HIP, "hipEventElapsedTime failed");
+    bool found = false;
+    for (auto& e : agg)
+      if (e.first == r.name) {
+        e.second.first += 1;
+        e.second.second += ms;
+        found = true;
+      }
+    if (!found) agg.push_back({r.name, {1, (double)ms}});
+  }
+  std::string out;
+  for (const auto& e : agg) {
+    char line[160];
+    snprintf(line, sizeof(line), "%s %d %.6f\n", e.first.c_str(), e.second.first, e.second.second);
+    out += line;
+  }
+  if (buf && buf_bytes) {
+    const size_t n = std::min(out.size(), buf_bytes - 1);
+    memcpy(buf, out.data(), n);
+    buf[n] = 0;
+  }
+  const int nrec = (int)ssm::g_prof_recs.size();
+  ssm::g_prof_recs.clear();
+  return nrec;
+}
 
 int64_t ssm_scan_nchunks(int64_t seqlen) { return seqlen <= 0 ? 0 : (seqlen + SSM_CHUNK - 1) / SSM_CHUNK; }
 

@@ -15,18 +15,20 @@
 //
 // Work decomposition mirrors the forward (workgroup = batch row b x 64
 // channels, 4 waves, lane = channel, wave w = state group G = g*4 + w).  Tiles
-// of 64 steps are walked from the end; inside a tile, 16-step sub-chunks are
+// of kTileBwd steps are walked from the end; inside a tile, 16-step sub-chunks are
 // walked from the end.  For each sub-chunk the wave reloads the state saved by
 // the forward at the sub-chunk start, recomputes the 16 states and decay
 // factors into registers, then runs the reverse recurrence.  Per-position sums
-// over states (sum G B, sum A G a h, sum C h) meet in LDS through LDS float
-// atomics; the per-position sums over channels (dB, dC) are reduced across the
+// over states (sum G B, sum A G a h, sum C h) leave each wave in its own LDS
+// slice and are added in a fixed order; the per-position sums over channels
+// (dB, dC) are reduced across the
 // 64 lanes with a permlane/DPP reduce-scatter and written as one partial per
 // (channel block, b, n, t), which a second small kernel adds up.  dA, dD and
 // dbias are written as per-batch-row partials reduced by the same kernel, so
 // the result is deterministic (no global atomics).
 #include "ss_io.cuh"
 #include "ss_params.h"
+#include "ss_prof.h"
 
 namespace ssm {
 
@@ -43,22 +45,26 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
   using E = Elem<T>;
   constexpr int kWaves = 4;
   constexpr int kThreads = 64 * kWaves;
+  constexpr int kTile = kTileBwd;
   constexpr int kVec = E::kVec;
-  constexpr int kLPR = kTileT / kVec;
+  constexpr int kLPR = kTile / kVec;
   constexpr int kRPP = kThreads / kLPR;
   constexpr int kPasses = kBlockCh / kRPP;
-  constexpr int kT4 = kTileT / 4;
+  constexpr int kT4 = kTile / 4;
   constexpr int kSub = kChunk;          // 16 steps per sub-chunk
-  constexpr int kStride = kTileT + 1;   // padded row of the [channel][step] LDS sums
+  constexpr int kStride = kTile + 1;    // padded row of the [channel][step] LDS sums
+  constexpr int kSlice = kBlockCh * kStride;
 
   __shared__ float4 sDelta[kT4][kBlockCh];  // delta (0 at padded steps)
   __shared__ float4 sDu[kT4][kBlockCh];     // delta * u
   __shared__ float4 sDout[kT4][kBlockCh];   // masked dout (after the z gate)
   __shared__ float4 sU[kT4][kBlockCh];
   __shared__ float4 sX[kT4][kBlockCh];      // delta_raw + bias
-  __shared__ float sGB[kBlockCh * kStride];   // sum_n G B
-  __shared__ float sDD[kBlockCh * kStride];   // sum_n A G a h_{t-1}
-  __shared__ float sY[kHasZ ? kBlockCh * kStride : 1];  // sum_n C h
+  // one slice per wave of the per-position sums over that wave's states; the
+  // slices are added in a fixed order in phase C (deterministic result)
+  __shared__ float sGB[kWaves * kSlice];   // sum_n G B
+  __shared__ float sDD[kWaves * kSlice];   // sum_n A G a h_{t-1}
+  __shared__ float sY[kHasZ ? kWaves * kSlice : 1];  // sum_n C h
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -103,15 +109,13 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
   }
   const bool softplus = p.softplus != 0;
 
-  for (int i = tid; i < kBlockCh * kStride; i += kThreads) {
-    sGB[i] = 0.0f;
-    sDD[i] = 0.0f;
-    if constexpr (kHasZ) sY[i] = 0.0f;
-  }
+  float* const wGB = sGB + w * kSlice;
+  float* const wDD = sDD + w * kSlice;
+  float* const wY = sY + (kHasZ ? w * kSlice : 0);
 
-  const int ntiles = (L + kTileT - 1) / kTileT;
+  const int ntiles = (L + kTile - 1) / kTile;
   for (int tile = ntiles - 1; tile >= 0; --tile) {
-    const int t0 = tile * kTileT;
+    const int t0 = tile * kTile;
     // ---- phase A: stage per-position quantities
     float dzf[kHasZ ? kPasses : 1][kVec];  // dy_masked * silu'(z), times out later
 #pragma unroll
@@ -157,14 +161,25 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
     __syncthreads();
 
     // ---- phase B: sub-chunks from the end of the tile
-    const int nsub = min(kTileT / kSub, (L - t0 + kSub - 1) / kSub);
+    const int nsub = min(kTile / kSub, (L - t0 + kSub - 1) / kSub);
     for (int k = nsub - 1; k >= 0; --k) {
       const int ts = t0 + k * kSub;  // first step of the sub-chunk
       const int c = ts / kChunk;     // its chunk index
 #pragma unroll
       for (int g = 0; g < kSG; ++g) {
         const int G = g * kWaves + w;
-        if (G >= ngroups) continue;  // wave-uniform
+        if (G >= ngroups) {  // wave-uniform; a wave with no states leaves zeros
+          if (g == 0) {
+#pragma unroll
+            for (int i = 0; i < kSub; ++i) {
+              const int li = lane * kStride + (ts - t0) + i;
+              wGB[li] = 0.0f;
+              wDD[li] = 0.0f;
+              if constexpr (kHasZ) wY[li] = 0.0f;
+            }
+          }
+          continue;
+        }
         float Av[4], A2v[4], Hc[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -200,7 +215,10 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
               H[s][i] = fmaf(a[s][i], hp, duv[j] * v.B(j, s));
               if constexpr (kHasZ) yv = fmaf(v.C(j, s), H[s][i], yv);
             }
-            if constexpr (kHasZ) atomicAdd(&sY[lane * kStride + (ts - t0) + i], yv);
+            if constexpr (kHasZ) {
+              float* dst = wY + lane * kStride + (ts - t0) + i;
+              *dst = (g == 0) ? yv : *dst + yv;
+            }
           }
         }
         // reverse recurrence
@@ -231,8 +249,8 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
               gam[g][s] = a[s][i] * Gt;
             }
             const int li = lane * kStride + (ts - t0) + i;
-            atomicAdd(&sGB[li], gB);
-            atomicAdd(&sDD[li], gD);
+            wGB[li] = (g == 0) ? gB : wGB[li] + gB;
+            wDD[li] = (g == 0) ? gD : wDD[li] + gD;
           }
         }
         // sum over the 64 channels of this block: lane holds indices 2*lane, 2*lane+1
@@ -272,10 +290,8 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
         for (int j = 0; j < 4; ++j) {
           const int tl = a_col + 4 * q + j;
           const int li = row * kStride + tl;
-          const float gb = sGB[li];
-          const float gd = sDD[li];
-          sGB[li] = 0.0f;
-          sDD[li] = 0.0f;
+          const float gb = (sGB[li] + sGB[kSlice + li]) + (sGB[2 * kSlice + li] + sGB[3 * kSlice + li]);
+          const float gd = (sDD[li] + sDD[kSlice + li]) + (sDD[2 * kSlice + li] + sDD[3 * kSlice + li]);
           const int tt = t + 4 * q + j;
           const bool valid = tt >= vlo && tt < vhi;
           const float ddl = fmaf(uu[j], gb, gd);
@@ -286,8 +302,8 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
           accD[ps] = fmaf(dov[j], uu[j], accD[ps]);
           accB[ps] += dd;
           if constexpr (kHasZ) {
-            const float yo = fmaf(Dv[ps], uu[j], sY[li]);
-            sY[li] = 0.0f;
+            const float ys = (sY[li] + sY[kSlice + li]) + (sY[2 * kSlice + li] + sY[3 * kSlice + li]);
+            const float yo = fmaf(Dv[ps], uu[j], ys);
             dzo[4 * q + j] = dzf[ps][4 * q + j] * yo;
           }
         }
@@ -298,8 +314,8 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
         if constexpr (kHasZ) store_row<T, kAligned>(dzp + (rb + c) * L, t, L, dzo);
       }
     }
-    // the next tile's phase B writes the LDS sums only after the barrier that
-    // ends its phase A, so no barrier is needed here
+    // the next tile's phase B overwrites the slices only after the barrier
+    // that ends its phase A, so no barrier is needed here
   }
 
   // ---- per-row partials
@@ -377,6 +393,7 @@ size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen) {
 template <typename T, int kSG, bool kHasZ, bool kAligned>
 static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t st) {
   dim3 grid(p.nblk, p.batch);
+  ProfScope prof("scan_bwd", st);
   hipLaunchKernelGGL((scan_bwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(256), 0, st,
                      dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias,
                      p.h_init, p.length, (const T*)p.z, p.h_chunks_in, (const T*)p.dout,
@@ -403,6 +420,7 @@ static hipError_t launch_bwd2(const ScanParams& p, const float* bc, bool aligned
   if (e != hipSuccess) return e;
   const size_t total = 2 * (size_t)p.batch * p.nstate * p.seqlen + (size_t)p.dim * p.nstate + p.dim;
   const int blocks = (int)std::min<size_t>((total + 255) / 256, 16384);
+  ProfScope prof("scan_bwd_reduce", st);
   hipLaunchKernelGGL(scan_bwd_reduce_kernel<T>, dim3(blocks), dim3(256), 0, st, p.batch, p.dim,
                      p.nstate, p.seqlen, p.nblk, p.ws_bc, p.ws_A, p.ws_D, p.ws_bias, (T*)p.dB,
                      (T*)p.dC, p.dA, p.dD, p.dbias);

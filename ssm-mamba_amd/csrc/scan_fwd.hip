@@ -21,6 +21,7 @@
 // The state after every kChunk steps is saved for the backward (h_chunks).
 #include "ss_io.cuh"
 #include "ss_params.h"
+#include "ss_prof.h"
 
 namespace ssm {
 
@@ -247,6 +248,7 @@ hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t
   const int Lp = bc_row_len(p.seqlen);
   const size_t total = (size_t)p.batch * ngroups * Lp;
   const int blocks = (int)std::min<size_t>((total + 255) / 256, 65535);
+  ProfScope prof("bc_prep", st);
   if (dtype == 1)
     hipLaunchKernelGGL(bc_prep_kernel<__hip_bfloat16>, dim3(blocks), dim3(256), 0, st, p.batch,
                        p.nstate, p.seqlen, ngroups, Lp, (const __hip_bfloat16*)p.B,
@@ -260,6 +262,7 @@ hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t
 template <typename T, int kSG, bool kHasZ, bool kAligned>
 static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t st) {
   dim3 grid(p.nblk, p.batch);
+  ProfScope prof("scan_fwd", st);
   hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(256), 0, st,
                      dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias,
                      p.h_init, p.length, (const T*)p.z, (T*)p.out, p.h_chunks, p.h_last);

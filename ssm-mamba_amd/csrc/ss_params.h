@@ -15,7 +15,8 @@
 namespace ssm {
 
 constexpr int kChunk = 16;    // steps between saved states
-constexpr int kTileT = 64;    // steps staged through LDS per tile
+constexpr int kTileT = 64;    // steps staged through LDS per forward tile
+constexpr int kTileBwd = 32;  // steps staged through LDS per backward tile
 constexpr int kBlockCh = 64;  // channels per workgroup (one per lane)
 
 // Scalar shape/flag block passed to the scan kernels (pointers travel as

@@ -11,6 +11,7 @@
 // before writing it.
 #include "ss_io.cuh"
 #include "ss_params.h"
+#include "ss_prof.h"
 
 namespace ssm {
 
@@ -76,6 +77,7 @@ template <typename T, int kQ>
 static hipError_t launch_upd2(const UpdateParams& p, bool vecN, hipStream_t st) {
   const size_t threads = (size_t)p.batch * p.dim * kQ;
   const unsigned blocks = (unsigned)((threads + 255) / 256);
+  ProfScope prof("state_update", st);
   if (vecN)
     hipLaunchKernelGGL((state_update_kernel<T, kQ, true>), dim3(blocks), dim3(256), 0, st, p.batch,
                        p.dim, p.nstate, p.softplus, p.state, p.new_state, (const T*)p.x,

@@ -16,10 +16,12 @@ def _ss():
 
 def run_case(cuda, batch, dim, seqlen, nstate, dtype, *, seed=0, with_z=True, h_init=False,
              length=None, padding_side="right", softplus=True, dlast=False, delta_shift=0.0,
-             bwd=True, with_D=True, with_bias=True):
+             bwd=True, with_D=True, with_bias=True, positive_delta=False):
     ss = _ss()
     c = make_case(batch, dim, seqlen, nstate, dtype, seed=seed, with_z=with_z, h_init=h_init,
                   delta_shift=delta_shift)
+    if positive_delta:  # without softplus the step size is delta itself and must stay > 0
+        c["delta"] = (c["delta"].float().abs() * 0.2).to(dtype)
     if not with_D:
         c["D"] = None
     if not with_bias:
@@ -88,7 +90,7 @@ def test_lengths(cuda, padding_side, dtype):
 
 def test_no_softplus_no_z_no_D(cuda):
     run_case(cuda, 2, 64, 96, 16, torch.float32, seed=8, with_z=False, softplus=False,
-             with_D=False, with_bias=False)
+             with_D=False, with_bias=False, positive_delta=True)
 
 
 def test_config0(cuda):
@@ -142,8 +144,12 @@ def test_config1_full_size_properties(cuda):
                                   dh["delta_bias"], hh, None, dy[:, lo:hi].contiguous(), None,
                                   z=dh["z"]))
     for idx, nm in ((2, "dB"), (3, "dC")):
-        tot = halves[0][idx].float() + halves[1][idx].float()
-        assert_close(r1[idx].float(), tot, torch.bfloat16, nm + " additivity")
+        # each of the three results is rounded to bf16 once (relative error
+        # <= 2^-9); the fp32 partial sums agree to ~1e-6
+        h0, h1, full = halves[0][idx].float(), halves[1][idx].float(), r1[idx].float()
+        bound = 2.0 ** -8 * (h0.abs() + h1.abs() + full.abs()) + 1e-5
+        err = (full - (h0 + h1)).abs()
+        assert bool((err <= bound).all()), f"{nm} additivity: max excess {(err - bound).max().item():.3g}"
     # per-channel gradients of the subset against the oracle
     rb = R.scan_bwd(cs["u"], cs["delta"], cs["A"], cs["B"], cs["C"], cs["D"], cs["delta_bias"],
                     None, None, True, cs["z"], True, dy=dy.cpu()[:, sub], dh_last=None)
