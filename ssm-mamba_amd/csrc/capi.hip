@@ -302,12 +302,11 @@ int ssm_selective_state_update(int64_t batch, int64_t dim, int64_t nstate, int d
   p.bias = dt_bias;
   p.z = z;
   p.out = out;
-  // 128-bit path: whole float4 groups and a power-of-two lane count per (b, d)
-  const int nq = (int)((nstate + 3) / 4);
-  const bool pow2 = (nq & (nq - 1)) == 0;
-  const bool vecN = nstate % 4 == 0 && pow2 && aligned16(state) && aligned16(new_state) &&
-                    aligned16(A) && (dtype == SSM_F32 ? aligned16(B) && aligned16(C)
-                                                      : (((uintptr_t)B | (uintptr_t)C) & 7) == 0);
+  // 128-bit path: N in {4, 8, 16, 32, 64} with 16-byte aligned state / A and
+  // 8-byte (bf16) or 16-byte (fp32) aligned B / C rows
+  const bool vecN = nstate % 4 == 0 && aligned16(state) && aligned16(new_state) && aligned16(A) &&
+                    (dtype == SSM_F32 ? aligned16(B) && aligned16(C)
+                                      : (((uintptr_t)B | (uintptr_t)C) & 7) == 0);
   return hip_status(ssm::launch_state_update(p, dtype, vecN, static_cast<hipStream_t>(stream)),
                     "selective_state_update launch");
 }

@@ -14,26 +14,87 @@
 // dz = dy * out * silu'(z) with out recomputed from the states.
 //
 // Work decomposition mirrors the forward (workgroup = batch row b x 64
-// channels, 4 waves, lane = channel, wave w = state group G = g*4 + w).  Tiles
-// of kTileBwd steps are walked from the end; inside a tile, 16-step sub-chunks are
-// walked from the end.  For each sub-chunk the wave reloads the state saved by
-// the forward at the sub-chunk start, recomputes the 16 states and decay
-// factors into registers, then runs the reverse recurrence.  Per-position sums
-// over states (sum G B, sum A G a h, sum C h) leave each wave in its own LDS
-// slice and are added in a fixed order; the per-position sums over channels
-// (dB, dC) are reduced across the
-// 64 lanes with a permlane/DPP reduce-scatter and written as one partial per
-// (channel block, b, n, t), which a second small kernel adds up.  dA, dD and
-// dbias are written as per-batch-row partials reduced by the same kernel, so
-// the result is deterministic (no global atomics).
+// channels, 8 waves, lane = channel, wave w = state pairs G = g*8 + w).  Tiles
+// of 16 steps (one saved-state chunk) are walked from the end.  For each tile
+// a wave reloads the state the forward saved at the tile start, recomputes the
+// 16 states and decay factors of its two states into registers, then runs the
+// reverse recurrence.  The tile's B/C block (prepped fp32 layout) is staged in
+// LDS together with the per-step values and read with broadcast LDS loads, so
+// the loop has no scalar-memory traffic and no scalar-register pressure.  Per-position
+// sums over states (sum G B, sum A G a h, sum C h) leave each wave in its own
+// LDS slice and are added in a fixed order; the per-position sums over
+// channels (dB, dC) are reduced across the 64 lanes with a permlane/DPP
+// reduce-scatter and written as one partial per (channel block, b, n, t),
+// which a second small kernel adds up.  dA, dD and dbias are written as
+// per-batch-row partials reduced by the same kernel, so the result is
+// deterministic (no atomics).
 #include "ss_io.cuh"
 #include "ss_params.h"
 #include "ss_prof.h"
 
 namespace ssm {
 
+namespace {
+
+struct StepVals {  // per-position LDS values of one 4-step block
+  float4 dl, du, dout;
+};
+
+// Recompute one 4-step block: decays a and states H for the wave's 2 states.
+__device__ __forceinline__ void bwd_recompute_block(int jq, const StepVals& sv, const BC2& v,
+                                                    const float (&A2)[2], const float (&Hc)[2],
+                                                    float (&a)[2][kChunk], float (&H)[2][kChunk],
+                                                    float (&y)[4]) {
+  const float dlv[4] = {sv.dl.x, sv.dl.y, sv.dl.z, sv.dl.w};
+  const float duv[4] = {sv.du.x, sv.du.y, sv.du.z, sv.du.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * jq + j;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      a[s][i] = fast_exp2(dlv[j] * A2[s]);
+      const float hp = i ? H[s][i - 1] : Hc[s];
+      H[s][i] = fmaf(a[s][i], hp, duv[j] * v.B(j, s));
+      y[j] = fmaf(v.C(j, s), H[s][i], y[j]);
+    }
+  }
+}
+
+// Reverse recurrence over one 4-step block (steps 4jq+3 .. 4jq).
+__device__ __forceinline__ void bwd_reverse_block(int jq, const StepVals& sv, const BC2& v,
+                                                  const float (&Av)[2], const float (&Hc)[2],
+                                                  const float (&a)[2][kChunk],
+                                                  const float (&H)[2][kChunk], float (&gam)[2],
+                                                  float (&dA)[2], float (&vals)[4 * kChunk],
+                                                  float (&gB)[4], float (&gD)[4]) {
+  const float dlv[4] = {sv.dl.x, sv.dl.y, sv.dl.z, sv.dl.w};
+  const float duv[4] = {sv.du.x, sv.du.y, sv.du.z, sv.du.w};
+  const float dov[4] = {sv.dout.x, sv.dout.y, sv.dout.z, sv.dout.w};
+#pragma unroll
+  for (int j = 3; j >= 0; --j) {
+    const int i = 4 * jq + j;
+    float sB = 0.0f, sD = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const float Gt = fmaf(dov[j], v.C(j, s), gam[s]);
+      sB = fmaf(Gt, v.B(j, s), sB);
+      const float hp = i ? H[s][i - 1] : Hc[s];
+      const float gah = Gt * a[s][i] * hp;
+      sD = fmaf(Av[s], gah, sD);
+      dA[s] = fmaf(dlv[j], gah, dA[s]);
+      vals[s * kChunk + i] = Gt * duv[j];               // dB partial
+      vals[2 * kChunk + s * kChunk + i] = dov[j] * H[s][i];  // dC partial
+      gam[s] = a[s][i] * Gt;
+    }
+    gB[j] = sB;
+    gD[j] = sD;
+  }
+}
+
+}  // namespace
+
 template <typename T, int kSG, bool kHasZ, bool kAligned>
-__global__ __launch_bounds__(256) void scan_bwd_kernel(
+__global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
     const float* __restrict__ Ap, const float* __restrict__ bc,
     const float* __restrict__ Dp, const float* __restrict__ biasp,
@@ -42,29 +103,27 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
     const float* __restrict__ dh_last, T* __restrict__ dup, T* __restrict__ ddp,
     T* __restrict__ dzp, float* __restrict__ dh_init, float* __restrict__ ws_bc,
     float* __restrict__ ws_A, float* __restrict__ ws_D, float* __restrict__ ws_bias) {
-  using E = Elem<T>;
-  constexpr int kWaves = 4;
-  constexpr int kThreads = 64 * kWaves;
-  constexpr int kTile = kTileBwd;
-  constexpr int kVec = E::kVec;
-  constexpr int kLPR = kTile / kVec;
-  constexpr int kRPP = kThreads / kLPR;
-  constexpr int kPasses = kBlockCh / kRPP;
-  constexpr int kT4 = kTile / 4;
-  constexpr int kSub = kChunk;          // 16 steps per sub-chunk
-  constexpr int kStride = kTile + 1;    // padded row of the [channel][step] LDS sums
-  constexpr int kSlice = kBlockCh * kStride;
+  using R4 = typename Raw4<T>::type;
+  constexpr int kT4 = kTileB / 4;       // 4-step blocks per tile (4)
+  constexpr int kItems = kBlockCh * kT4;  // tile-phase work items (256)
+  constexpr int kStr = kTileB + 4;      // row stride of a slice (floats; 16-byte aligned rows)
+  constexpr int kSlice = kBlockCh * kStr;
+  static_assert(kTileB == kChunk, "one saved state per backward tile");
+  constexpr int kMaxPairs = kSG * kWaves;  // state pairs covered by the dispatch bucket
+  static_assert(kMaxPairs * kTileB <= kThreads, "one B/C float4 per thread per tile");
 
   __shared__ float4 sDelta[kT4][kBlockCh];  // delta (0 at padded steps)
   __shared__ float4 sDu[kT4][kBlockCh];     // delta * u
   __shared__ float4 sDout[kT4][kBlockCh];   // masked dout (after the z gate)
   __shared__ float4 sU[kT4][kBlockCh];
   __shared__ float4 sX[kT4][kBlockCh];      // delta_raw + bias
-  // one slice per wave of the per-position sums over that wave's states; the
-  // slices are added in a fixed order in phase C (deterministic result)
+  // one slice per wave of the per-position sums over that wave's states,
+  // added in a fixed order in phase C (deterministic result)
   __shared__ float sGB[kWaves * kSlice];   // sum_n G B
   __shared__ float sDD[kWaves * kSlice];   // sum_n A G a h_{t-1}
-  __shared__ float sY[kHasZ ? kWaves * kSlice : 1];  // sum_n C h
+  __shared__ float sY[kHasZ ? kWaves * kSlice : 4];  // sum_n C h
+  // the tile's prepped B/C rows of every state pair: [G][step][s][B, C]
+  __shared__ float4 sBC[kMaxPairs][kTileB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -73,7 +132,7 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
   const int blk = blockIdx.x;
   const int d0 = blk * kBlockCh;
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
-  const int ngroups = (N + 3) / 4;
+  const int ngroups = (N + 1) / 2;
   const int Lp = bc_row_len(L);
   const size_t rb = (size_t)b * Dm;
   const size_t nBC = (size_t)p.batch * N * L;
@@ -85,233 +144,245 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
   const bool ch_ok = ch < Dm;
 
   // persistent per-state values: reverse carry gamma and dA accumulator
-  float gam[kSG][4], dA[kSG][4];
+  float gam[kSG][2], dA[kSG][2], Av[kSG][2], A2[kSG][2];
 #pragma unroll
   for (int g = 0; g < kSG; ++g)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int n = (g * kWaves + w) * 4 + s;
+    for (int s = 0; s < 2; ++s) {
+      const int n = (g * kWaves + w) * 2 + s;
       const bool ok = ch_ok && n < N;
       gam[g][s] = (ok && dh_last) ? dh_last[(rb + ch) * N + n] : 0.0f;
       dA[g][s] = 0.0f;
+      Av[g][s] = ok ? Ap[(size_t)ch * N + n] : 0.0f;
+      A2[g][s] = Av[g][s] * kLog2e;
     }
 
-  const int a_row = tid / kLPR;
-  const int a_col = (tid % kLPR) * kVec;
-  float Dv[kPasses], Bias[kPasses], accD[kPasses], accB[kPasses];
-#pragma unroll
-  for (int ps = 0; ps < kPasses; ++ps) {
-    const int c = d0 + a_row + ps * kRPP;
-    Dv[ps] = (c < Dm && Dp) ? Dp[c] : 0.0f;
-    Bias[ps] = (c < Dm && biasp) ? biasp[c] : 0.0f;
-    accD[ps] = 0.0f;
-    accB[ps] = 0.0f;
-  }
+  // ---- tile-phase mapping: threads < kItems, item = (channel row, 4 steps)
+  const bool a_act = tid < kItems;
+  const int a_row = (tid % kItems) / kT4;
+  const int a_q = tid % kT4;
+  const int a_col = a_q * 4;
+  const int a_ch = d0 + a_row;
+  const bool a_ok = a_act && a_ch < Dm;
+  const float Dv = (a_ok && Dp) ? Dp[a_ch] : 0.0f;
+  const float Bias = (a_ok && biasp) ? biasp[a_ch] : 0.0f;
+  const T* __restrict__ u_row = u + (rb + a_ch) * L;
+  const T* __restrict__ d_row = dl + (rb + a_ch) * L;
+  const T* __restrict__ y_row = dyp + (rb + a_ch) * L;
+  const T* __restrict__ z_row = zp + (rb + a_ch) * L;
   const bool softplus = p.softplus != 0;
+  float accD = 0.0f, accB = 0.0f;
+
+  const int ntiles = (L + kTileB - 1) / kTileB;
+  // raw rows of the next tile to process (walking backwards), in flight
+  R4 nu, nd, ny, nz{};
+  auto issue_tile_loads = [&](int tile) {
+    const int t = tile * kTileB + a_col;
+    nu = load_raw4<T, kAligned>(u_row, t, L, a_ok);
+    nd = load_raw4<T, kAligned>(d_row, t, L, a_ok);
+    ny = load_raw4<T, kAligned>(y_row, t, L, a_ok);
+    if constexpr (kHasZ) nz = load_raw4<T, kAligned>(z_row, t, L, a_ok);
+  };
+  // state saved by the forward just before a tile (per group and state)
+  auto load_hc = [&](int tile, float (&hc)[kSG][2]) {
+#pragma unroll
+    for (int g = 0; g < kSG; ++g)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int n = (g * kWaves + w) * 2 + s;
+        float v = 0.0f;
+        if (ch_ok && n < N) {
+          if (tile > 0) v = h_chunks[((rb + ch) * p.nchunks + (tile - 1)) * N + n];
+          else if (h_init) v = h_init[(rb + ch) * N + n];
+        }
+        hc[g][s] = v;
+      }
+  };
+  // thread -> one float4 of the tile's B/C block (pair G, step i)
+  const int bc_G = tid / kTileB;
+  const int bc_i = tid % kTileB;
+  const bool bc_act = bc_G < ngroups;
+  float4 nbc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  auto load_bc_tile = [&](int tile) {
+    if (bc_act)
+      nbc = reinterpret_cast<const float4*>(bc)[((size_t)b * ngroups + bc_G) * Lp + tile * kTileB + bc_i];
+  };
+  issue_tile_loads(ntiles - 1);
+  load_bc_tile(ntiles - 1);
+  float hcn[kSG][2];
+  load_hc(ntiles - 1, hcn);
 
   float* const wGB = sGB + w * kSlice;
   float* const wDD = sDD + w * kSlice;
   float* const wY = sY + (kHasZ ? w * kSlice : 0);
 
-  const int ntiles = (L + kTile - 1) / kTile;
   for (int tile = ntiles - 1; tile >= 0; --tile) {
-    const int t0 = tile * kTile;
+    const int t0 = tile * kTileB;
+    float hc[kSG][2];
+#pragma unroll
+    for (int g = 0; g < kSG; ++g) hc[g][0] = hcn[g][0], hc[g][1] = hcn[g][1];
     // ---- phase A: stage per-position quantities
-    float dzf[kHasZ ? kPasses : 1][kVec];  // dy_masked * silu'(z), times out later
+    float dzf[4];  // dy_masked * silu'(z), times out in phase C
+    {
+      float uv[4], dv[4], yv[4], zv[4], de[4], du[4], dov[4], xv[4];
+      decode4(nu, uv);
+      decode4(nd, dv);
+      decode4(ny, yv);
+      if constexpr (kHasZ) decode4(nz, zv);
 #pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-      const int row = a_row + ps * kRPP;
-      const int c = d0 + row;
-      const int t = t0 + a_col;
-      const bool ok = c < Dm;
-      float uv[kVec], dv[kVec], yv[kVec];
-      load_row<T, kAligned>(u + (rb + c) * L, t, L, ok, uv);
-      load_row<T, kAligned>(dl + (rb + c) * L, t, L, ok, dv);
-      load_row<T, kAligned>(dyp + (rb + c) * L, t, L, ok, yv);
-      float zv[kVec];
-      if constexpr (kHasZ) load_row<T, kAligned>(zp + (rb + c) * L, t, L, ok, zv);
-      float de[kVec], du[kVec], dov[kVec], xv[kVec];
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        const float x = dv[j] + Bias[ps];
+      for (int j = 0; j < 4; ++j) {
+        const float x = dv[j] + Bias;
         const float dt = softplus ? softplus_t20(x) : x;
-        const int tt = t + j;
+        const int tt = t0 + a_col + j;
         const bool valid = tt >= vlo && tt < vhi;
         de[j] = valid ? dt : 0.0f;
         du[j] = de[j] * uv[j];
         const float dym = valid ? yv[j] : 0.0f;
         if constexpr (kHasZ) {
           dov[j] = dym * silu_f(zv[j]);
-          dzf[ps][j] = dym * silu_grad_f(zv[j]);
+          dzf[j] = dym * silu_grad_f(zv[j]);
         } else {
           dov[j] = dym;
+          dzf[j] = 0.0f;
         }
         xv[j] = x;
       }
-#pragma unroll
-      for (int q = 0; q < kVec / 4; ++q) {
-        const int t4 = a_col / 4 + q;
-        sDelta[t4][row] = make_float4(de[4 * q], de[4 * q + 1], de[4 * q + 2], de[4 * q + 3]);
-        sDu[t4][row] = make_float4(du[4 * q], du[4 * q + 1], du[4 * q + 2], du[4 * q + 3]);
-        sDout[t4][row] = make_float4(dov[4 * q], dov[4 * q + 1], dov[4 * q + 2], dov[4 * q + 3]);
-        sU[t4][row] = make_float4(uv[4 * q], uv[4 * q + 1], uv[4 * q + 2], uv[4 * q + 3]);
-        sX[t4][row] = make_float4(xv[4 * q], xv[4 * q + 1], xv[4 * q + 2], xv[4 * q + 3]);
+      if (bc_act) sBC[bc_G][bc_i] = nbc;
+      if (a_act) {
+        sDelta[a_q][a_row] = make_float4(de[0], de[1], de[2], de[3]);
+        sDu[a_q][a_row] = make_float4(du[0], du[1], du[2], du[3]);
+        sDout[a_q][a_row] = make_float4(dov[0], dov[1], dov[2], dov[3]);
+        sU[a_q][a_row] = make_float4(uv[0], uv[1], uv[2], uv[3]);
+        sX[a_q][a_row] = make_float4(xv[0], xv[1], xv[2], xv[3]);
       }
     }
     __syncthreads();
+    if (tile > 0) {  // the previous tile's rows, B/C and saved state stream in meanwhile
+      issue_tile_loads(tile - 1);
+      load_bc_tile(tile - 1);
+      load_hc(tile - 1, hcn);
+    }
 
-    // ---- phase B: sub-chunks from the end of the tile
-    const int nsub = min(kTile / kSub, (L - t0 + kSub - 1) / kSub);
-    for (int k = nsub - 1; k >= 0; --k) {
-      const int ts = t0 + k * kSub;  // first step of the sub-chunk
-      const int c = ts / kChunk;     // its chunk index
+    // ---- phase B
 #pragma unroll
-      for (int g = 0; g < kSG; ++g) {
-        const int G = g * kWaves + w;
-        if (G >= ngroups) {  // wave-uniform; a wave with no states leaves zeros
-          if (g == 0) {
+    for (int g = 0; g < kSG; ++g) {
+      const int G = g * kWaves + w;
+      if (G >= ngroups) {  // wave-uniform; a wave with no states leaves zeros
+        if (g == 0) {
+          const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-            for (int i = 0; i < kSub; ++i) {
-              const int li = lane * kStride + (ts - t0) + i;
-              wGB[li] = 0.0f;
-              wDD[li] = 0.0f;
-              if constexpr (kHasZ) wY[li] = 0.0f;
-            }
-          }
-          continue;
-        }
-        float Av[4], A2v[4], Hc[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int n = G * 4 + s;
-          const bool ok = ch_ok && n < N;
-          Av[s] = ok ? Ap[(size_t)ch * N + n] : 0.0f;
-          A2v[s] = Av[s] * kLog2e;
-          float hc = 0.0f;
-          if (ok) {
-            if (c > 0) hc = h_chunks[((rb + ch) * p.nchunks + (c - 1)) * N + n];
-            else if (h_init) hc = h_init[(rb + ch) * N + n];
-          }
-          Hc[s] = hc;
-        }
-        // recompute the 16 states and decays of the sub-chunk
-        float a[4][kSub], H[4][kSub];
-#pragma unroll
-        for (int jq = 0; jq < kSub / 4; ++jq) {
-          const int t4 = k * (kSub / 4) + jq;
-          float dlv[4], duv[4];
-          f4_to(sDelta[t4][lane], dlv);
-          f4_to(sDu[t4][lane], duv);
-          BC4 v;
-          load_bc_block(bc, bc_offset(b, G, ngroups, Lp, ts + 4 * jq), v);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int i = 4 * jq + j;
-            float yv = 0.0f;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              a[s][i] = fast_exp2(dlv[j] * A2v[s]);
-              const float hp = i ? H[s][i - 1] : Hc[s];
-              H[s][i] = fmaf(a[s][i], hp, duv[j] * v.B(j, s));
-              if constexpr (kHasZ) yv = fmaf(v.C(j, s), H[s][i], yv);
-            }
-            if constexpr (kHasZ) {
-              float* dst = wY + lane * kStride + (ts - t0) + i;
-              *dst = (g == 0) ? yv : *dst + yv;
-            }
+          for (int q = 0; q < kT4; ++q) {
+            *reinterpret_cast<float4*>(wGB + lane * kStr + 4 * q) = zero;
+            *reinterpret_cast<float4*>(wDD + lane * kStr + 4 * q) = zero;
+            if constexpr (kHasZ) *reinterpret_cast<float4*>(wY + lane * kStr + 4 * q) = zero;
           }
         }
-        // reverse recurrence
-        float vals[2 * 4 * kSub];  // [kind: 0 dB, 1 dC][s][i]
-#pragma unroll
-        for (int jq = kSub / 4 - 1; jq >= 0; --jq) {
-          const int t4 = k * (kSub / 4) + jq;
-          float dlv[4], duv[4], dov[4];
-          f4_to(sDelta[t4][lane], dlv);
-          f4_to(sDu[t4][lane], duv);
-          f4_to(sDout[t4][lane], dov);
-          BC4 v;
-          load_bc_block(bc, bc_offset(b, G, ngroups, Lp, ts + 4 * jq), v);
-#pragma unroll
-          for (int j = 3; j >= 0; --j) {
-            const int i = 4 * jq + j;
-            float gB = 0.0f, gD = 0.0f;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              const float Gt = fmaf(dov[j], v.C(j, s), gam[g][s]);
-              gB = fmaf(Gt, v.B(j, s), gB);
-              const float hp = i ? H[s][i - 1] : Hc[s];
-              const float gah = Gt * a[s][i] * hp;
-              gD = fmaf(Av[s], gah, gD);
-              dA[g][s] = fmaf(dlv[j], gah, dA[g][s]);
-              vals[s * kSub + i] = Gt * duv[j];
-              vals[4 * kSub + s * kSub + i] = dov[j] * H[s][i];
-              gam[g][s] = a[s][i] * Gt;
-            }
-            const int li = lane * kStride + (ts - t0) + i;
-            wGB[li] = (g == 0) ? gB : wGB[li] + gB;
-            wDD[li] = (g == 0) ? gD : wDD[li] + gD;
-          }
+        continue;
+      }
+      float a[2][kChunk], H[2][kChunk];
+      float vals[4 * kChunk];
+      StepVals X, Y;
+      BC2 bX, bY;
+      // slice update: the first group writes, later groups add
+      auto put4 = [&](float* slice, int q, const float (&v)[4]) {
+        float4* dst = reinterpret_cast<float4*>(slice + lane * kStr + 4 * q);
+        if (g == 0) {
+          *dst = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+          float4 o = *dst;
+          *dst = make_float4(o.x + v[0], o.y + v[1], o.z + v[2], o.w + v[3]);
         }
-        // sum over the 64 channels of this block: lane holds indices 2*lane, 2*lane+1
-        wave_reduce_scatter<2 * 4 * kSub>(vals, lane);
-        {
-          const int kind = lane >> 5;
-          const int s = (lane >> 3) & 3;
-          const int i0 = (lane & 7) * 2;
-          const int n = G * 4 + s;
-          const int t = ts + i0;
-          if (n < N) {
-            float* dst = ws_bc + ((size_t)kind * p.nblk + blk) * nBC + ((size_t)b * N + n) * L;
-            if (t < L) dst[t] = vals[0];
-            if (t + 1 < L) dst[t + 1] = vals[1];
-          }
+      };
+      auto fwd = [&](int jq, const StepVals& sv, const BC2& v) {
+        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        bwd_recompute_block(jq, sv, v, A2[g], hc[g], a, H, y);
+        if constexpr (kHasZ) put4(wY, jq, y);
+      };
+      auto rev = [&](int jq, const StepVals& sv, const BC2& v) {
+        float gB[4], gD[4];
+        bwd_reverse_block(jq, sv, v, Av[g], hc[g], a, H, gam[g], dA[g], vals, gB, gD);
+        put4(wGB, jq, gB);
+        put4(wDD, jq, gD);
+      };
+      auto ld = [&](int jq, StepVals& sv, BC2& v, bool with_dout) {
+        sv.dl = sDelta[jq][lane];
+        sv.du = sDu[jq][lane];
+        if (with_dout) sv.dout = sDout[jq][lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {  // broadcast reads (same address in every lane)
+          const float4 q = sBC[G][4 * jq + j];
+          v.v[4 * j] = q.x; v.v[4 * j + 1] = q.y; v.v[4 * j + 2] = q.z; v.v[4 * j + 3] = q.w;
         }
+      };
+      // fixed schedule F0 F1 F2 F3 R3 R2 R1 R0 (recompute, then reverse); LDS
+      // reads return in order, so the compiler overlaps them with the math
+      ld(0, X, bX, false); fwd(0, X, bX);
+      ld(1, Y, bY, false); fwd(1, Y, bY);
+      ld(2, X, bX, false); fwd(2, X, bX);
+      ld(3, Y, bY, true);  fwd(3, Y, bY);
+      rev(3, Y, bY);
+      ld(2, X, bX, true); rev(2, X, bX);
+      ld(1, Y, bY, true); rev(1, Y, bY);
+      ld(0, X, bX, true); rev(0, X, bX);
+      // sum over the 64 channels of this block: lane l holds value index l
+      wave_reduce_scatter<4 * kChunk>(vals, lane);
+      {
+        const int kind = lane >> 5;
+        const int s = (lane >> 4) & 1;
+        const int i = lane & 15;
+        const int n = G * 2 + s;
+        const int t = t0 + i;
+        if (n < N && t < L)
+          ws_bc[((size_t)kind * p.nblk + blk) * nBC + ((size_t)b * N + n) * L + t] = vals[0];
       }
     }
     __syncthreads();
 
     // ---- phase C: per-position gradients
+    if (a_act) {
+      const int li = a_row * kStr + a_col;
+      float4 gb = *reinterpret_cast<const float4*>(sGB + li);
+      float4 gd = *reinterpret_cast<const float4*>(sDD + li);
+      float4 ys = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if constexpr (kHasZ) ys = *reinterpret_cast<const float4*>(sY + li);
 #pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-      const int row = a_row + ps * kRPP;
-      const int c = d0 + row;
-      const int t = t0 + a_col;
-      float duo[kVec], ddo[kVec], dzo[kVec];
-#pragma unroll
-      for (int q = 0; q < kVec / 4; ++q) {
-        const int t4 = a_col / 4 + q;
-        float de[4], uu[4], dov[4], xv[4];
-        f4_to(sDelta[t4][row], de);
-        f4_to(sU[t4][row], uu);
-        f4_to(sDout[t4][row], dov);
-        f4_to(sX[t4][row], xv);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int tl = a_col + 4 * q + j;
-          const int li = row * kStride + tl;
-          const float gb = (sGB[li] + sGB[kSlice + li]) + (sGB[2 * kSlice + li] + sGB[3 * kSlice + li]);
-          const float gd = (sDD[li] + sDD[kSlice + li]) + (sDD[2 * kSlice + li] + sDD[3 * kSlice + li]);
-          const int tt = t + 4 * q + j;
-          const bool valid = tt >= vlo && tt < vhi;
-          const float ddl = fmaf(uu[j], gb, gd);
-          const float dsp = softplus ? softplus_grad_t20(xv[j]) : 1.0f;
-          const float dd = valid ? ddl * dsp : 0.0f;
-          duo[4 * q + j] = fmaf(Dv[ps], dov[j], de[j] * gb);
-          ddo[4 * q + j] = dd;
-          accD[ps] = fmaf(dov[j], uu[j], accD[ps]);
-          accB[ps] += dd;
-          if constexpr (kHasZ) {
-            const float ys = (sY[li] + sY[kSlice + li]) + (sY[2 * kSlice + li] + sY[3 * kSlice + li]);
-            const float yo = fmaf(Dv[ps], uu[j], ys);
-            dzo[4 * q + j] = dzf[ps][4 * q + j] * yo;
-          }
+      for (int ww = 1; ww < kWaves; ++ww) {
+        const float4 v1 = *reinterpret_cast<const float4*>(sGB + ww * kSlice + li);
+        const float4 v2 = *reinterpret_cast<const float4*>(sDD + ww * kSlice + li);
+        gb.x += v1.x; gb.y += v1.y; gb.z += v1.z; gb.w += v1.w;
+        gd.x += v2.x; gd.y += v2.y; gd.z += v2.z; gd.w += v2.w;
+        if constexpr (kHasZ) {
+          const float4 v3 = *reinterpret_cast<const float4*>(sY + ww * kSlice + li);
+          ys.x += v3.x; ys.y += v3.y; ys.z += v3.z; ys.w += v3.w;
         }
       }
-      if (c < Dm && t < L) {
-        store_row<T, kAligned>(dup + (rb + c) * L, t, L, duo);
-        store_row<T, kAligned>(ddp + (rb + c) * L, t, L, ddo);
-        if constexpr (kHasZ) store_row<T, kAligned>(dzp + (rb + c) * L, t, L, dzo);
+      const float gbv[4] = {gb.x, gb.y, gb.z, gb.w};
+      const float gdv[4] = {gd.x, gd.y, gd.z, gd.w};
+      const float ysv[4] = {ys.x, ys.y, ys.z, ys.w};
+      float de[4], uu[4], dov[4], xv[4];
+      f4_to(sDelta[a_q][a_row], de);
+      f4_to(sU[a_q][a_row], uu);
+      f4_to(sDout[a_q][a_row], dov);
+      f4_to(sX[a_q][a_row], xv);
+      float duo[4], ddo[4], dzo[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tt = t0 + a_col + j;
+        const bool valid = tt >= vlo && tt < vhi;
+        const float ddl = fmaf(uu[j], gbv[j], gdv[j]);
+        const float dsp = softplus ? softplus_grad_t20(xv[j]) : 1.0f;
+        const float dd = valid ? ddl * dsp : 0.0f;
+        duo[j] = fmaf(Dv, dov[j], de[j] * gbv[j]);
+        ddo[j] = dd;
+        accD = fmaf(dov[j], uu[j], accD);
+        accB += dd;
+        if constexpr (kHasZ) dzo[j] = dzf[j] * fmaf(Dv, uu[j], ysv[j]);
+      }
+      const int t = t0 + a_col;
+      if (a_ok && t < L) {
+        store4<T, kAligned>(dup + (rb + a_ch) * L, t, L, duo);
+        store4<T, kAligned>(ddp + (rb + a_ch) * L, t, L, ddo);
+        if constexpr (kHasZ) store4<T, kAligned>(dzp + (rb + a_ch) * L, t, L, dzo);
       }
     }
     // the next tile's phase B overwrites the slices only after the barrier
@@ -322,22 +393,19 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(
 #pragma unroll
   for (int g = 0; g < kSG; ++g)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int n = (g * kWaves + w) * 4 + s;
+    for (int s = 0; s < 2; ++s) {
+      const int n = (g * kWaves + w) * 2 + s;
       if (ch_ok && n < N) {
         ws_A[(rb + ch) * N + n] = dA[g][s];
         if (dh_init) dh_init[(rb + ch) * N + n] = gam[g][s];
       }
     }
-#pragma unroll
-  for (int ps = 0; ps < kPasses; ++ps) {
-    const float sd = group_sum<kLPR>(accD[ps]);
-    const float sb = group_sum<kLPR>(accB[ps]);
-    const int c = d0 + a_row + ps * kRPP;
-    if ((tid % kLPR) == 0 && c < Dm) {
-      ws_D[rb + c] = sd;
-      ws_bias[rb + c] = sb;
-    }
+  // the 4 items of a channel row are 4 consecutive lanes
+  const float sd = group_sum<kT4>(accD);
+  const float sb = group_sum<kT4>(accB);
+  if (a_ok && a_q == 0) {
+    ws_D[rb + a_ch] = sd;
+    ws_bias[rb + a_ch] = sb;
   }
 }
 
@@ -383,18 +451,11 @@ __global__ __launch_bounds__(256) void scan_bwd_reduce_kernel(
 size_t bc_prep_floats(int batch, int nstate, int seqlen);
 hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t st);
 
-size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen) {
-  const size_t nblk = (dim + kBlockCh - 1) / kBlockCh;
-  return 2 * nblk * (size_t)batch * nstate * seqlen   // dB/dC partials
-         + (size_t)batch * dim * nstate              // dA partials
-         + 2 * (size_t)batch * dim;                  // dD, dbias partials
-}
-
 template <typename T, int kSG, bool kHasZ, bool kAligned>
 static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t st) {
   dim3 grid(p.nblk, p.batch);
   ProfScope prof("scan_bwd", st);
-  hipLaunchKernelGGL((scan_bwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(256), 0, st,
+  hipLaunchKernelGGL((scan_bwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(kThreads), 0, st,
                      dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias,
                      p.h_init, p.length, (const T*)p.z, p.h_chunks_in, (const T*)p.dout,
                      p.dh_last, (T*)p.du, (T*)p.ddelta, (T*)p.dz, p.dh_init, p.ws_bc, p.ws_A,
@@ -427,8 +488,8 @@ static hipError_t launch_bwd2(const ScanParams& p, const float* bc, bool aligned
   return hipGetLastError();
 }
 
-// bc must hold bc_prep_floats() floats; ws_* must be laid out by the caller
-// (see bwd_ws_floats).  nstate <= 64.
+// bc must hold bc_prep_floats() floats; ws_* are laid out by the caller.
+// nstate <= 64.
 hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* bc,
                            hipStream_t st) {
   hipError_t e = launch_bc_prep(p, dtype, bc, st);

@@ -6,18 +6,22 @@
 //   h_t     = exp(delta_t * A_dn) * h_{t-1} + delta_t * u_t * B_nt
 //   out_t   = D_d * u_t + sum_n C_nt * h_t     (* silu(z_t) when z is given)
 //
-// Work decomposition (one workgroup = one batch row b x 64 channels, 4 waves):
-//   phase A  all 256 threads stream a 64-channel x 64-step tile of u / delta
-//            (/ z) with 128-bit coalesced loads, evaluate softplus once per
-//            element and stage delta and delta*u in LDS as float4 columns;
-//   phase B  lane = channel, wave w = state group G = g*4 + w (4 states each):
-//            a sequential recurrence over the 64 steps held in registers.  B
-//            and C are wave-uniform (same b, n, t across the wave) and come
-//            from the prepped fp32 block layout through scalar loads, so they
-//            cost no VALU or LDS bandwidth.  Each wave leaves its partial sum
-//            over its states of C*h in LDS;
-//   phase C  the same threads as phase A add the four partials, D*u and the
-//            z gate, and store the tile with 128-bit stores.
+// Work decomposition (one workgroup = one batch row b x 64 channels, 8 waves,
+// two waves per SIMD):
+//   phase A  the 512 threads stream a 64-channel x 32-step tile of u / delta
+//            (/ z) (4 consecutive steps per thread, coalesced rows), evaluate
+//            softplus once per element and stage delta and delta*u in LDS as
+//            float4 columns.  The next tile's rows are already in flight: they
+//            are loaded during the previous tile's phase B;
+//   phase B  lane = channel, wave w = state pairs G = g*8 + w: a sequential
+//            recurrence over the tile held in registers.  B and C are
+//            wave-uniform (same b, n, t across the wave) and come from the
+//            prepped fp32 block layout through scalar loads, double-buffered so
+//            each 4-step block's scalar and LDS loads are issued one block
+//            ahead.  Each wave leaves its partial sum over its states of C*h in
+//            its own LDS slice;
+//   phase C  the phase-A threads add the eight slices in a fixed order, D*u
+//            and the z gate, and store the tile.
 // The state after every kChunk steps is saved for the backward (h_chunks).
 #include "ss_io.cuh"
 #include "ss_params.h"
@@ -27,8 +31,8 @@ namespace ssm {
 
 // ---------------------------------------------------------------- B/C prep
 
-// bc[b][G][t][s][0/1] = B/C[b][4G+s][t] as fp32 (zero for padded states/steps);
-// rows are bc_row_len(L) steps long.
+// bc[b][G][t][s][0/1] = B/C[b][2G+s][t] as fp32 (zero for padded states and
+// steps); rows are bc_row_len(L) steps long.
 template <typename T>
 __global__ __launch_bounds__(256) void bc_prep_kernel(const int batch, const int N, const int L,
                                                       const int ngroups, const int Lp,
@@ -42,42 +46,51 @@ __global__ __launch_bounds__(256) void bc_prep_kernel(const int batch, const int
     const size_t bg = i / Lp;
     const int G = (int)(bg % ngroups);
     const int b = (int)(bg / ngroups);
-    float v[8];
+    float v[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int n = G * 4 + s;
+    for (int s = 0; s < 2; ++s) {
+      const int n = G * 2 + s;
       const bool ok = n < N && t < L;
       const size_t src = ((size_t)b * N + n) * L + t;
       v[2 * s] = ok ? Elem<T>::load1(Bp + src) : 0.0f;
       v[2 * s + 1] = ok ? Elem<T>::load1(Cp + src) : 0.0f;
     }
-    float4* dst = reinterpret_cast<float4*>(bc + i * 8);
-    dst[0] = make_float4(v[0], v[1], v[2], v[3]);
-    dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+    reinterpret_cast<float4*>(bc)[i] = make_float4(v[0], v[1], v[2], v[3]);
   }
 }
 
 // ---------------------------------------------------------------- forward
 
+// One 4-step block of the recurrence for the wave's 2 states.
+__device__ __forceinline__ void fwd_block(const float4 dl4, const float4 du4, const BC2& v,
+                                          const float (&A2)[2], float (&h)[2], float (&y)[4]) {
+  const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+  const float duv[4] = {du4.x, du4.y, du4.z, du4.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const float a = fast_exp2(dlv[j] * A2[s]);
+      h[s] = fmaf(a, h[s], duv[j] * v.B(j, s));
+      y[j] = fmaf(v.C(j, s), h[s], y[j]);
+    }
+  }
+}
+
 // Every pointer is its own __restrict__ argument: with that no-alias
 // information the compiler can prove the output stores never clobber the
 // prepped B/C block, which is what lets its wave-uniform reads be scalar loads.
 template <typename T, int kSG, bool kHasZ, bool kAligned>
-__global__ __launch_bounds__(256) void scan_fwd_kernel(
+__global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
     const float* __restrict__ Ap, const float* __restrict__ bc,
     const float* __restrict__ Dp, const float* __restrict__ biasp,
     const float* __restrict__ h_init, const int64_t* __restrict__ length,
     const T* __restrict__ zp, T* __restrict__ out, float* __restrict__ h_chunks,
     float* __restrict__ h_last) {
-  using E = Elem<T>;
-  constexpr int kWaves = 4;
-  constexpr int kThreads = 64 * kWaves;
-  constexpr int kVec = E::kVec;
-  constexpr int kLPR = kTileT / kVec;    // threads per channel row of a tile
-  constexpr int kRPP = kThreads / kLPR;  // rows per pass
-  constexpr int kPasses = kBlockCh / kRPP;
-  constexpr int kT4 = kTileT / 4;
+  using R4 = typename Raw4<T>::type;
+  constexpr int kT4 = kTileF / 4;
+  static_assert(kBlockCh * kT4 == kThreads, "one 4-step row piece per thread");
 
   __shared__ float4 sDelta[kT4][kBlockCh];
   __shared__ float4 sDu[kT4][kBlockCh];
@@ -89,7 +102,7 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
   const int b = blockIdx.y;
   const int d0 = blockIdx.x * kBlockCh;
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
-  const int ngroups = (N + 3) / 4;
+  const int ngroups = (N + 1) / 2;
   const int Lp = bc_row_len(L);
   const size_t rb = (size_t)b * Dm;
 
@@ -99,128 +112,169 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
   // ---- scan lane state
   const int ch = d0 + lane;
   const bool ch_ok = ch < Dm;
-  float h[kSG][4], A2[kSG][4];
+  float h[kSG][2], A2[kSG][2];
 #pragma unroll
   for (int g = 0; g < kSG; ++g)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int n = (g * kWaves + w) * 4 + s;
+    for (int s = 0; s < 2; ++s) {
+      const int n = (g * kWaves + w) * 2 + s;
       const bool ok = ch_ok && n < N;
       A2[g][s] = ok ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
       h[g][s] = (ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
     }
 
-  // ---- tile-phase mapping
-  const int a_row = tid / kLPR;
-  const int a_col = (tid % kLPR) * kVec;
-  float Dv[kPasses], Bias[kPasses];
-#pragma unroll
-  for (int ps = 0; ps < kPasses; ++ps) {
-    const int c = d0 + a_row + ps * kRPP;
-    Dv[ps] = (c < Dm && Dp) ? Dp[c] : 0.0f;
-    Bias[ps] = (c < Dm && biasp) ? biasp[c] : 0.0f;
-  }
+  // ---- tile-phase mapping: thread = (channel row, 4 consecutive steps)
+  const int a_row = tid / kT4;
+  const int a_q = tid % kT4;
+  const int a_col = a_q * 4;
+  const int a_ch = d0 + a_row;
+  const bool a_ok = a_ch < Dm;
+  const float Dv = (a_ok && Dp) ? Dp[a_ch] : 0.0f;
+  const float Bias = (a_ok && biasp) ? biasp[a_ch] : 0.0f;
+  const T* __restrict__ u_row = u + (rb + a_ch) * L;
+  const T* __restrict__ d_row = dl + (rb + a_ch) * L;
+  const T* __restrict__ z_row = zp + (rb + a_ch) * L;
   const bool softplus = p.softplus != 0;
   const bool save = h_chunks != nullptr;
 
-  for (int t0 = 0; t0 < L; t0 += kTileT) {
+  R4 nu = load_raw4<T, kAligned>(u_row, a_col, L, a_ok);
+  R4 nd = load_raw4<T, kAligned>(d_row, a_col, L, a_ok);
+  R4 nz{};
+  if constexpr (kHasZ) nz = load_raw4<T, kAligned>(z_row, a_col, L, a_ok);
+
+  for (int t0 = 0; t0 < L; t0 += kTileF) {
+    const R4 ru = nu;
+    const R4 rz = nz;
     // ---- phase A
-    float uv[kPasses][kVec];
-    float zv[kHasZ ? kPasses : 1][kVec];
+    {
+      float uv[4], dv[4], de[4], du[4];
+      decode4(ru, uv);
+      decode4(nd, dv);
 #pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-      const int row = a_row + ps * kRPP;
-      const int c = d0 + row;
-      const int t = t0 + a_col;
-      const bool ok = c < Dm;
-      float dv[kVec];
-      load_row<T, kAligned>(u + (rb + c) * L, t, L, ok, uv[ps]);
-      load_row<T, kAligned>(dl + (rb + c) * L, t, L, ok, dv);
-      if constexpr (kHasZ) load_row<T, kAligned>(zp + (rb + c) * L, t, L, ok, zv[ps]);
-      float de[kVec], du[kVec];
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        const float x = dv[j] + Bias[ps];
+      for (int j = 0; j < 4; ++j) {
+        const float x = dv[j] + Bias;
         const float dt = softplus ? softplus_t20(x) : x;
-        const int tt = t + j;
+        const int tt = t0 + a_col + j;
         const bool valid = tt >= vlo && tt < vhi;
         de[j] = valid ? dt : 0.0f;
-        du[j] = de[j] * uv[ps][j];
+        du[j] = de[j] * uv[j];
       }
-#pragma unroll
-      for (int q = 0; q < kVec / 4; ++q) {
-        sDelta[a_col / 4 + q][row] = make_float4(de[4 * q], de[4 * q + 1], de[4 * q + 2], de[4 * q + 3]);
-        sDu[a_col / 4 + q][row] = make_float4(du[4 * q], du[4 * q + 1], du[4 * q + 2], du[4 * q + 3]);
-      }
+      sDelta[a_q][a_row] = make_float4(de[0], de[1], de[2], de[3]);
+      sDu[a_q][a_row] = make_float4(du[0], du[1], du[2], du[3]);
     }
     __syncthreads();
+    // the next tile's rows stream in while this tile is scanned
+    if (t0 + kTileF < L) {
+      const int t = t0 + kTileF + a_col;
+      nu = load_raw4<T, kAligned>(u_row, t, L, a_ok);
+      nd = load_raw4<T, kAligned>(d_row, t, L, a_ok);
+      if constexpr (kHasZ) nz = load_raw4<T, kAligned>(z_row, t, L, a_ok);
+    }
 
     // ---- phase B
     const int nT4 = min(kT4, (L - t0 + 3) / 4);
-    for (int t4 = 0; t4 < nT4; ++t4) {
-      float dlv[4], duv[4];
-      f4_to(sDelta[t4][lane], dlv);
-      f4_to(sDu[t4][lane], duv);
-      float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      const int tb = t0 + 4 * t4;
-#pragma unroll
-      for (int g = 0; g < kSG; ++g) {
-        const int G = g * kWaves + w;
-        if (G < ngroups) {
-          BC4 v;
-          load_bc_block(bc, bc_offset(b, G, ngroups, Lp, tb), v);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              const float a = fast_exp2(dlv[j] * A2[g][s]);
-              h[g][s] = fmaf(a, h[g][s], duv[j] * v.B(j, s));
-              y[j] = fmaf(v.C(j, s), h[g][s], y[j]);
-            }
-          }
-        }
-      }
-      sY[w][t4][lane] = make_float4(y[0], y[1], y[2], y[3]);
+    auto store_carry = [&](int t4) {
       if (save && (((t4 & 3) == 3) || t4 == nT4 - 1) && ch_ok) {
-        const int c = tb / kChunk;
+        const int c = (t0 + 4 * t4) / kChunk;
         float* hc = h_chunks + ((rb + ch) * p.nchunks + c) * N;
 #pragma unroll
         for (int g = 0; g < kSG; ++g)
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const int n = (g * kWaves + w) * 4 + s;
+          for (int s = 0; s < 2; ++s) {
+            const int n = (g * kWaves + w) * 2 + s;
             if (n < N) hc[n] = h[g][s];
           }
+      }
+    };
+    if constexpr (kSG == 1) {
+      // software-pipelined: block k+1's LDS and scalar loads are issued right
+      // after block k's have arrived, then block k is computed
+      if (w < ngroups) {
+        const size_t off0 = bc_offset(b, w, ngroups, Lp, t0);
+        float4 dlA = sDelta[0][lane], duA = sDu[0][lane], dlB, duB;
+        BC2 bcA, bcB;
+        load_bc_block(bc, off0, bcA);
+        int t4 = 0;
+        // pairs of blocks; every prefetch is unconditional (the index is
+        // clamped to the last block) so the buffers stay in scalar registers
+        for (; t4 + 1 < nT4; t4 += 2) {
+          wait_lgkm_fence();
+          dlB = sDelta[t4 + 1][lane];
+          duB = sDu[t4 + 1][lane];
+          load_bc_block(bc, off0 + (size_t)(t4 + 1) * 16, bcB);
+          sched_fence();
+          {
+            float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            fwd_block(dlA, duA, bcA, A2[0], h[0], y);
+            sY[w][t4][lane] = make_float4(y[0], y[1], y[2], y[3]);
+            store_carry(t4);
+          }
+          wait_lgkm_fence();
+          const int n2 = min(t4 + 2, nT4 - 1);
+          dlA = sDelta[n2][lane];
+          duA = sDu[n2][lane];
+          load_bc_block(bc, off0 + (size_t)n2 * 16, bcA);
+          sched_fence();
+          {
+            float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            fwd_block(dlB, duB, bcB, A2[0], h[0], y);
+            sY[w][t4 + 1][lane] = make_float4(y[0], y[1], y[2], y[3]);
+            store_carry(t4 + 1);
+          }
+        }
+        if (t4 < nT4) {  // odd last block
+          wait_lgkm_fence();
+          float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          fwd_block(dlA, duA, bcA, A2[0], h[0], y);
+          sY[w][t4][lane] = make_float4(y[0], y[1], y[2], y[3]);
+          store_carry(t4);
+        }
+      } else {
+        for (int t4 = 0; t4 < nT4; ++t4) sY[w][t4][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    } else {
+      for (int t4 = 0; t4 < nT4; ++t4) {
+        const float4 dl4 = sDelta[t4][lane], du4 = sDu[t4][lane];
+        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int tb = t0 + 4 * t4;
+#pragma unroll
+        for (int g = 0; g < kSG; ++g) {
+          const int G = g * kWaves + w;
+          if (G < ngroups) {
+            BC2 v;
+            load_bc_block(bc, bc_offset(b, G, ngroups, Lp, tb), v);
+            fwd_block(dl4, du4, v, A2[g], h[g], y);
+          }
+        }
+        sY[w][t4][lane] = make_float4(y[0], y[1], y[2], y[3]);
+        store_carry(t4);
       }
     }
     __syncthreads();
 
     // ---- phase C
-#pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-      const int row = a_row + ps * kRPP;
-      const int c = d0 + row;
+    {
       const int t = t0 + a_col;
-      if (c < Dm && t < L) {
-        float y[kVec];
+      if (a_ok && t < L) {
+        float uv[4], y[4];
+        decode4(ru, uv);
+        float4 acc = sY[0][a_q][a_row];
 #pragma unroll
-        for (int q = 0; q < kVec / 4; ++q) {
-          const float4 y0 = sY[0][a_col / 4 + q][row];
-          const float4 y1 = sY[1][a_col / 4 + q][row];
-          const float4 y2 = sY[2][a_col / 4 + q][row];
-          const float4 y3 = sY[3][a_col / 4 + q][row];
-          y[4 * q + 0] = (y0.x + y1.x) + (y2.x + y3.x);
-          y[4 * q + 1] = (y0.y + y1.y) + (y2.y + y3.y);
-          y[4 * q + 2] = (y0.z + y1.z) + (y2.z + y3.z);
-          y[4 * q + 3] = (y0.w + y1.w) + (y2.w + y3.w);
+        for (int ww = 1; ww < kWaves; ++ww) {
+          const float4 v = sY[ww][a_q][a_row];
+          acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
         }
+        y[0] = fmaf(Dv, uv[0], acc.x);
+        y[1] = fmaf(Dv, uv[1], acc.y);
+        y[2] = fmaf(Dv, uv[2], acc.z);
+        y[3] = fmaf(Dv, uv[3], acc.w);
+        if constexpr (kHasZ) {
+          float zv[4];
+          decode4(rz, zv);
 #pragma unroll
-        for (int j = 0; j < kVec; ++j) {
-          float v = fmaf(Dv[ps], uv[ps][j], y[j]);
-          if constexpr (kHasZ) v *= silu_f(zv[ps][j]);
-          y[j] = v;
+          for (int j = 0; j < 4; ++j) y[j] *= silu_f(zv[j]);
         }
-        store_row<T, kAligned>(out + (rb + c) * L, t, L, y);
+        store4<T, kAligned>(out + (rb + a_ch) * L, t, L, y);
       }
     }
   }
@@ -229,8 +283,8 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 #pragma unroll
     for (int g = 0; g < kSG; ++g)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int n = (g * kWaves + w) * 4 + s;
+      for (int s = 0; s < 2; ++s) {
+        const int n = (g * kWaves + w) * 2 + s;
         if (n < N) h_last[(rb + ch) * N + n] = h[g][s];
       }
   }
@@ -239,12 +293,12 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 // ---------------------------------------------------------------- launch
 
 size_t bc_prep_floats(int batch, int nstate, int seqlen) {
-  const size_t ngroups = (nstate + 3) / 4;
-  return (size_t)batch * ngroups * bc_row_len(seqlen) * 8;
+  const size_t ngroups = (nstate + 1) / 2;
+  return (size_t)batch * ngroups * bc_row_len(seqlen) * 4;
 }
 
 hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t st) {
-  const int ngroups = (p.nstate + 3) / 4;
+  const int ngroups = (p.nstate + 1) / 2;
   const int Lp = bc_row_len(p.seqlen);
   const size_t total = (size_t)p.batch * ngroups * Lp;
   const int blocks = (int)std::min<size_t>((total + 255) / 256, 65535);
@@ -263,7 +317,7 @@ template <typename T, int kSG, bool kHasZ, bool kAligned>
 static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t st) {
   dim3 grid(p.nblk, p.batch);
   ProfScope prof("scan_fwd", st);
-  hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(256), 0, st,
+  hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(kThreads), 0, st,
                      dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias,
                      p.h_init, p.length, (const T*)p.z, (T*)p.out, p.h_chunks, p.h_last);
   return hipGetLastError();

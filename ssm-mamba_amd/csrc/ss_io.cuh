@@ -39,20 +39,20 @@ __device__ __forceinline__ void store_row(T* __restrict__ row, int t, int L,
 }
 
 // B and C re-laid out for the scan kernels by bc_prep_kernel: fp32,
-// [b][state group G = n/4][t (padded to a multiple of 4)][s = n%4][B, C].
-// One 4-step block of one state group is 32 contiguous floats, which a wave
-// (whose group, batch row and steps are uniform) reads with two scalar
-// s_load_dwordx16 -- no VALU or LDS work for B/C.
-struct BC4 {
-  float v[32];  // [j (step)][s (state)][0: B, 1: C]
-  __device__ __forceinline__ float B(int j, int s) const { return v[j * 8 + s * 2]; }
-  __device__ __forceinline__ float C(int j, int s) const { return v[j * 8 + s * 2 + 1]; }
+// [b][state pair G = n/2][t (rows padded to whole 16-step chunks)][s = n%2][B, C].
+// One 4-step block of one state pair is 16 contiguous floats, which a wave
+// (whose pair, batch row and steps are uniform) reads with one scalar
+// s_load_dwordx16 -- no VALU, LDS or vector-memory work for B and C.
+struct BC2 {
+  float v[16];  // [j (step)][s (state)][0: B, 1: C]
+  __device__ __forceinline__ float B(int j, int s) const { return v[j * 4 + s * 2]; }
+  __device__ __forceinline__ float C(int j, int s) const { return v[j * 4 + s * 2 + 1]; }
 };
 
-__device__ __forceinline__ void load_bc_block(const float* __restrict__ bc, size_t off, BC4& r) {
+__device__ __forceinline__ void load_bc_block(const float* __restrict__ bc, size_t off, BC2& r) {
   // off is wave-uniform; the __restrict__ kernel argument lets these be s_loads
 #pragma unroll
-  for (int i = 0; i < 32; ++i) r.v[i] = bc[off + i];
+  for (int i = 0; i < 16; ++i) r.v[i] = bc[off + i];
 }
 
 // Row length of the prepped layout: whole 16-step chunks, so every 4-step
@@ -60,8 +60,73 @@ __device__ __forceinline__ void load_bc_block(const float* __restrict__ bc, size
 __host__ __device__ inline int bc_row_len(int L) { return (L + 15) & ~15; }
 
 __device__ __forceinline__ size_t bc_offset(int b, int G, int ngroups, int Lp, int t) {
-  return (((size_t)b * ngroups + G) * Lp + t) * 8;
+  return (((size_t)b * ngroups + G) * Lp + t) * 4;
 }
+
+// 4 consecutive elements of a row as raw bits (8 B of bf16 or 16 B of fp32).
+template <typename T> struct Raw4;
+template <> struct Raw4<float> { using type = uint4; };
+template <> struct Raw4<__hip_bfloat16> { using type = uint2; };
+
+// kAligned: L % 4 == 0 and rows 16-byte aligned, so a 4-element group is
+// either wholly inside or wholly outside [0, L).
+template <typename T, bool kAligned>
+__device__ __forceinline__ typename Raw4<T>::type load_raw4(const T* __restrict__ row, int t, int L,
+                                                            bool ok) {
+  using R = typename Raw4<T>::type;
+  if constexpr (kAligned) {
+    if (ok && t < L) return *reinterpret_cast<const R*>(row + t);
+    R z{};
+    return z;
+  } else {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (ok && t + j < L) ? Elem<T>::load1(row + t + j) : 0.0f;
+    if constexpr (sizeof(T) == 4) {
+      return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                        __float_as_uint(v[3]));
+    } else {
+      return make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+  }
+}
+
+__device__ __forceinline__ void decode4(const uint4 r, float (&v)[4]) {
+  v[0] = __uint_as_float(r.x); v[1] = __uint_as_float(r.y);
+  v[2] = __uint_as_float(r.z); v[3] = __uint_as_float(r.w);
+}
+__device__ __forceinline__ void decode4(const uint2 r, float (&v)[4]) {
+  v[0] = bf16_lo(r.x); v[1] = bf16_hi(r.x); v[2] = bf16_lo(r.y); v[3] = bf16_hi(r.y);
+}
+
+template <typename T, bool kAligned>
+__device__ __forceinline__ void store4(T* __restrict__ row, int t, int L, const float (&v)[4]) {
+  if constexpr (kAligned) {
+    if (t < L) {
+      if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<float4*>(row + t) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+        *reinterpret_cast<uint2*>(row + t) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (t + j < L) Elem<T>::store1(row + t + j, v[j]);
+  }
+}
+
+// Wait until every outstanding LDS and scalar-memory load of this wave has
+// returned (s_waitcnt lgkmcnt(0)) and keep the scheduler from moving
+// instructions across this point.  Orders "consume block k" before "issue
+// block k+1", so one block of work hides the latency of the next block's loads
+// (scalar loads may return out of order, so lgkmcnt can only be waited to 0).
+__device__ __forceinline__ void wait_lgkm_fence() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt=63, expcnt=7, lgkmcnt=0 (gfx9 encoding)
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 __device__ __forceinline__ void f4_to(const float4 x, float (&v)[4]) {
   v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;

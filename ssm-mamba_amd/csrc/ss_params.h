@@ -15,9 +15,11 @@
 namespace ssm {
 
 constexpr int kChunk = 16;    // steps between saved states
-constexpr int kTileT = 64;    // steps staged through LDS per forward tile
-constexpr int kTileBwd = 32;  // steps staged through LDS per backward tile
+constexpr int kTileF = 32;    // steps staged through LDS per forward tile
+constexpr int kTileB = 16;    // steps staged through LDS per backward tile
 constexpr int kBlockCh = 64;  // channels per workgroup (one per lane)
+constexpr int kWaves = 8;     // waves per workgroup; wave w owns state pairs G = g*8 + w
+constexpr int kThreads = 64 * kWaves;
 
 // Scalar shape/flag block passed to the scan kernels (pointers travel as
 // separate __restrict__ kernel arguments).
