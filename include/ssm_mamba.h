@@ -16,9 +16,9 @@
  * Shapes: u/delta/z/out/dout/du/ddelta/dz (batch, dim, seqlen);
  * B/C/dB/dC (batch, nstate, seqlen); A/dA (dim, nstate); D/delta_bias/dD/
  * ddelta_bias (dim); h_init/h_last/dh_last/dh_init (batch, dim, nstate);
- * h_chunks (batch, dim, ssm_scan_nchunks(seqlen), nstate): the state after
- * each SSM_CHUNK steps (the last entry is the final state); length (batch)
- * int64.
+ * h_chunks (batch, ssm_scan_nchunks(seqlen), nstate, dim): the state after
+ * each SSM_CHUNK steps, channel-contiguous (h_chunks[:, -1] transposed is the
+ * final state); length (batch) int64.
  */
 #ifndef SSM_MAMBA_H_
 #define SSM_MAMBA_H_

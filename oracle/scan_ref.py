@@ -280,17 +280,18 @@ def make_inputs(batch, dim, seqlen, nstate, seed=0, dtype=torch.float32,
     D = 1 (``modules/mamba.py:75``).  Values are generated in float32 on the CPU
     and rounded once to ``dtype`` for u/delta/z/B/C."""
     g = torch.Generator().manual_seed(seed)
-    u = torch.randn(batch, dim, seqlen, generator=g)
-    delta = torch.randn(batch, dim, seqlen, generator=g) + delta_shift
-    z = torch.randn(batch, dim, seqlen, generator=g) if with_z else None
-    Bm = torch.randn(batch, nstate, seqlen, generator=g)
-    Cm = torch.randn(batch, nstate, seqlen, generator=g)
-    A = -torch.arange(1, nstate + 1, dtype=torch.float32)[None, :].expand(dim, nstate).contiguous()
-    dtv = torch.exp(torch.rand(dim, generator=g) * (math.log(0.1) - math.log(1e-3))
+    f32 = torch.float32
+    u = torch.randn(batch, dim, seqlen, generator=g, dtype=f32)
+    delta = torch.randn(batch, dim, seqlen, generator=g, dtype=f32) + delta_shift
+    z = torch.randn(batch, dim, seqlen, generator=g, dtype=f32) if with_z else None
+    Bm = torch.randn(batch, nstate, seqlen, generator=g, dtype=f32)
+    Cm = torch.randn(batch, nstate, seqlen, generator=g, dtype=f32)
+    A = -torch.arange(1, nstate + 1, dtype=f32)[None, :].expand(dim, nstate).contiguous()
+    dtv = torch.exp(torch.rand(dim, generator=g, dtype=f32) * (math.log(0.1) - math.log(1e-3))
                     + math.log(1e-3)).clamp(min=1e-4)
     bias = inv_softplus(dtv)
-    Dv = torch.ones(dim)
-    hi = torch.randn(batch, dim, nstate, generator=g) if h_init else None
+    Dv = torch.ones(dim, dtype=f32)
+    hi = torch.randn(batch, dim, nstate, generator=g, dtype=f32) if h_init else None
     rd = lambda t: None if t is None else t.to(dtype)
     return {
         "u": rd(u), "delta": rd(delta), "A": A, "B": rd(Bm), "C": rd(Cm),

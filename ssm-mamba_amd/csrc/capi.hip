@@ -282,8 +282,8 @@ int ssm_selective_state_update(int64_t batch, int64_t dim, int64_t nstate, int d
                                int dt_softplus, void* out, void* stream) {
   g_err.clear();
   if (int e = check_common(batch, dim, 1, nstate, dtype, 256)) return e;
-  if ((uint64_t)batch * (uint64_t)dim * 64 > (uint64_t)UINT_MAX * 256)
-    return fail(SSM_ERR_UNSUPPORTED, "batch * dim too large");
+  if (dim * 64 > INT_MAX || batch * dim * nstate >= ((int64_t)1 << 31))
+    return fail(SSM_ERR_UNSUPPORTED, "state too large: batch * dim * nstate must be < 2^31");
   if (!state || !new_state || !x || !dt || !A || !B || !C || !out)
     return fail(SSM_ERR_INVALID, "state, new_state, x, dt, A, B, C and out must be non-NULL");
   ssm::UpdateParams p{};

@@ -192,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         const int n = (g * kWaves + w) * 2 + s;
         float v = 0.0f;
         if (ch_ok && n < N) {
-          if (tile > 0) v = h_chunks[((rb + ch) * p.nchunks + (tile - 1)) * N + n];
+          if (tile > 0) v = h_chunks[(((size_t)b * p.nchunks + (tile - 1)) * N + n) * Dm + ch];
           else if (h_init) v = h_init[(rb + ch) * N + n];
         }
         hc[g][s] = v;

@@ -22,7 +22,8 @@
 //            its own LDS slice;
 //   phase C  the phase-A threads add the eight slices in a fixed order, D*u
 //            and the z gate, and store the tile.
-// The state after every kChunk steps is saved for the backward (h_chunks).
+// The state after every kChunk steps is saved for the backward (h_chunks,
+// laid out (batch, nchunks, nstate, dim) so the saves are coalesced).
 #include "ss_io.cuh"
 #include "ss_params.h"
 #include "ss_prof.h"
@@ -175,14 +176,16 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
     const int nT4 = min(kT4, (L - t0 + 3) / 4);
     auto store_carry = [&](int t4) {
       if (save && (((t4 & 3) == 3) || t4 == nT4 - 1) && ch_ok) {
+        // layout (batch, nchunks, nstate, dim): each state is one contiguous
+        // 256 B run of the wave's 64 channels
         const int c = (t0 + 4 * t4) / kChunk;
-        float* hc = h_chunks + ((rb + ch) * p.nchunks + c) * N;
+        float* hc = h_chunks + ((size_t)b * p.nchunks + c) * N * (size_t)Dm + ch;
 #pragma unroll
         for (int g = 0; g < kSG; ++g)
 #pragma unroll
           for (int s = 0; s < 2; ++s) {
             const int n = (g * kWaves + w) * 2 + s;
-            if (n < N) hc[n] = h[g][s];
+            if (n < N) hc[(size_t)n * Dm] = h[g][s];
           }
       }
     };

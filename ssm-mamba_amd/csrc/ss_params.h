@@ -5,7 +5,7 @@
 //   A, dA                                  : (dim, nstate)          fp32
 //   D, delta_bias, dD, ddelta_bias         : (dim,)                 fp32
 //   h_init, h_last, dh_last, dh_init       : (batch, dim, nstate)   fp32
-//   h_chunks                               : (batch, dim, nchunks, nstate) fp32,
+//   h_chunks                               : (batch, nchunks, nstate, dim) fp32,
 //                                            state after each kChunk steps
 //   length                                 : (batch,) int64
 #pragma once

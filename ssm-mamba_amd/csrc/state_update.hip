@@ -4,103 +4,127 @@
 //   delta = softplus(dt + bias_d);  h'_n = exp(delta * A_dn) * h_n + delta * x * B_n
 //   out   = D_d * x + sum_n C_n h'_n            (* silu(z) when z is given)
 // The step is a pure stream over the fp32 state (64 B in and 64 B out per
-// (b, d) at N = 16), so one thread owns one (b, d) row and all its states:
-// consecutive lanes own consecutive rows, a wave streams 64 contiguous state
-// rows (4 KB at N = 16) with 128-bit accesses, the sum over states stays in
-// registers and x / dt / z / out are coalesced 16-bit accesses.  A and the
-// per-batch B, C rows are small and cache-resident.  The new state may alias
-// the old one (in-place update): each thread reads its whole row before
-// writing it.
+// (b, d) at N = 16), so the layout is chosen for contiguous 128-bit access:
+// kQ lanes per (b, d) row, each owning 4 consecutive states (one float4 of h,
+// of A and of the new state), so a wave's state access is one contiguous
+// 1 KB stretch; the out-sum over states is a kQ-lane DPP/shuffle reduction.
+// Measured on MI355X this runs at ~1.27x the time of a plain copy of the
+// state, where one thread per row (64 B per lane, 64 lines per wave access)
+// runs at ~1.6x.  The new state may alias the old one (in-place update): every
+// lane reads its float4 before writing it.
 #include "ss_io.cuh"
 #include "ss_params.h"
 #include "ss_prof.h"
 
 namespace ssm {
 
-// kN4: number of float4 state groups handled per thread when N % 4 == 0
-// (N = 4 * kN4); kN4 = 0 selects the generic scalar path for any N.
-template <typename T, int kN4>
+// Sum over aligned groups of kW lanes (every lane gets its group's sum); DPP
+// quad permutes for the 2- and 4-lane levels, shuffles above.
+template <int kW>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  if constexpr (kW >= 2) v += dpp_mov<kDppQuadXor1>(v);
+  if constexpr (kW >= 4) v += dpp_mov<kDppQuadXor2>(v);
+#pragma unroll
+  for (int m = 4; m < kW; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// kQ lanes per (b, d); kVecN: N == 4 * kQ (whole float4 groups, aligned).
+template <typename T, int kQ, bool kVecN>
 __global__ __launch_bounds__(256) void state_update_kernel(
     const int batch, const int dim, const int N, const int softplus,
     const float* __restrict__ state, float* new_state, const T* __restrict__ xp,
     const T* __restrict__ dtp, const float* __restrict__ Ap, const T* __restrict__ Bp,
     const T* __restrict__ Cp, const float* __restrict__ Dp, const float* __restrict__ biasp,
     const T* __restrict__ zp, T* __restrict__ out) {
-  const size_t bd = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-  if (bd >= (size_t)batch * dim) return;
-  const int d = (int)(bd % dim);
-  const int b = (int)(bd / dim);
-
-  const float x = Elem<T>::load1(xp + bd);
-  const float v = Elem<T>::load1(dtp + bd) + (biasp ? biasp[d] : 0.0f);
-  const float zv = zp ? Elem<T>::load1(zp + bd) : 0.0f;
-  const float delta = softplus ? softplus_t20(v) : v;
-  const float dx = delta * x;
-  const float dl2 = delta * kLog2e;
+  // grid: x covers dim * kQ lanes of one batch row, y = batch row (no
+  // integer division by runtime sizes); offsets are 32-bit (the host checks
+  // batch * dim * nstate < 2^31) so loads use a scalar base + 32-bit offset
+  const int gx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int q = gx % kQ;
+  const int d = gx / kQ;
+  // groups of kQ lanes are aligned inside a wave and are either all in range
+  // or all out of range, so the group reduction below sees whole groups
+  if (d >= dim) return;
+  const int b = blockIdx.y;
+  const unsigned bd = (unsigned)b * dim + d;
+  const int n0 = q * 4;
+  const unsigned so = bd * (unsigned)N + n0;        // state offset
+  const unsigned ao = (unsigned)d * N + n0;         // A offset
+  const unsigned bo = (unsigned)b * N + n0;         // B / C offset
 
   float part = 0.0f;
-  if constexpr (kN4 > 0) {
-    const float4* __restrict__ hs = reinterpret_cast<const float4*>(state + bd * (4 * kN4));
-    const float4* __restrict__ as = reinterpret_cast<const float4*>(Ap + (size_t)d * (4 * kN4));
-    float4 h4[kN4];
+  float x, delta;
+  if constexpr (kVecN) {
+    const float4 h4 = *reinterpret_cast<const float4*>(state + so);
+    const float4 a4 = *reinterpret_cast<const float4*>(Ap + ao);
+    float Bv[4], Cv[4];
+    Elem<T>::load4(Bp + bo, Bv);
+    Elem<T>::load4(Cp + bo, Cv);
+    x = Elem<T>::load1(xp + bd);
+    const float v = Elem<T>::load1(dtp + bd) + (biasp ? biasp[d] : 0.0f);
+    delta = softplus ? softplus_t20(v) : v;
+    const float dx = delta * x, dl2 = delta * kLog2e;
+    float hv[4] = {h4.x, h4.y, h4.z, h4.w};
+    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
-    for (int q = 0; q < kN4; ++q) h4[q] = hs[q];
-#pragma unroll
-    for (int q = 0; q < kN4; ++q) {
-      const float4 a4 = as[q];
-      float Bv[4], Cv[4];
-      Elem<T>::load4(Bp + (size_t)b * (4 * kN4) + 4 * q, Bv);
-      Elem<T>::load4(Cp + (size_t)b * (4 * kN4) + 4 * q, Cv);
-      float hv[4] = {h4[q].x, h4[q].y, h4[q].z, h4[q].w};
-      const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        hv[s] = fmaf(fast_exp2(dl2 * av[s]), hv[s], dx * Bv[s]);
-        part = fmaf(Cv[s], hv[s], part);
-      }
-      h4[q] = make_float4(hv[0], hv[1], hv[2], hv[3]);
+    for (int s = 0; s < 4; ++s) {
+      hv[s] = fmaf(fast_exp2(dl2 * av[s]), hv[s], dx * Bv[s]);
+      part = fmaf(Cv[s], hv[s], part);
     }
-    float4* hn = reinterpret_cast<float4*>(new_state + bd * (4 * kN4));
-#pragma unroll
-    for (int q = 0; q < kN4; ++q) hn[q] = h4[q];
+    *reinterpret_cast<float4*>(new_state + so) = make_float4(hv[0], hv[1], hv[2], hv[3]);
   } else {
-    for (int n = 0; n < N; ++n) {
-      const float hn = fmaf(fast_exp2(dl2 * Ap[(size_t)d * N + n]), state[bd * N + n],
-                            dx * Elem<T>::load1(Bp + (size_t)b * N + n));
-      new_state[bd * N + n] = hn;
-      part = fmaf(Elem<T>::load1(Cp + (size_t)b * N + n), hn, part);
+    x = Elem<T>::load1(xp + bd);
+    const float v = Elem<T>::load1(dtp + bd) + (biasp ? biasp[d] : 0.0f);
+    delta = softplus ? softplus_t20(v) : v;
+    const float dx = delta * x, dl2 = delta * kLog2e;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (n0 + s < N) {
+        const float hn = fmaf(fast_exp2(dl2 * Ap[ao + s]), state[so + s], dx * Elem<T>::load1(Bp + bo + s));
+        new_state[so + s] = hn;
+        part = fmaf(Elem<T>::load1(Cp + bo + s), hn, part);
+      }
     }
   }
-  float y = fmaf(Dp ? Dp[d] : 0.0f, x, part);
-  if (zp) y *= silu_f(zv);
-  Elem<T>::store1(out + bd, y);
+  part = lane_group_sum<kQ>(part);
+  if (q == 0) {
+    float y = fmaf(Dp ? Dp[d] : 0.0f, x, part);
+    if (zp) y *= silu_f(Elem<T>::load1(zp + bd));
+    Elem<T>::store1(out + bd, y);
+  }
 }
 
-template <typename T, int kN4>
-static hipError_t launch_upd2(const UpdateParams& p, hipStream_t st) {
-  const size_t threads = (size_t)p.batch * p.dim;
-  const unsigned blocks = (unsigned)((threads + 255) / 256);
+template <typename T, int kQ>
+static hipError_t launch_upd2(const UpdateParams& p, bool vecN, hipStream_t st) {
+  const size_t lanes = (size_t)p.dim * kQ;
+  const dim3 grid((unsigned)((lanes + 255) / 256), (unsigned)p.batch);
   ProfScope prof("state_update", st);
-  hipLaunchKernelGGL((state_update_kernel<T, kN4>), dim3(blocks), dim3(256), 0, st, p.batch,
-                     p.dim, p.nstate, p.softplus, p.state, p.new_state, (const T*)p.x,
-                     (const T*)p.dt, p.A, (const T*)p.B, (const T*)p.C, p.D, p.bias,
-                     (const T*)p.z, (T*)p.out);
+  if (vecN)
+    hipLaunchKernelGGL((state_update_kernel<T, kQ, true>), grid, dim3(256), 0, st, p.batch,
+                       p.dim, p.nstate, p.softplus, p.state, p.new_state, (const T*)p.x,
+                       (const T*)p.dt, p.A, (const T*)p.B, (const T*)p.C, p.D, p.bias,
+                       (const T*)p.z, (T*)p.out);
+  else
+    hipLaunchKernelGGL((state_update_kernel<T, kQ, false>), grid, dim3(256), 0, st,
+                       p.batch, p.dim, p.nstate, p.softplus, p.state, p.new_state, (const T*)p.x,
+                       (const T*)p.dt, p.A, (const T*)p.B, (const T*)p.C, p.D, p.bias,
+                       (const T*)p.z, (T*)p.out);
   return hipGetLastError();
 }
 
 template <typename T>
 static hipError_t launch_upd1(const UpdateParams& p, bool vecN, hipStream_t st) {
-  if (vecN) {
-    switch (p.nstate) {
-      case 4: return launch_upd2<T, 1>(p, st);
-      case 8: return launch_upd2<T, 2>(p, st);
-      case 16: return launch_upd2<T, 4>(p, st);
-      case 32: return launch_upd2<T, 8>(p, st);
-      case 64: return launch_upd2<T, 16>(p, st);
-      default: break;
-    }
-  }
-  return launch_upd2<T, 0>(p, st);
+  const int nq = (p.nstate + 3) / 4;
+  // the vector path needs N == 4 * kQ exactly
+  auto vec = [&](int kq) { return vecN && p.nstate == 4 * kq; };
+  if (nq <= 1) return launch_upd2<T, 1>(p, vec(1), st);
+  if (nq <= 2) return launch_upd2<T, 2>(p, vec(2), st);
+  if (nq <= 4) return launch_upd2<T, 4>(p, vec(4), st);
+  if (nq <= 8) return launch_upd2<T, 8>(p, vec(8), st);
+  if (nq <= 16) return launch_upd2<T, 16>(p, vec(16), st);
+  if (nq <= 32) return launch_upd2<T, 32>(p, vec(32), st);
+  return launch_upd2<T, 64>(p, vec(64), st);
 }
 
 hipError_t launch_state_update(const UpdateParams& p, int dtype, bool vecN, hipStream_t st) {

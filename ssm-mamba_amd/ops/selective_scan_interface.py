@@ -48,7 +48,7 @@ class SelectiveScanFn(torch.autograd.Function):
         if need_grad:
             ctx.save_for_backward(u, A32, B, C, D32, delta, bias32, h, h0, length)
             ctx.padding_size = padding_size
-            return out, h[..., -1, :]
+            return out, selective_scan.last_state(h)
         return out, h
 
     @staticmethod
@@ -82,7 +82,7 @@ class _SelectiveScanExtFn(torch.autograd.Function):
             ctx.save_for_backward(u, delta, A32, B, C, D32, z, bias32, h, h0, length)
             ctx.delta_softplus = delta_softplus
             ctx.padding_side = padding_side
-            return out, h[..., -1, :]
+            return out, selective_scan.last_state(h)
         return out, h
 
     @staticmethod

@@ -12,8 +12,10 @@ Differences, all deliberate:
   (one dtype for all of them); A, D, delta_bias, h_init are float32.
 * The chunk-state carrier ``h`` returned by ``forward`` and consumed by
   ``backward`` holds the state after every 16 steps, shape
-  (batch, dim, ceil(seqlen/16), state_dim), float32; its last chunk is the
-  final state (the reference stores (prod a, h) pairs per 128 steps).
+  (batch, ceil(seqlen/16), state_dim, dim), float32, channel-contiguous so
+  the kernels' saves and reloads are coalesced; ``h[:, -1].transpose(1, 2)``
+  is the final state (the reference stores (prod a, h) pairs per 128 steps,
+  ``(batch, dim, nchunks, 2*state_dim)``, and takes ``h[..., -1, 1::2]``).
 * Keyword extensions: ``z`` (fused output gate out * silu(z)),
   ``delta_softplus`` and, for ``forward``, ``save_chunks=False`` (inference:
   only the final state is produced).
@@ -104,21 +106,26 @@ def nchunks(seqlen: int) -> int:
     return (seqlen + N.SSM_CHUNK - 1) // N.SSM_CHUNK
 
 
+def last_state(h: torch.Tensor) -> torch.Tensor:
+    """Final state (batch, dim, state_dim) of a chunk-state carrier, as a view."""
+    return h[:, -1].transpose(1, 2)
+
+
 def forward(u: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
             D: Optional[torch.Tensor], delta: torch.Tensor, delta_bias: Optional[torch.Tensor],
             h_init: Optional[torch.Tensor] = None, length: Optional[torch.Tensor] = None,
             padding_side: Optional[str] = None, *, z: Optional[torch.Tensor] = None,
             delta_softplus: bool = True, save_chunks: bool = True) -> List[torch.Tensor]:
     """Returns [out, h]: out (batch, dim, seqlen) in u's dtype (gated by silu(z)
-    when z is given) and h, the chunk-state carrier (batch, dim, nchunks,
-    state_dim) float32 -- or, with save_chunks=False, the final state
+    when z is given) and h, the chunk-state carrier (batch, nchunks,
+    state_dim, dim) float32 -- or, with save_chunks=False, the final state
     (batch, dim, state_dim)."""
     batch, dim, seqlen, nstate = _validate(u, A, B, C, D, delta, delta_bias, h_init, length, z)
     L = N.lib()
     dev = u.device
     out = torch.empty_like(u)
     if save_chunks:
-        h = torch.empty(batch, dim, nchunks(seqlen), nstate, device=dev, dtype=torch.float32)
+        h = torch.empty(batch, nchunks(seqlen), nstate, dim, device=dev, dtype=torch.float32)
         h_chunks, h_last = h, None
     else:
         h = torch.empty(batch, dim, nstate, device=dev, dtype=torch.float32)
@@ -150,8 +157,8 @@ def backward(u: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
     if nstate > 64:
         raise RuntimeError("selective_scan backward only supports state_dim <= 64")
     _check_dim(h, 4, "h")
-    _check(h, "h", (batch, dim, nchunks(seqlen), nstate),
-           "batch_size, num_channels, num_chunks, state_dim", (torch.float32,), "float32")
+    _check(h, "h", (batch, nchunks(seqlen), nstate, dim),
+           "batch_size, num_chunks, state_dim, num_channels", (torch.float32,), "float32")
     _check_dim(dout, 3, "dout")
     _check(dout, "dout", (batch, dim, seqlen), "batch_size, num_channels, seq_len", (u.dtype,),
            str(u.dtype).replace("torch.", "") + " (the dtype of u)")

@@ -35,8 +35,8 @@ def run_case(cuda, batch, dim, seqlen, nstate, dtype, *, seed=0, with_z=True, h_
                      c["h_init"], length, pr, c["z"], softplus)
     torch.cuda.synchronize()
     assert_close(out, ref["y"], dtype, "out")
-    assert_close(h, ref["h_chunks"], torch.float32 if dtype == torch.float32 else dtype, "h_chunks",
-                 scale_atol=True)
+    assert_close(h.permute(0, 3, 1, 2), ref["h_chunks"],
+                 torch.float32 if dtype == torch.float32 else dtype, "h_chunks", scale_atol=True)
     if not bwd:
         return
     g = torch.Generator().manual_seed(seed + 100)
@@ -123,7 +123,8 @@ def test_config1_full_size_properties(cuda):
     ref = R.scan_fwd(cs["u"], cs["delta"], cs["A"], cs["B"], cs["C"], cs["D"], cs["delta_bias"],
                      None, None, True, cs["z"], True, dtype=torch.float64)
     assert_close(out[:, sub], ref["y"], torch.bfloat16, "out[subset]")
-    assert_close(h[:, sub], ref["h_chunks"], torch.bfloat16, "h[subset]", scale_atol=True)
+    assert_close(h.permute(0, 3, 1, 2)[:, sub], ref["h_chunks"], torch.bfloat16, "h[subset]",
+                 scale_atol=True)
     g = torch.Generator().manual_seed(5)
     dy = torch.randn(batch, dim, seqlen, generator=g).to(torch.bfloat16).to(cuda)
     args = (d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"], h, None, dy, None)
@@ -173,9 +174,9 @@ def test_split_sequence_on_gpu(cuda):
     o1, h1 = ss.forward(p1["u"], c["A"], p1["B"], p1["C"], c["D"], p1["delta"], c["delta_bias"],
                         None, None, None, z=p1["z"])
     o2, h2 = ss.forward(p2["u"], c["A"], p2["B"], p2["C"], c["D"], p2["delta"], c["delta_bias"],
-                        h1[:, :, -1].contiguous(), None, None, z=p2["z"])
+                        ss.last_state(h1).contiguous(), None, None, z=p2["z"])
     torch.testing.assert_close(torch.cat([o1, o2], -1), out, rtol=1e-5, atol=1e-6)
-    torch.testing.assert_close(h2[:, :, -1], h[:, :, -1], rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(ss.last_state(h2), ss.last_state(h), rtol=1e-5, atol=1e-6)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -14,7 +14,16 @@ import torch.nn.functional as F
 
 from oracle import scan_ref as R
 
-torch.set_default_dtype(torch.float64)
+
+
+@pytest.fixture(autouse=True)
+def _float64_default():
+    """These checks run in float64; the default is restored afterwards so
+    other test modules keep float32."""
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
 
 
 def rand_case(batch=2, dim=3, seqlen=37, nstate=4, seed=0, h_init=True, z=True,
