@@ -28,6 +28,14 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 
+# HBM bytes per launch of the config-1 scan kernels from rocprofv3 counter runs
+# of `bench.py --profile-run` (profiles/scan_decode_hbm_bytes.md):
+# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB, the factors being what the same
+# counters read for a 256 MiB device-to-device copy.  Re-measure after a
+# kernel change.
+TRAFFIC_BYTES = {"scan_fwd": (2 * 115_362 + 213_144) * 1024,
+                 "scan_bwd": (2 * 396_834 + 374_343) * 1024}
+
 
 def inputs(batch, dim, seqlen, nstate, dtype, dev, seed, delta_shift=0.0):
     import math
@@ -138,6 +146,23 @@ def time_decode(su, dev, steps, cold):
     return 1e3 * e0.elapsed_time(e1) / steps
 
 
+def decode_eager(su, dev, steps):
+    """Config 2 decode steps launched one by one over 16 rotating states (for
+    counter runs, which see each launch as its own dispatch)."""
+    import torch
+    batch, dim, nstate = 64, 5120, 16
+    g = torch.Generator().manual_seed(2)
+    states = [(torch.randn(batch, dim, nstate, generator=g) * 0.1).to(dev) for _ in range(16)]
+    A = -torch.arange(1, nstate + 1, dtype=torch.float32)[None].expand(dim, nstate).contiguous().to(dev)
+    bias = torch.full((dim,), -4.0, device=dev)
+    D = torch.ones(dim, device=dev)
+    x, dt, z = (torch.randn(batch, dim, generator=g).bfloat16().to(dev) for _ in range(3))
+    B, C = (torch.randn(batch, nstate, generator=g).bfloat16().to(dev) for _ in range(2))
+    out = torch.empty(batch, dim, dtype=torch.bfloat16, device=dev)
+    for k in range(steps):
+        su.apply_ext(x, A, B, C, D, dt, bias, states[k % 16], z=z, inplace=True, out=out)
+
+
 def cpu_baseline(seconds: float):
     """Times the CPU oracle (fp32 torch) forward+backward on the config-1 shape
     with a reduced channel count, sized to run about `seconds`."""
@@ -175,7 +200,19 @@ def cpu_baseline(seconds: float):
                    f"with z ({t:.1f} s); GB/s = token-channels/s x config-1 bytes per "
                    f"token-channel ({per_tc:.2f})"),
         "tokens_channels_per_s": round(tok_ch / t, 1),
+        "cpu_model": _cpu_model(),
     }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():
@@ -187,8 +224,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-extra", action="store_true", help="only the config-1 step")
     ap.add_argument("--profile-run", action="store_true",
-                    help="for rocprofv3 counter runs: config-1 fwd+bwd (--steps times) plus one "
-                         "256 MiB device-to-device copy (reference for the byte counters); no JSON")
+                    help="for rocprofv3 counter runs: one 256 MiB device-to-device copy (reference for "
+                         "the byte counters), config-1 fwd+bwd (--steps times), 32 eager config-2 "
+                         "decode steps; no JSON")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -211,7 +249,9 @@ def main():
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
         dst.copy_(src)  # 256 MiB read + 256 MiB written
+        del src, dst
         time_scan(ss, N, x, args.steps, args.warmup)
+        decode_eager(su, dev, 32)
         torch.cuda.synchronize()
         print("profile run done", flush=True)
         return
@@ -246,7 +286,7 @@ def main():
         "kernels_ms": {k: round(v, 4) for k, v in kern.items()},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": TRAFFIC_BYTES.get(dom), "traffic_unit": "B",
                      "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_ms": round(dom_ms, 4)},
     }
     if not args.no_extra:
