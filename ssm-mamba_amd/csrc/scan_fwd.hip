@@ -62,6 +62,14 @@ __global__ __launch_bounds__(256) void bc_prep_kernel(const int batch, const int
 
 // ---------------------------------------------------------------- forward
 
+// LDS column swizzle.  Tile columns (4-step groups q = 0..7) of 64 channel
+// rows are stored at row index r ^ col_swz(q).  Phase A/C threads access one
+// row's 8 columns across 8 consecutive lanes, and without the swizzle those
+// columns (1 KiB apart) fall in the same banks; with it every 8- or 16-lane
+// group of a ds_write_b128 / ds_read_b128 touches distinct banks.  Phase B
+// reads whole columns, a permutation of 64 consecutive float4s.
+__device__ __forceinline__ constexpr int col_swz(int q) { return q | ((q & 1) << 3); }
+
 // One 4-step block of the recurrence for the wave's 2 states.
 __device__ __forceinline__ void fwd_block(const float4 dl4, const float4 du4, const BC2& v,
                                           const float (&A2)[2], float (&h)[2], float (&y)[4]) {
@@ -128,6 +136,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   const int a_row = tid / kT4;
   const int a_q = tid % kT4;
   const int a_col = a_q * 4;
+  const int a_sw = a_row ^ col_swz(a_q);
   const int a_ch = d0 + a_row;
   const bool a_ok = a_ch < Dm;
   const float Dv = (a_ok && Dp) ? Dp[a_ch] : 0.0f;
@@ -160,8 +169,8 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
         de[j] = valid ? dt : 0.0f;
         du[j] = de[j] * uv[j];
       }
-      sDelta[a_q][a_row] = make_float4(de[0], de[1], de[2], de[3]);
-      sDu[a_q][a_row] = make_float4(du[0], du[1], du[2], du[3]);
+      sDelta[a_q][a_sw] = make_float4(de[0], de[1], de[2], de[3]);
+      sDu[a_q][a_sw] = make_float4(du[0], du[1], du[2], du[3]);
     }
     __syncthreads();
     // the next tile's rows stream in while this tile is scanned
@@ -190,38 +199,70 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       }
     };
     if constexpr (kSG == 1) {
-      // software-pipelined: block k+1's LDS and scalar loads are issued right
-      // after block k's have arrived, then block k is computed
-      if (w < ngroups) {
+      if (w < ngroups && nT4 == kT4) {
+        // full tile, fully unrolled: static B/C offsets and buffers, carries
+        // after blocks 3 and 7.  Block k+1's LDS and scalar loads are issued
+        // right after block k's have arrived, then block k is computed.
         const size_t off0 = bc_offset(b, w, ngroups, Lp, t0);
-        float4 dlA = sDelta[0][lane], duA = sDu[0][lane], dlB, duB;
+        float* hc = (save && ch_ok)
+                        ? h_chunks + (((size_t)b * p.nchunks + t0 / kChunk) * N + 2 * w) * Dm + ch
+                        : nullptr;
+        const bool second = 2 * w + 1 < N;
+        BC2 bcb[2];
+        float4 dlb[2], dub[2];
+        load_bc_block(bc, off0, bcb[0]);
+        dlb[0] = sDelta[0][lane ^ col_swz(0)];
+        dub[0] = sDu[0][lane ^ col_swz(0)];
+#pragma unroll
+        for (int k = 0; k < kT4; ++k) {
+          const int c = k & 1;
+          wait_lgkm_fence();
+          if (k + 1 < kT4) {
+            dlb[c ^ 1] = sDelta[k + 1][lane ^ col_swz(k + 1)];
+            dub[c ^ 1] = sDu[k + 1][lane ^ col_swz(k + 1)];
+            load_bc_block(bc, off0 + (size_t)(k + 1) * 16, bcb[c ^ 1]);
+          }
+          sched_fence();
+          float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          fwd_block(dlb[c], dub[c], bcb[c], A2[0], h[0], y);
+          sY[w][k][lane ^ col_swz(k)] = make_float4(y[0], y[1], y[2], y[3]);
+          if ((k & 3) == 3 && hc) {
+            float* q = hc + (size_t)(k / 4) * N * Dm;
+            q[0] = h[0][0];
+            if (second) q[Dm] = h[0][1];
+          }
+        }
+      } else if (w < ngroups) {
+        // partial last tile: software-pipelined pairs of blocks; every
+        // prefetch is unconditional (the index is clamped to the last block)
+        // so the buffers stay in scalar registers
+        const size_t off0 = bc_offset(b, w, ngroups, Lp, t0);
+        float4 dlA = sDelta[0][lane ^ col_swz(0)], duA = sDu[0][lane ^ col_swz(0)], dlB, duB;
         BC2 bcA, bcB;
         load_bc_block(bc, off0, bcA);
         int t4 = 0;
-        // pairs of blocks; every prefetch is unconditional (the index is
-        // clamped to the last block) so the buffers stay in scalar registers
         for (; t4 + 1 < nT4; t4 += 2) {
           wait_lgkm_fence();
-          dlB = sDelta[t4 + 1][lane];
-          duB = sDu[t4 + 1][lane];
+          dlB = sDelta[t4 + 1][lane ^ col_swz(t4 + 1)];
+          duB = sDu[t4 + 1][lane ^ col_swz(t4 + 1)];
           load_bc_block(bc, off0 + (size_t)(t4 + 1) * 16, bcB);
           sched_fence();
           {
             float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             fwd_block(dlA, duA, bcA, A2[0], h[0], y);
-            sY[w][t4][lane] = make_float4(y[0], y[1], y[2], y[3]);
+            sY[w][t4][lane ^ col_swz(t4)] = make_float4(y[0], y[1], y[2], y[3]);
             store_carry(t4);
           }
           wait_lgkm_fence();
           const int n2 = min(t4 + 2, nT4 - 1);
-          dlA = sDelta[n2][lane];
-          duA = sDu[n2][lane];
+          dlA = sDelta[n2][lane ^ col_swz(n2)];
+          duA = sDu[n2][lane ^ col_swz(n2)];
           load_bc_block(bc, off0 + (size_t)n2 * 16, bcA);
           sched_fence();
           {
             float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             fwd_block(dlB, duB, bcB, A2[0], h[0], y);
-            sY[w][t4 + 1][lane] = make_float4(y[0], y[1], y[2], y[3]);
+            sY[w][t4 + 1][lane ^ col_swz(t4 + 1)] = make_float4(y[0], y[1], y[2], y[3]);
             store_carry(t4 + 1);
           }
         }
@@ -229,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
           wait_lgkm_fence();
           float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
           fwd_block(dlA, duA, bcA, A2[0], h[0], y);
-          sY[w][t4][lane] = make_float4(y[0], y[1], y[2], y[3]);
+          sY[w][t4][lane ^ col_swz(t4)] = make_float4(y[0], y[1], y[2], y[3]);
           store_carry(t4);
         }
       } else {
@@ -237,7 +278,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       }
     } else {
       for (int t4 = 0; t4 < nT4; ++t4) {
-        const float4 dl4 = sDelta[t4][lane], du4 = sDu[t4][lane];
+        const float4 dl4 = sDelta[t4][lane ^ col_swz(t4)], du4 = sDu[t4][lane ^ col_swz(t4)];
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         const int tb = t0 + 4 * t4;
 #pragma unroll
@@ -249,7 +290,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
             fwd_block(dl4, du4, v, A2[g], h[g], y);
           }
         }
-        sY[w][t4][lane] = make_float4(y[0], y[1], y[2], y[3]);
+        sY[w][t4][lane ^ col_swz(t4)] = make_float4(y[0], y[1], y[2], y[3]);
         store_carry(t4);
       }
     }
@@ -261,10 +302,10 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       if (a_ok && t < L) {
         float uv[4], y[4];
         decode4(ru, uv);
-        float4 acc = sY[0][a_q][a_row];
+        float4 acc = sY[0][a_q][a_sw];
 #pragma unroll
         for (int ww = 1; ww < kWaves; ++ww) {
-          const float4 v = sY[ww][a_q][a_row];
+          const float4 v = sY[ww][a_q][a_sw];
           acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
         }
         y[0] = fmaf(Dv, uv[0], acc.x);
