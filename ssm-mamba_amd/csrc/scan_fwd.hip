@@ -70,6 +70,16 @@ __global__ __launch_bounds__(256) void bc_prep_kernel(const int batch, const int
 // reads whole columns, a permutation of 64 consecutive float4s.
 __device__ __forceinline__ constexpr int col_swz(int q) { return q | ((q & 1) << 3); }
 
+// A 4-step block of one state pair's prepped B/C from LDS (the same address
+// in every lane: broadcast reads).
+__device__ __forceinline__ void lds_bc_block(const float4* __restrict__ row, int step, BC2& r) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float4 q = row[step + j];
+    r.v[4 * j] = q.x; r.v[4 * j + 1] = q.y; r.v[4 * j + 2] = q.z; r.v[4 * j + 3] = q.w;
+  }
+}
+
 // One 4-step block of the recurrence for the wave's 2 states.
 __device__ __forceinline__ void fwd_block(const float4 dl4, const float4 du4, const BC2& v,
                                           const float (&A2)[2], float (&h)[2], float (&y)[4]) {
@@ -98,12 +108,15 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
     const T* __restrict__ zp, T* __restrict__ out, float* __restrict__ h_chunks,
     float* __restrict__ h_last) {
   using R4 = typename Raw4<T>::type;
-  constexpr int kT4 = kTileF / 4;
+  constexpr int kT4 = kTileF / 4;        // 4-step columns per sub-tile
+  constexpr int kSup = kSubF * kTileF;   // steps staged per super-tile
   static_assert(kBlockCh * kT4 == kThreads, "one 4-step row piece per thread");
 
-  __shared__ float4 sDelta[kT4][kBlockCh];
-  __shared__ float4 sDu[kT4][kBlockCh];
+  __shared__ float4 sDelta[kSubF * kT4][kBlockCh];
+  __shared__ float4 sDu[kSubF * kT4][kBlockCh];
   __shared__ float4 sY[kWaves][kT4][kBlockCh];
+  // prepped B/C of the super-tile for state pairs 0..7: [sub][pair][step]
+  __shared__ float4 sBC[kSubF][kWaves][kTileF];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -132,7 +145,8 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       h[g][s] = (ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
     }
 
-  // ---- tile-phase mapping: thread = (channel row, 4 consecutive steps)
+  // ---- tile-phase mapping: thread = (channel row, 4 consecutive steps of
+  // every sub-tile)
   const int a_row = tid / kT4;
   const int a_q = tid % kT4;
   const int a_col = a_q * 4;
@@ -147,180 +161,230 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   const bool softplus = p.softplus != 0;
   const bool save = h_chunks != nullptr;
 
-  R4 nu = load_raw4<T, kAligned>(u_row, a_col, L, a_ok);
-  R4 nd = load_raw4<T, kAligned>(d_row, a_col, L, a_ok);
-  R4 nz{};
-  if constexpr (kHasZ) nz = load_raw4<T, kAligned>(z_row, a_col, L, a_ok);
-
-  for (int t0 = 0; t0 < L; t0 += kTileF) {
-    const R4 ru = nu;
-    const R4 rz = nz;
-    // ---- phase A
-    {
-      float uv[4], dv[4], de[4], du[4];
-      decode4(ru, uv);
-      decode4(nd, dv);
+  // Raw row pieces of the next super-tile, all loads issued at once right
+  // after the current super-tile's phase A.  They are consumed together at
+  // the next phase A, so each register is carried exactly one iteration.
+  // Past the end the last sub-tile is re-read (unconditional loads keep the
+  // registers free of merges).
+  const int last_t0 = (L - 1) / kTileF * kTileF;
+  R4 qu[kSubF], qd[kSubF], qz[kSubF];
+  // B/C staging: thread -> (pair, step) of the super-tile, kBCPer float4 each
+  constexpr int kBCItems = kSubF * kWaves * kTileF;
+  constexpr int kBCPer = kBCItems / kThreads;
+  static_assert(kBCItems % kThreads == 0, "whole B/C items per thread");
+  const float4* __restrict__ bc4 = reinterpret_cast<const float4*>(bc);
+  float4 qbc[kBCPer];
+  auto issue = [&](int T0) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float x = dv[j] + Bias;
-        const float dt = softplus ? softplus_t20(x) : x;
-        const int tt = t0 + a_col + j;
-        const bool valid = tt >= vlo && tt < vhi;
-        de[j] = valid ? dt : 0.0f;
-        du[j] = de[j] * uv[j];
+    for (int i = 0; i < kSubF; ++i) {
+      const int t = min(T0 + i * kTileF, last_t0) + a_col;
+      qu[i] = load_raw4<T, kAligned>(u_row, t, L, a_ok);
+      qd[i] = load_raw4<T, kAligned>(d_row, t, L, a_ok);
+      if constexpr (kHasZ) qz[i] = load_raw4<T, kAligned>(z_row, t, L, a_ok);
+      else qz[i] = R4{};
+    }
+    if constexpr (kSG == 1) {
+#pragma unroll
+      for (int r = 0; r < kBCPer; ++r) {
+        const int item = r * kThreads + tid;
+        const int step = item % kTileF;
+        const int G = (item / kTileF) % kWaves;
+        const int sub = item / (kTileF * kWaves);
+        // clamped into the pair's prepped row (rows are padded to 16 steps;
+        // steps past it are never read by phase B)
+        const int t = min(min(T0, last_t0) + sub * kTileF + step, Lp - 1);
+        const int Gc = min(G, ngroups - 1);
+        qbc[r] = bc4[((size_t)b * ngroups + Gc) * Lp + t];
       }
-      sDelta[a_q][a_sw] = make_float4(de[0], de[1], de[2], de[3]);
-      sDu[a_q][a_sw] = make_float4(du[0], du[1], du[2], du[3]);
+    }
+  };
+  issue(0);
+
+  for (int T0 = 0; T0 < L; T0 += kSup) {
+    // ---- phase A: softplus once per element, stage delta and delta*u for
+    // the whole super-tile; D*u and silu(z) are kept for phase C.
+    float skip[kSubF][4], gate[kSubF][4];
+#pragma unroll
+    for (int i = 0; i < kSubF; ++i) {
+      const int t0 = T0 + i * kTileF;
+      if (t0 < L) {
+        float uv[4], dv[4], de[4], du[4];
+        decode4(qu[i], uv);
+        decode4(qd[i], dv);
+        if constexpr (kHasZ) {
+          float zv[4];
+          decode4(qz[i], zv);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) gate[i][j] = silu_f(zv[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          skip[i][j] = Dv * uv[j];
+          const float x = dv[j] + Bias;
+          const float dt = softplus ? softplus_t20(x) : x;
+          const int tt = t0 + a_col + j;
+          const bool valid = tt >= vlo && tt < vhi;
+          de[j] = valid ? dt : 0.0f;
+          du[j] = de[j] * uv[j];
+        }
+        sDelta[i * kT4 + a_q][a_sw] = make_float4(de[0], de[1], de[2], de[3]);
+        sDu[i * kT4 + a_q][a_sw] = make_float4(du[0], du[1], du[2], du[3]);
+      }
+    }
+    if constexpr (kSG == 1) {
+#pragma unroll
+      for (int r = 0; r < kBCPer; ++r) {
+        const int item = r * kThreads + tid;
+        sBC[item / (kTileF * kWaves)][(item / kTileF) % kWaves][item % kTileF] = qbc[r];
+      }
     }
     __syncthreads();
-    // the next tile's rows stream in while this tile is scanned
-    if (t0 + kTileF < L) {
-      const int t = t0 + kTileF + a_col;
-      nu = load_raw4<T, kAligned>(u_row, t, L, a_ok);
-      nd = load_raw4<T, kAligned>(d_row, t, L, a_ok);
-      if constexpr (kHasZ) nz = load_raw4<T, kAligned>(z_row, t, L, a_ok);
-    }
+    issue(T0 + kSup);
 
-    // ---- phase B
-    const int nT4 = min(kT4, (L - t0 + 3) / 4);
-    auto store_carry = [&](int t4) {
-      if (save && (((t4 & 3) == 3) || t4 == nT4 - 1) && ch_ok) {
-        // layout (batch, nchunks, nstate, dim): each state is one contiguous
-        // 256 B run of the wave's 64 channels
-        const int c = (t0 + 4 * t4) / kChunk;
-        float* hc = h_chunks + ((size_t)b * p.nchunks + c) * N * (size_t)Dm + ch;
 #pragma unroll
-        for (int g = 0; g < kSG; ++g)
+    for (int i = 0; i < kSubF; ++i) {
+      const int t0 = T0 + i * kTileF;
+      if (t0 >= L) break;
+      const float4* __restrict__ cDelta = sDelta[i * kT4];
+      const float4* __restrict__ cDu = sDu[i * kT4];
+      // ---- phase B over sub-tile i
+      const int nT4 = min(kT4, (L - t0 + 3) / 4);
+      auto store_carry = [&](int t4) {
+        if (save && (((t4 & 3) == 3) || t4 == nT4 - 1) && ch_ok) {
+          // layout (batch, nchunks, nstate, dim): each state is one
+          // contiguous 256 B run of the wave's 64 channels
+          const int c = (t0 + 4 * t4) / kChunk;
+          float* hc = h_chunks + ((size_t)b * p.nchunks + c) * N * (size_t)Dm + ch;
 #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const int n = (g * kWaves + w) * 2 + s;
-            if (n < N) hc[(size_t)n * Dm] = h[g][s];
-          }
-      }
-    };
-    if constexpr (kSG == 1) {
-      if (w < ngroups && nT4 == kT4) {
-        // full tile, fully unrolled: static B/C offsets and buffers, carries
-        // after blocks 3 and 7.  Block k+1's LDS and scalar loads are issued
-        // right after block k's have arrived, then block k is computed.
-        const size_t off0 = bc_offset(b, w, ngroups, Lp, t0);
-        float* hc = (save && ch_ok)
-                        ? h_chunks + (((size_t)b * p.nchunks + t0 / kChunk) * N + 2 * w) * Dm + ch
-                        : nullptr;
-        const bool second = 2 * w + 1 < N;
-        BC2 bcb[2];
-        float4 dlb[2], dub[2];
-        load_bc_block(bc, off0, bcb[0]);
-        dlb[0] = sDelta[0][lane ^ col_swz(0)];
-        dub[0] = sDu[0][lane ^ col_swz(0)];
+          for (int g = 0; g < kSG; ++g)
 #pragma unroll
-        for (int k = 0; k < kT4; ++k) {
-          const int c = k & 1;
-          wait_lgkm_fence();
-          if (k + 1 < kT4) {
-            dlb[c ^ 1] = sDelta[k + 1][lane ^ col_swz(k + 1)];
-            dub[c ^ 1] = sDu[k + 1][lane ^ col_swz(k + 1)];
-            load_bc_block(bc, off0 + (size_t)(k + 1) * 16, bcb[c ^ 1]);
-          }
-          sched_fence();
-          float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-          fwd_block(dlb[c], dub[c], bcb[c], A2[0], h[0], y);
-          sY[w][k][lane ^ col_swz(k)] = make_float4(y[0], y[1], y[2], y[3]);
-          if ((k & 3) == 3 && hc) {
-            float* q = hc + (size_t)(k / 4) * N * Dm;
-            q[0] = h[0][0];
-            if (second) q[Dm] = h[0][1];
-          }
+            for (int s = 0; s < 2; ++s) {
+              const int n = (g * kWaves + w) * 2 + s;
+              if (n < N) hc[(size_t)n * Dm] = h[g][s];
+            }
         }
-      } else if (w < ngroups) {
-        // partial last tile: software-pipelined pairs of blocks; every
-        // prefetch is unconditional (the index is clamped to the last block)
-        // so the buffers stay in scalar registers
-        const size_t off0 = bc_offset(b, w, ngroups, Lp, t0);
-        float4 dlA = sDelta[0][lane ^ col_swz(0)], duA = sDu[0][lane ^ col_swz(0)], dlB, duB;
-        BC2 bcA, bcB;
-        load_bc_block(bc, off0, bcA);
-        int t4 = 0;
-        for (; t4 + 1 < nT4; t4 += 2) {
-          wait_lgkm_fence();
-          dlB = sDelta[t4 + 1][lane ^ col_swz(t4 + 1)];
-          duB = sDu[t4 + 1][lane ^ col_swz(t4 + 1)];
-          load_bc_block(bc, off0 + (size_t)(t4 + 1) * 16, bcB);
-          sched_fence();
-          {
+      };
+      if constexpr (kSG == 1) {
+        if (w < ngroups && nT4 == kT4) {
+          // full sub-tile, fully unrolled: static B/C offsets and buffers,
+          // carries after blocks 3 and 7.  Block k+1's LDS and scalar loads
+          // are issued right after block k's have arrived, then block k is
+          // computed.
+          const float4* __restrict__ cBC = sBC[i][w];
+          float* hc = (save && ch_ok)
+                          ? h_chunks + (((size_t)b * p.nchunks + t0 / kChunk) * N + 2 * w) * Dm + ch
+                          : nullptr;
+          const bool second = 2 * w + 1 < N;
+          BC2 bcb[2];
+          float4 dlb[2], dub[2];
+          lds_bc_block(cBC, 0, bcb[0]);
+          dlb[0] = cDelta[lane ^ col_swz(0)];
+          dub[0] = cDu[lane ^ col_swz(0)];
+#pragma unroll
+          for (int k = 0; k < kT4; ++k) {
+            const int c = k & 1;
+            if (k + 1 < kT4) {
+              dlb[c ^ 1] = cDelta[(k + 1) * kBlockCh + (lane ^ col_swz(k + 1))];
+              dub[c ^ 1] = cDu[(k + 1) * kBlockCh + (lane ^ col_swz(k + 1))];
+              lds_bc_block(cBC, 4 * (k + 1), bcb[c ^ 1]);
+            }
+            float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            fwd_block(dlb[c], dub[c], bcb[c], A2[0], h[0], y);
+            sY[w][k][lane ^ col_swz(k)] = make_float4(y[0], y[1], y[2], y[3]);
+            if ((k & 3) == 3 && hc) {
+              float* q = hc + (size_t)(k / 4) * N * Dm;
+              q[0] = h[0][0];
+              if (second) q[Dm] = h[0][1];
+            }
+          }
+        } else if (w < ngroups) {
+          // partial last sub-tile: pairs of blocks; every prefetch is
+          // unconditional (the index is clamped to the last block) so the
+          // buffers stay in scalar registers
+          const float4* __restrict__ cBC = sBC[i][w];
+          float4 dlA = cDelta[lane ^ col_swz(0)], duA = cDu[lane ^ col_swz(0)], dlB, duB;
+          BC2 bcA, bcB;
+          lds_bc_block(cBC, 0, bcA);
+          int t4 = 0;
+          for (; t4 + 1 < nT4; t4 += 2) {
+            dlB = cDelta[(t4 + 1) * kBlockCh + (lane ^ col_swz(t4 + 1))];
+            duB = cDu[(t4 + 1) * kBlockCh + (lane ^ col_swz(t4 + 1))];
+            lds_bc_block(cBC, 4 * (t4 + 1), bcB);
+            {
+              float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+              fwd_block(dlA, duA, bcA, A2[0], h[0], y);
+              sY[w][t4][lane ^ col_swz(t4)] = make_float4(y[0], y[1], y[2], y[3]);
+              store_carry(t4);
+            }
+            const int n2 = min(t4 + 2, nT4 - 1);
+            dlA = cDelta[n2 * kBlockCh + (lane ^ col_swz(n2))];
+            duA = cDu[n2 * kBlockCh + (lane ^ col_swz(n2))];
+            lds_bc_block(cBC, 4 * n2, bcA);
+            {
+              float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+              fwd_block(dlB, duB, bcB, A2[0], h[0], y);
+              sY[w][t4 + 1][lane ^ col_swz(t4 + 1)] = make_float4(y[0], y[1], y[2], y[3]);
+              store_carry(t4 + 1);
+            }
+          }
+          if (t4 < nT4) {  // odd last block
             float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             fwd_block(dlA, duA, bcA, A2[0], h[0], y);
             sY[w][t4][lane ^ col_swz(t4)] = make_float4(y[0], y[1], y[2], y[3]);
             store_carry(t4);
           }
-          wait_lgkm_fence();
-          const int n2 = min(t4 + 2, nT4 - 1);
-          dlA = sDelta[n2][lane ^ col_swz(n2)];
-          duA = sDu[n2][lane ^ col_swz(n2)];
-          load_bc_block(bc, off0 + (size_t)n2 * 16, bcA);
-          sched_fence();
-          {
-            float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            fwd_block(dlB, duB, bcB, A2[0], h[0], y);
-            sY[w][t4 + 1][lane ^ col_swz(t4 + 1)] = make_float4(y[0], y[1], y[2], y[3]);
-            store_carry(t4 + 1);
-          }
+        } else {
+          for (int t4 = 0; t4 < nT4; ++t4) sY[w][t4][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
-        if (t4 < nT4) {  // odd last block
-          wait_lgkm_fence();
+      } else {
+        for (int t4 = 0; t4 < nT4; ++t4) {
+          const float4 dl4 = cDelta[t4 * kBlockCh + (lane ^ col_swz(t4))];
+          const float4 du4 = cDu[t4 * kBlockCh + (lane ^ col_swz(t4))];
           float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-          fwd_block(dlA, duA, bcA, A2[0], h[0], y);
+          const int tb = t0 + 4 * t4;
+#pragma unroll
+          for (int g = 0; g < kSG; ++g) {
+            const int G = g * kWaves + w;
+            if (G < ngroups) {
+              BC2 v;
+              load_bc_block(bc, bc_offset(b, G, ngroups, Lp, tb), v);
+              fwd_block(dl4, du4, v, A2[g], h[g], y);
+            }
+          }
           sY[w][t4][lane ^ col_swz(t4)] = make_float4(y[0], y[1], y[2], y[3]);
           store_carry(t4);
         }
-      } else {
-        for (int t4 = 0; t4 < nT4; ++t4) sY[w][t4][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
-    } else {
-      for (int t4 = 0; t4 < nT4; ++t4) {
-        const float4 dl4 = sDelta[t4][lane ^ col_swz(t4)], du4 = sDu[t4][lane ^ col_swz(t4)];
-        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const int tb = t0 + 4 * t4;
-#pragma unroll
-        for (int g = 0; g < kSG; ++g) {
-          const int G = g * kWaves + w;
-          if (G < ngroups) {
-            BC2 v;
-            load_bc_block(bc, bc_offset(b, G, ngroups, Lp, tb), v);
-            fwd_block(dl4, du4, v, A2[g], h[g], y);
-          }
-        }
-        sY[w][t4][lane ^ col_swz(t4)] = make_float4(y[0], y[1], y[2], y[3]);
-        store_carry(t4);
-      }
-    }
-    __syncthreads();
+      __syncthreads();
 
-    // ---- phase C
-    {
-      const int t = t0 + a_col;
-      if (a_ok && t < L) {
-        float uv[4], y[4];
-        decode4(ru, uv);
-        float4 acc = sY[0][a_q][a_sw];
+      // ---- phase C over sub-tile i: add the eight slices in a fixed order,
+      // D*u and the gate
+      {
+        const int t = t0 + a_col;
+        if (a_ok && t < L) {
+          float y[4];
+          float4 acc = sY[0][a_q][a_sw];
 #pragma unroll
-        for (int ww = 1; ww < kWaves; ++ww) {
-          const float4 v = sY[ww][a_q][a_sw];
-          acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-        }
-        y[0] = fmaf(Dv, uv[0], acc.x);
-        y[1] = fmaf(Dv, uv[1], acc.y);
-        y[2] = fmaf(Dv, uv[2], acc.z);
-        y[3] = fmaf(Dv, uv[3], acc.w);
-        if constexpr (kHasZ) {
-          float zv[4];
-          decode4(rz, zv);
+          for (int ww = 1; ww < kWaves; ++ww) {
+            const float4 v = sY[ww][a_q][a_sw];
+            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+          }
+          y[0] = skip[i][0] + acc.x;
+          y[1] = skip[i][1] + acc.y;
+          y[2] = skip[i][2] + acc.z;
+          y[3] = skip[i][3] + acc.w;
+          if constexpr (kHasZ) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) y[j] *= silu_f(zv[j]);
+            for (int j = 0; j < 4; ++j) y[j] *= gate[i][j];
+          }
+          store4<T, kAligned>(out + (rb + a_ch) * L, t, L, y);
         }
-        store4<T, kAligned>(out + (rb + a_ch) * L, t, L, y);
       }
+      // the next sub-tile's phase B rewrites the slices
+      if (i + 1 < kSubF && t0 + kTileF < L) __syncthreads();
     }
+    // the next phase A rewrites only sDelta / sDu, last read by the final
+    // phase B before the barrier that preceded the final phase C
   }
 
   if (!save && h_last && ch_ok) {

@@ -16,6 +16,7 @@ namespace ssm {
 
 constexpr int kChunk = 16;    // steps between saved states
 constexpr int kTileF = 32;    // steps staged through LDS per forward tile
+constexpr int kSubF = 4;      // forward sub-tiles staged (and loaded) together
 constexpr int kTileB = 16;    // steps staged through LDS per backward tile
 constexpr int kBlockCh = 64;  // channels per workgroup (one per lane)
 constexpr int kWaves = 8;     // waves per workgroup; wave w owns state pairs G = g*8 + w
