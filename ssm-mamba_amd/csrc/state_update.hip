@@ -29,8 +29,76 @@ __device__ __forceinline__ float lane_group_sum(float v) {
   return v;
 }
 
-// kQ lanes per (b, d); kVecN: N == 4 * kQ (whole float4 groups, aligned).
-template <typename T, int kQ, bool kVecN>
+// Vector path (N == 4 * kQ, 16-byte aligned state and A): kQ lanes per
+// (b, d) row and kRows rows per thread.  A wave covers 64 / kQ rows per slice
+// and kRows slices, each slice one contiguous 1 KB stretch of state; all of a
+// thread's loads are issued before any arithmetic, so a wave has kRows KB of
+// state in flight and the whole grid fits the machine in about one round.
+// Rows past `dim` load a clamped row and skip their stores.
+template <typename T, int kQ, int kRows>
+__global__ __launch_bounds__(256) void state_update_vec_kernel(
+    const int dim, const int N, const int softplus, const float* __restrict__ state,
+    float* new_state, const T* __restrict__ xp, const T* __restrict__ dtp,
+    const float* __restrict__ Ap, const T* __restrict__ Bp, const T* __restrict__ Cp,
+    const float* __restrict__ Dp, const float* __restrict__ biasp, const T* __restrict__ zp,
+    T* __restrict__ out) {
+  constexpr int kRW = 64 / kQ;  // rows per wave slice
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int q = lane % kQ;
+  const int b = blockIdx.y;
+  const int dbase = (blockIdx.x * 4 + wave) * (kRows * kRW) + lane / kQ;
+  const int n0 = q * 4;
+  const unsigned bo = (unsigned)b * N + n0;
+  float Bv[4], Cv[4];
+  Elem<T>::load4(Bp + bo, Bv);
+  Elem<T>::load4(Cp + bo, Cv);
+  float4 h4[kRows], a4[kRows];
+  float xv[kRows], dtv[kRows], bias[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const int d = min(dbase + r * kRW, dim - 1);
+    const unsigned bd = (unsigned)b * dim + d;
+    h4[r] = *reinterpret_cast<const float4*>(state + bd * (unsigned)N + n0);
+    a4[r] = *reinterpret_cast<const float4*>(Ap + (unsigned)d * N + n0);
+    xv[r] = Elem<T>::load1(xp + bd);
+    dtv[r] = Elem<T>::load1(dtp + bd);
+    bias[r] = biasp ? biasp[d] : 0.0f;
+  }
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const int dr = dbase + r * kRW;
+    const int d = min(dr, dim - 1);
+    const unsigned bd = (unsigned)b * dim + d;
+    const float v = dtv[r] + bias[r];
+    const float delta = softplus ? softplus_t20(v) : v;
+    const float dx = delta * xv[r], dl2 = delta * kLog2e;
+    float hv[4] = {h4[r].x, h4[r].y, h4[r].z, h4[r].w};
+    const float av[4] = {a4[r].x, a4[r].y, a4[r].z, a4[r].w};
+    float part = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      hv[s] = fmaf(fast_exp2(dl2 * av[s]), hv[s], dx * Bv[s]);
+      part = fmaf(Cv[s], hv[s], part);
+    }
+    // a row's kQ lanes are aligned in the wave and share `dr`, so the group
+    // reduction always sees whole rows
+    part = lane_group_sum<kQ>(part);
+    if (dr < dim) {
+      *reinterpret_cast<float4*>(new_state + bd * (unsigned)N + n0) =
+          make_float4(hv[0], hv[1], hv[2], hv[3]);
+      if (q == 0) {
+        float y = fmaf(Dp ? Dp[d] : 0.0f, xv[r], part);
+        if (zp) y *= silu_f(Elem<T>::load1(zp + bd));
+        Elem<T>::store1(out + bd, y);
+      }
+    }
+  }
+}
+
+// Scalar path (any N, any alignment): kQ lanes per (b, d) row, each owning
+// up to 4 consecutive states.
+template <typename T, int kQ>
 __global__ __launch_bounds__(256) void state_update_kernel(
     const int batch, const int dim, const int N, const int softplus,
     const float* __restrict__ state, float* new_state, const T* __restrict__ xp,
@@ -39,7 +107,7 @@ __global__ __launch_bounds__(256) void state_update_kernel(
     const T* __restrict__ zp, T* __restrict__ out) {
   // grid: x covers dim * kQ lanes of one batch row, y = batch row (no
   // integer division by runtime sizes); offsets are 32-bit (the host checks
-  // batch * dim * nstate < 2^31) so loads use a scalar base + 32-bit offset
+  // batch * dim * nstate < 2^31)
   const int gx = blockIdx.x * blockDim.x + threadIdx.x;
   const int q = gx % kQ;
   const int d = gx / kQ;
@@ -54,37 +122,16 @@ __global__ __launch_bounds__(256) void state_update_kernel(
   const unsigned bo = (unsigned)b * N + n0;         // B / C offset
 
   float part = 0.0f;
-  float x, delta;
-  if constexpr (kVecN) {
-    const float4 h4 = *reinterpret_cast<const float4*>(state + so);
-    const float4 a4 = *reinterpret_cast<const float4*>(Ap + ao);
-    float Bv[4], Cv[4];
-    Elem<T>::load4(Bp + bo, Bv);
-    Elem<T>::load4(Cp + bo, Cv);
-    x = Elem<T>::load1(xp + bd);
-    const float v = Elem<T>::load1(dtp + bd) + (biasp ? biasp[d] : 0.0f);
-    delta = softplus ? softplus_t20(v) : v;
-    const float dx = delta * x, dl2 = delta * kLog2e;
-    float hv[4] = {h4.x, h4.y, h4.z, h4.w};
-    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+  const float x = Elem<T>::load1(xp + bd);
+  const float v = Elem<T>::load1(dtp + bd) + (biasp ? biasp[d] : 0.0f);
+  const float delta = softplus ? softplus_t20(v) : v;
+  const float dx = delta * x, dl2 = delta * kLog2e;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      hv[s] = fmaf(fast_exp2(dl2 * av[s]), hv[s], dx * Bv[s]);
-      part = fmaf(Cv[s], hv[s], part);
-    }
-    *reinterpret_cast<float4*>(new_state + so) = make_float4(hv[0], hv[1], hv[2], hv[3]);
-  } else {
-    x = Elem<T>::load1(xp + bd);
-    const float v = Elem<T>::load1(dtp + bd) + (biasp ? biasp[d] : 0.0f);
-    delta = softplus ? softplus_t20(v) : v;
-    const float dx = delta * x, dl2 = delta * kLog2e;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (n0 + s < N) {
-        const float hn = fmaf(fast_exp2(dl2 * Ap[ao + s]), state[so + s], dx * Elem<T>::load1(Bp + bo + s));
-        new_state[so + s] = hn;
-        part = fmaf(Elem<T>::load1(Cp + bo + s), hn, part);
-      }
+  for (int s = 0; s < 4; ++s) {
+    if (n0 + s < N) {
+      const float hn = fmaf(fast_exp2(dl2 * Ap[ao + s]), state[so + s], dx * Elem<T>::load1(Bp + bo + s));
+      new_state[so + s] = hn;
+      part = fmaf(Elem<T>::load1(Cp + bo + s), hn, part);
     }
   }
   part = lane_group_sum<kQ>(part);
@@ -95,21 +142,26 @@ __global__ __launch_bounds__(256) void state_update_kernel(
   }
 }
 
+constexpr int kUpdRows = 4;  // rows per thread on the vector path
+
 template <typename T, int kQ>
 static hipError_t launch_upd2(const UpdateParams& p, bool vecN, hipStream_t st) {
-  const size_t lanes = (size_t)p.dim * kQ;
-  const dim3 grid((unsigned)((lanes + 255) / 256), (unsigned)p.batch);
   ProfScope prof("state_update", st);
-  if (vecN)
-    hipLaunchKernelGGL((state_update_kernel<T, kQ, true>), grid, dim3(256), 0, st, p.batch,
-                       p.dim, p.nstate, p.softplus, p.state, p.new_state, (const T*)p.x,
-                       (const T*)p.dt, p.A, (const T*)p.B, (const T*)p.C, p.D, p.bias,
-                       (const T*)p.z, (T*)p.out);
-  else
-    hipLaunchKernelGGL((state_update_kernel<T, kQ, false>), grid, dim3(256), 0, st,
-                       p.batch, p.dim, p.nstate, p.softplus, p.state, p.new_state, (const T*)p.x,
-                       (const T*)p.dt, p.A, (const T*)p.B, (const T*)p.C, p.D, p.bias,
-                       (const T*)p.z, (T*)p.out);
+  if (vecN) {
+    const int per_block = 4 * kUpdRows * (64 / kQ);  // rows per 256-thread block
+    const dim3 grid((unsigned)((p.dim + per_block - 1) / per_block), (unsigned)p.batch);
+    hipLaunchKernelGGL((state_update_vec_kernel<T, kQ, kUpdRows>), grid, dim3(256), 0, st, p.dim,
+                       p.nstate, p.softplus, p.state, p.new_state, (const T*)p.x, (const T*)p.dt,
+                       p.A, (const T*)p.B, (const T*)p.C, p.D, p.bias, (const T*)p.z,
+                       (T*)p.out);
+  } else {
+    const size_t lanes = (size_t)p.dim * kQ;
+    const dim3 grid((unsigned)((lanes + 255) / 256), (unsigned)p.batch);
+    hipLaunchKernelGGL((state_update_kernel<T, kQ>), grid, dim3(256), 0, st, p.batch, p.dim,
+                       p.nstate, p.softplus, p.state, p.new_state, (const T*)p.x, (const T*)p.dt,
+                       p.A, (const T*)p.B, (const T*)p.C, p.D, p.bias, (const T*)p.z,
+                       (T*)p.out);
+  }
   return hipGetLastError();
 }
 
