@@ -190,7 +190,8 @@ int64_t ssm_scan_nchunks(int64_t seqlen) { return seqlen <= 0 ? 0 : (seqlen + SS
 size_t ssm_scan_fwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate) {
   (void)dim;
   if (batch < 1 || seqlen < 1 || nstate < 1) return 0;
-  return round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
+  return round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float)) +
+         ssm::kDummyBytes;
 }
 
 size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate) {
@@ -199,7 +200,7 @@ size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, 
   return round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float)) +
          round256(2 * nblk * batch * nstate * seqlen * sizeof(float)) +
          round256((size_t)batch * dim * nstate * sizeof(float)) +
-         2 * round256((size_t)batch * dim * sizeof(float));
+         2 * round256((size_t)batch * dim * sizeof(float)) + ssm::kDummyBytes;
 }
 
 int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
@@ -220,6 +221,9 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   p.out = out;
   p.h_chunks = h_chunks;
   p.h_last = h_last;
+  // workspace: [prepped B/C][dummy]
+  p.dummy = static_cast<char*>(workspace) +
+            round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
   const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out});
   return hip_status(ssm::launch_scan_fwd(p, dtype, aligned, static_cast<float*>(workspace),
                                          static_cast<hipStream_t>(stream)),
@@ -259,7 +263,7 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   p.dC = dC;
   p.dD = dD;
   p.dbias = ddelta_bias;
-  // workspace: [prepped B/C][dB/dC partials][dA partials][dD partials][dbias partials]
+  // workspace: [prepped B/C][dB/dC partials][dA partials][dD partials][dbias partials][dummy]
   char* ws = static_cast<char*>(workspace);
   float* bc = reinterpret_cast<float*>(ws);
   ws += round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
@@ -270,6 +274,8 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   p.ws_D = reinterpret_cast<float*>(ws);
   ws += round256((size_t)batch * dim * sizeof(float));
   p.ws_bias = reinterpret_cast<float*>(ws);
+  ws += round256((size_t)batch * dim * sizeof(float));
+  p.dummy = ws;
   const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, dout, du, ddelta, dz});
   return hip_status(ssm::launch_scan_bwd(p, dtype, aligned, bc, static_cast<hipStream_t>(stream)),
                     "selective_scan backward launch");

@@ -79,12 +79,13 @@ __device__ __forceinline__ void bwd_reverse_block(int jq, const StepVals& sv, co
       const float Gt = fmaf(dov[j], v.C(j, s), gam[s]);
       sB = fmaf(Gt, v.B(j, s), sB);
       const float hp = i ? H[s][i - 1] : Hc[s];
-      const float gah = Gt * a[s][i] * hp;
-      sD = fmaf(Av[s], gah, sD);
-      dA[s] = fmaf(dlv[j], gah, dA[s]);
+      const float ng = a[s][i] * Gt;  // gamma_{t-1}
+      const float q = ng * hp;        // G_t a_t h_{t-1}
+      sD = fmaf(Av[s], q, sD);
+      dA[s] = fmaf(dlv[j], q, dA[s]);
       vals[s * kChunk + i] = Gt * duv[j];               // dB partial
       vals[2 * kChunk + s * kChunk + i] = dov[j] * H[s][i];  // dC partial
-      gam[s] = a[s][i] * Gt;
+      gam[s] = ng;
     }
     gB[j] = sB;
     gD[j] = sD;
@@ -92,6 +93,14 @@ __device__ __forceinline__ void bwd_reverse_block(int jq, const StepVals& sv, co
 }
 
 }  // namespace
+
+// LDS column swizzle of the 4-column (16-step) tiles: (row, column q) is
+// stored at row index row ^ bcol_swz(q).  The tile-phase threads access 4
+// columns of 16 rows per wave, and without the swizzle the columns (1 KiB
+// apart) share banks; with it every 8- or 16-lane group of a 128-bit LDS
+// access touches distinct banks.  Phase B reads whole columns (permutations of
+// 64 consecutive float4s).
+__device__ __forceinline__ constexpr int bcol_swz(int q) { return 4 * q + 2 * (q >> 1); }
 
 template <typename T, int kSG, bool kHasZ, bool kAligned>
 __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
@@ -104,24 +113,26 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     T* __restrict__ dzp, float* __restrict__ dh_init, float* __restrict__ ws_bc,
     float* __restrict__ ws_A, float* __restrict__ ws_D, float* __restrict__ ws_bias) {
   using R4 = typename Raw4<T>::type;
-  constexpr int kT4 = kTileB / 4;       // 4-step blocks per tile (4)
-  constexpr int kItems = kBlockCh * kT4;  // tile-phase work items (256)
-  constexpr int kStr = kTileB + 4;      // row stride of a slice (floats; 16-byte aligned rows)
-  constexpr int kSlice = kBlockCh * kStr;
+  constexpr int kT4 = kTileB / 4;         // 4-step columns per tile (4)
+  constexpr int kItems = kBlockCh * kT4;  // (row, column) items per tile (256)
+  static_assert(2 * kItems == kThreads, "two thread groups of one item each");
   static_assert(kTileB == kChunk, "one saved state per backward tile");
   constexpr int kMaxPairs = kSG * kWaves;  // state pairs covered by the dispatch bucket
   static_assert(kMaxPairs * kTileB <= kThreads, "one B/C float4 per thread per tile");
 
   __shared__ float4 sDelta[kT4][kBlockCh];  // delta (0 at padded steps)
   __shared__ float4 sDu[kT4][kBlockCh];     // delta * u
-  __shared__ float4 sDout[kT4][kBlockCh];   // masked dout (after the z gate)
-  __shared__ float4 sU[kT4][kBlockCh];
-  __shared__ float4 sX[kT4][kBlockCh];      // delta_raw + bias
+  // sDout and sU are written in phase A by one thread group and read in
+  // phase C by the other, with no barrier between a tile's phase C and the
+  // next tile's phase A: they alternate between two buffers by tile parity
+  __shared__ float4 sDout[2][kT4][kBlockCh];  // masked dout (after the z gate)
+  __shared__ float4 sU[2][kT4][kBlockCh];
+  __shared__ float4 sSg[kT4][kBlockCh];     // softplus'(x) (0 at padded steps)
   // one slice per wave of the per-position sums over that wave's states,
   // added in a fixed order in phase C (deterministic result)
-  __shared__ float sGB[kWaves * kSlice];   // sum_n G B
-  __shared__ float sDD[kWaves * kSlice];   // sum_n A G a h_{t-1}
-  __shared__ float sY[kHasZ ? kWaves * kSlice : 4];  // sum_n C h
+  __shared__ float4 sGB[kWaves][kT4][kBlockCh];  // sum_n G B
+  __shared__ float4 sDD[kWaves][kT4][kBlockCh];  // sum_n A G a h_{t-1}
+  __shared__ float4 sY[kHasZ ? kWaves : 1][kT4][kBlockCh];  // sum_n C h
   // the tile's prepped B/C rows of every state pair: [G][step][s][B, C]
   __shared__ float4 sBC[kMaxPairs][kTileB];
 
@@ -157,110 +168,126 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       A2[g][s] = Av[g][s] * kLog2e;
     }
 
-  // ---- tile-phase mapping: threads < kItems, item = (channel row, 4 steps)
-  const bool a_act = tid < kItems;
-  const int a_row = (tid % kItems) / kT4;
-  const int a_q = tid % kT4;
+  // ---- tile-phase mapping.  Group 0 (waves 0-3) owns the u / delta side
+  // (softplus, staging, then du, ddelta, dD, dbias); group 1 (waves 4-7) the
+  // dout / z side (the gate, staging dout, then dz).  Item = (channel row, 4
+  // consecutive steps) in both groups.
+  const bool grp1 = w >= kWaves / 2;
+  const int item = tid % kItems;
+  const int a_row = item / kT4;
+  const int a_q = item % kT4;
   const int a_col = a_q * 4;
+  const int a_sw = a_row ^ bcol_swz(a_q);
   const int a_ch = d0 + a_row;
-  const bool a_ok = a_act && a_ch < Dm;
+  const bool a_ok = a_ch < Dm;
   const float Dv = (a_ok && Dp) ? Dp[a_ch] : 0.0f;
   const float Bias = (a_ok && biasp) ? biasp[a_ch] : 0.0f;
-  const T* __restrict__ u_row = u + (rb + a_ch) * L;
-  const T* __restrict__ d_row = dl + (rb + a_ch) * L;
-  const T* __restrict__ y_row = dyp + (rb + a_ch) * L;
-  const T* __restrict__ z_row = zp + (rb + a_ch) * L;
+  const T* __restrict__ row1 = (grp1 ? dyp : u) + (rb + a_ch) * L;
+  const T* __restrict__ row2 = (grp1 ? zp : dl) + (rb + a_ch) * L;
+  const bool load2 = !grp1 || kHasZ;
   const bool softplus = p.softplus != 0;
   float accD = 0.0f, accB = 0.0f;
 
   const int ntiles = (L + kTileB - 1) / kTileB;
   // raw rows of the next tile to process (walking backwards), in flight
-  R4 nu, nd, ny, nz{};
+  // Every prefetch below is an unconditional load from a clamped, valid
+  // address (with a select for values that must be zero): branches around
+  // loads make the compiler wait for all outstanding memory operations
+  // (stores included) before them and move them to the loop latch.
+  const T* __restrict__ row2s = load2 ? row2 : row1;
+  R4 n1, n2;
   auto issue_tile_loads = [&](int tile) {
     const int t = tile * kTileB + a_col;
-    nu = load_raw4<T, kAligned>(u_row, t, L, a_ok);
-    nd = load_raw4<T, kAligned>(d_row, t, L, a_ok);
-    ny = load_raw4<T, kAligned>(y_row, t, L, a_ok);
-    if constexpr (kHasZ) nz = load_raw4<T, kAligned>(z_row, t, L, a_ok);
+    n1 = load_raw4<T, kAligned>(row1, t, L, a_ok);
+    n2 = load_raw4<T, kAligned>(row2s, t, L, a_ok);
   };
   // state saved by the forward just before a tile (per group and state)
+  const int chc = min(ch, Dm - 1);
   auto load_hc = [&](int tile, float (&hc)[kSG][2]) {
 #pragma unroll
     for (int g = 0; g < kSG; ++g)
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const int n = (g * kWaves + w) * 2 + s;
-        float v = 0.0f;
-        if (ch_ok && n < N) {
-          if (tile > 0) v = h_chunks[(((size_t)b * p.nchunks + (tile - 1)) * N + n) * Dm + ch];
-          else if (h_init) v = h_init[(rb + ch) * N + n];
-        }
-        hc[g][s] = v;
+        const int nc = min(n, N - 1);
+        const float* src = tile > 0
+            ? h_chunks + (((size_t)b * p.nchunks + (tile - 1)) * N + nc) * Dm + chc
+            : (h_init ? h_init + (rb + chc) * N + nc : h_chunks);
+        const float v = *src;
+        hc[g][s] = (ch_ok && n < N && (tile > 0 || h_init)) ? v : 0.0f;
       }
   };
   // thread -> one float4 of the tile's B/C block (pair G, step i)
   const int bc_G = tid / kTileB;
   const int bc_i = tid % kTileB;
   const bool bc_act = bc_G < ngroups;
-  float4 nbc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  const int bc_Gc = min(bc_G, ngroups - 1);
+  float4 nbc;
   auto load_bc_tile = [&](int tile) {
-    if (bc_act)
-      nbc = reinterpret_cast<const float4*>(bc)[((size_t)b * ngroups + bc_G) * Lp + tile * kTileB + bc_i];
+    nbc = reinterpret_cast<const float4*>(bc)[((size_t)b * ngroups + bc_Gc) * Lp + tile * kTileB + bc_i];
   };
   issue_tile_loads(ntiles - 1);
   load_bc_tile(ntiles - 1);
   float hcn[kSG][2];
   load_hc(ntiles - 1, hcn);
 
-  float* const wGB = sGB + w * kSlice;
-  float* const wDD = sDD + w * kSlice;
-  float* const wY = sY + (kHasZ ? w * kSlice : 0);
-
   for (int tile = ntiles - 1; tile >= 0; --tile) {
     const int t0 = tile * kTileB;
+    const int par = tile & 1;
     float hc[kSG][2];
 #pragma unroll
     for (int g = 0; g < kSG; ++g) hc[g][0] = hcn[g][0], hc[g][1] = hcn[g][1];
     // ---- phase A: stage per-position quantities
-    float dzf[4];  // dy_masked * silu'(z), times out in phase C
+    float dzf[4];  // group 1: dy_masked * silu'(z), times out in phase C
     {
-      float uv[4], dv[4], yv[4], zv[4], de[4], du[4], dov[4], xv[4];
-      decode4(nu, uv);
-      decode4(nd, dv);
-      decode4(ny, yv);
-      if constexpr (kHasZ) decode4(nz, zv);
+      float v1[4], v2[4];
+      decode4(n1, v1);
+      if (load2) decode4(n2, v2);
+      if (!grp1) {  // u = v1, delta_raw = v2
+        float de[4], du[4], sg[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float x = dv[j] + Bias;
-        const float dt = softplus ? softplus_t20(x) : x;
-        const int tt = t0 + a_col + j;
-        const bool valid = tt >= vlo && tt < vhi;
-        de[j] = valid ? dt : 0.0f;
-        du[j] = de[j] * uv[j];
-        const float dym = valid ? yv[j] : 0.0f;
-        if constexpr (kHasZ) {
-          dov[j] = dym * silu_f(zv[j]);
-          dzf[j] = dym * silu_grad_f(zv[j]);
-        } else {
-          dov[j] = dym;
-          dzf[j] = 0.0f;
+        for (int j = 0; j < 4; ++j) {
+          const float x = v2[j] + Bias;
+          float dt = x, g = 1.0f;
+          if (softplus) softplus_and_grad_t20(x, dt, g);
+          const int tt = t0 + a_col + j;
+          const bool valid = tt >= vlo && tt < vhi;
+          de[j] = valid ? dt : 0.0f;
+          du[j] = de[j] * v1[j];
+          sg[j] = valid ? g : 0.0f;
         }
-        xv[j] = x;
+        sDelta[a_q][a_sw] = make_float4(de[0], de[1], de[2], de[3]);
+        sDu[a_q][a_sw] = make_float4(du[0], du[1], du[2], du[3]);
+        sU[par][a_q][a_sw] = make_float4(v1[0], v1[1], v1[2], v1[3]);
+        sSg[a_q][a_sw] = make_float4(sg[0], sg[1], sg[2], sg[3]);
+      } else {  // dy = v1, z = v2
+        float dov[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tt = t0 + a_col + j;
+          const bool valid = tt >= vlo && tt < vhi;
+          const float dym = valid ? v1[j] : 0.0f;
+          if constexpr (kHasZ) {
+            const float sz = sigmoidf_fast(v2[j]);
+            dov[j] = dym * (v2[j] * sz);
+            dzf[j] = dym * (sz * fmaf(v2[j], 1.0f - sz, 1.0f));
+          } else {
+            dov[j] = dym;
+            dzf[j] = 0.0f;
+          }
+        }
+        sDout[par][a_q][a_sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
       }
       if (bc_act) sBC[bc_G][bc_i] = nbc;
-      if (a_act) {
-        sDelta[a_q][a_row] = make_float4(de[0], de[1], de[2], de[3]);
-        sDu[a_q][a_row] = make_float4(du[0], du[1], du[2], du[3]);
-        sDout[a_q][a_row] = make_float4(dov[0], dov[1], dov[2], dov[3]);
-        sU[a_q][a_row] = make_float4(uv[0], uv[1], uv[2], uv[3]);
-        sX[a_q][a_row] = make_float4(xv[0], xv[1], xv[2], xv[3]);
-      }
     }
     __syncthreads();
-    if (tile > 0) {  // the previous tile's rows, B/C and saved state stream in meanwhile
-      issue_tile_loads(tile - 1);
-      load_bc_tile(tile - 1);
-      load_hc(tile - 1, hcn);
+    {  // the previous tile's rows, B/C and saved state stream in meanwhile
+       // (at tile 0 the tile itself is re-read, unused)
+      const int tp = max(tile - 1, 0);
+      issue_tile_loads(tp);
+      load_bc_tile(tp);
+      load_hc(tp, hcn);
+      sched_fence();
     }
 
     // ---- phase B
@@ -272,9 +299,9 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
           const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
           for (int q = 0; q < kT4; ++q) {
-            *reinterpret_cast<float4*>(wGB + lane * kStr + 4 * q) = zero;
-            *reinterpret_cast<float4*>(wDD + lane * kStr + 4 * q) = zero;
-            if constexpr (kHasZ) *reinterpret_cast<float4*>(wY + lane * kStr + 4 * q) = zero;
+            sGB[w][q][lane] = zero;
+            sDD[w][q][lane] = zero;
+            if constexpr (kHasZ) sY[w][q][lane] = zero;
           }
         }
         continue;
@@ -284,30 +311,31 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       StepVals X, Y;
       BC2 bX, bY;
       // slice update: the first group writes, later groups add
-      auto put4 = [&](float* slice, int q, const float (&v)[4]) {
-        float4* dst = reinterpret_cast<float4*>(slice + lane * kStr + 4 * q);
+      auto put4 = [&](float4 (&slice)[kT4][kBlockCh], int q, const float (&v)[4]) {
+        float4& dst = slice[q][lane ^ bcol_swz(q)];
         if (g == 0) {
-          *dst = make_float4(v[0], v[1], v[2], v[3]);
+          dst = make_float4(v[0], v[1], v[2], v[3]);
         } else {
-          float4 o = *dst;
-          *dst = make_float4(o.x + v[0], o.y + v[1], o.z + v[2], o.w + v[3]);
+          const float4 o = dst;
+          dst = make_float4(o.x + v[0], o.y + v[1], o.z + v[2], o.w + v[3]);
         }
       };
       auto fwd = [&](int jq, const StepVals& sv, const BC2& v) {
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         bwd_recompute_block(jq, sv, v, A2[g], hc[g], a, H, y);
-        if constexpr (kHasZ) put4(wY, jq, y);
+        if constexpr (kHasZ) put4(sY[w], jq, y);
       };
       auto rev = [&](int jq, const StepVals& sv, const BC2& v) {
         float gB[4], gD[4];
         bwd_reverse_block(jq, sv, v, Av[g], hc[g], a, H, gam[g], dA[g], vals, gB, gD);
-        put4(wGB, jq, gB);
-        put4(wDD, jq, gD);
+        put4(sGB[w], jq, gB);
+        put4(sDD[w], jq, gD);
       };
       auto ld = [&](int jq, StepVals& sv, BC2& v, bool with_dout) {
-        sv.dl = sDelta[jq][lane];
-        sv.du = sDu[jq][lane];
-        if (with_dout) sv.dout = sDout[jq][lane];
+        const int li = lane ^ bcol_swz(jq);
+        sv.dl = sDelta[jq][li];
+        sv.du = sDu[jq][li];
+        if (with_dout) sv.dout = sDout[par][jq][li];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {  // broadcast reads (same address in every lane)
           const float4 q = sBC[G][4 * jq + j];
@@ -339,51 +367,51 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     __syncthreads();
 
     // ---- phase C: per-position gradients
-    if (a_act) {
-      const int li = a_row * kStr + a_col;
-      float4 gb = *reinterpret_cast<const float4*>(sGB + li);
-      float4 gd = *reinterpret_cast<const float4*>(sDD + li);
-      float4 ys = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if constexpr (kHasZ) ys = *reinterpret_cast<const float4*>(sY + li);
+    if (!grp1) {
+      float4 gb = sGB[0][a_q][a_sw];
+      float4 gd = sDD[0][a_q][a_sw];
 #pragma unroll
       for (int ww = 1; ww < kWaves; ++ww) {
-        const float4 v1 = *reinterpret_cast<const float4*>(sGB + ww * kSlice + li);
-        const float4 v2 = *reinterpret_cast<const float4*>(sDD + ww * kSlice + li);
+        const float4 v1 = sGB[ww][a_q][a_sw];
+        const float4 v2 = sDD[ww][a_q][a_sw];
         gb.x += v1.x; gb.y += v1.y; gb.z += v1.z; gb.w += v1.w;
         gd.x += v2.x; gd.y += v2.y; gd.z += v2.z; gd.w += v2.w;
-        if constexpr (kHasZ) {
-          const float4 v3 = *reinterpret_cast<const float4*>(sY + ww * kSlice + li);
-          ys.x += v3.x; ys.y += v3.y; ys.z += v3.z; ys.w += v3.w;
-        }
       }
       const float gbv[4] = {gb.x, gb.y, gb.z, gb.w};
       const float gdv[4] = {gd.x, gd.y, gd.z, gd.w};
-      const float ysv[4] = {ys.x, ys.y, ys.z, ys.w};
-      float de[4], uu[4], dov[4], xv[4];
-      f4_to(sDelta[a_q][a_row], de);
-      f4_to(sU[a_q][a_row], uu);
-      f4_to(sDout[a_q][a_row], dov);
-      f4_to(sX[a_q][a_row], xv);
-      float duo[4], ddo[4], dzo[4];
+      float de[4], uu[4], dov[4], sg[4];
+      f4_to(sDelta[a_q][a_sw], de);
+      f4_to(sU[par][a_q][a_sw], uu);
+      f4_to(sDout[par][a_q][a_sw], dov);
+      f4_to(sSg[a_q][a_sw], sg);
+      float duo[4], ddo[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int tt = t0 + a_col + j;
-        const bool valid = tt >= vlo && tt < vhi;
-        const float ddl = fmaf(uu[j], gbv[j], gdv[j]);
-        const float dsp = softplus ? softplus_grad_t20(xv[j]) : 1.0f;
-        const float dd = valid ? ddl * dsp : 0.0f;
+        const float dd = fmaf(uu[j], gbv[j], gdv[j]) * sg[j];  // sg is 0 at padded steps
         duo[j] = fmaf(Dv, dov[j], de[j] * gbv[j]);
         ddo[j] = dd;
         accD = fmaf(dov[j], uu[j], accD);
         accB += dd;
-        if constexpr (kHasZ) dzo[j] = dzf[j] * fmaf(Dv, uu[j], ysv[j]);
       }
       const int t = t0 + a_col;
       if (a_ok && t < L) {
         store4<T, kAligned>(dup + (rb + a_ch) * L, t, L, duo);
         store4<T, kAligned>(ddp + (rb + a_ch) * L, t, L, ddo);
-        if constexpr (kHasZ) store4<T, kAligned>(dzp + (rb + a_ch) * L, t, L, dzo);
       }
+    } else if constexpr (kHasZ) {
+      float4 ys = sY[0][a_q][a_sw];
+#pragma unroll
+      for (int ww = 1; ww < kWaves; ++ww) {
+        const float4 v3 = sY[ww][a_q][a_sw];
+        ys.x += v3.x; ys.y += v3.y; ys.z += v3.z; ys.w += v3.w;
+      }
+      const float ysv[4] = {ys.x, ys.y, ys.z, ys.w};
+      float uu[4], dzo[4];
+      f4_to(sU[par][a_q][a_sw], uu);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dzo[j] = dzf[j] * fmaf(Dv, uu[j], ysv[j]);
+      const int t = t0 + a_col;
+      if (a_ok && t < L) store4<T, kAligned>(dzp + (rb + a_ch) * L, t, L, dzo);
     }
     // the next tile's phase B overwrites the slices only after the barrier
     // that ends its phase A, so no barrier is needed here
@@ -400,12 +428,14 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         if (dh_init) dh_init[(rb + ch) * N + n] = gam[g][s];
       }
     }
-  // the 4 items of a channel row are 4 consecutive lanes
-  const float sd = group_sum<kT4>(accD);
-  const float sb = group_sum<kT4>(accB);
-  if (a_ok && a_q == 0) {
-    ws_D[rb + a_ch] = sd;
-    ws_bias[rb + a_ch] = sb;
+  // the 4 items of a channel row are 4 consecutive lanes of group 0
+  if (!grp1) {
+    const float sd = group_sum<kT4>(accD);
+    const float sb = group_sum<kT4>(accB);
+    if (a_ok && a_q == 0) {
+      ws_D[rb + a_ch] = sd;
+      ws_bias[rb + a_ch] = sb;
+    }
   }
 }
 

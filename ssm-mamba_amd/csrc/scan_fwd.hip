@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
     const float* __restrict__ Dp, const float* __restrict__ biasp,
     const float* __restrict__ h_init, const int64_t* __restrict__ length,
     const T* __restrict__ zp, T* __restrict__ out, float* __restrict__ h_chunks,
-    float* __restrict__ h_last) {
+    float* __restrict__ h_last, void* __restrict__ dummy) {
   using R4 = typename Raw4<T>::type;
   constexpr int kT4 = kTileF / 4;        // 4-step columns per sub-tile
   constexpr int kSup = kSubF * kTileF;   // steps staged per super-tile
@@ -155,11 +155,15 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   const bool a_ok = a_ch < Dm;
   const float Dv = (a_ok && Dp) ? Dp[a_ch] : 0.0f;
   const float Bias = (a_ok && biasp) ? biasp[a_ch] : 0.0f;
-  const T* __restrict__ u_row = u + (rb + a_ch) * L;
-  const T* __restrict__ d_row = dl + (rb + a_ch) * L;
-  const T* __restrict__ z_row = zp + (rb + a_ch) * L;
+  // rows of the clamped channel (always valid addresses; loads of rows past
+  // the last channel are zeroed)
+  const int a_chc = min(a_ch, Dm - 1);
+  const T* __restrict__ u_row = u + (rb + a_chc) * L;
+  const T* __restrict__ d_row = dl + (rb + a_chc) * L;
+  const T* __restrict__ z_row = zp + (rb + a_chc) * L;
   const bool softplus = p.softplus != 0;
   const bool save = h_chunks != nullptr;
+  float* const dummyf = static_cast<float*>(dummy);
 
   // Raw row pieces of the next super-tile, all loads issued at once right
   // after the current super-tile's phase A.  They are consumed together at
@@ -178,9 +182,9 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
 #pragma unroll
     for (int i = 0; i < kSubF; ++i) {
       const int t = min(T0 + i * kTileF, last_t0) + a_col;
-      qu[i] = load_raw4<T, kAligned>(u_row, t, L, a_ok);
-      qd[i] = load_raw4<T, kAligned>(d_row, t, L, a_ok);
-      if constexpr (kHasZ) qz[i] = load_raw4<T, kAligned>(z_row, t, L, a_ok);
+      qu[i] = load_raw4_nb<T, kAligned>(u_row, t, L, a_ok);
+      qd[i] = load_raw4_nb<T, kAligned>(d_row, t, L, a_ok);
+      if constexpr (kHasZ) qz[i] = load_raw4_nb<T, kAligned>(z_row, t, L, a_ok);
       else qz[i] = R4{};
     }
     if constexpr (kSG == 1) {
@@ -198,16 +202,25 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       }
     }
   };
-  issue(0);
 
-  for (int T0 = 0; T0 < L; T0 += kSup) {
-    // ---- phase A: softplus once per element, stage delta and delta*u for
-    // the whole super-tile; D*u and silu(z) are kept for phase C.
-    float skip[kSubF][4], gate[kSubF][4];
+  // kFull (whole super-tile inside the sequence, kSG == 1): the steady
+  // state, with no branches around memory operations, so the compiler's
+  // waits for the prefetched rows count exactly what is needed.  Otherwise
+  // the general code (last super-tile, N > 16).
+  //
+  // The loop is rotated: a super-tile's phase A runs at the end of the
+  // previous iteration, so the wait for its rows sits in the same iteration
+  // as their loads and the stores issued after them (no loop-header merge in
+  // between that would make the compiler wait for those stores too).
+  float skip[kSubF][4], gate[kSubF][4];  // phase A -> phase C: D*u, silu(z)
+  // ---- phase A: softplus once per element, stage delta and delta*u for
+  // the whole super-tile; D*u and silu(z) are kept for phase C.
+  auto phase_a = [&](const int T0, auto full_tag) {
+    constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
     for (int i = 0; i < kSubF; ++i) {
       const int t0 = T0 + i * kTileF;
-      if (t0 < L) {
+      if (kFull || t0 < L) {
         float uv[4], dv[4], de[4], du[4];
         decode4(qu[i], uv);
         decode4(qd[i], dv);
@@ -232,19 +245,28 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       }
     }
     if constexpr (kSG == 1) {
+      // pairs past the last one get zero B and C, so their waves run the
+      // common path and contribute nothing
 #pragma unroll
       for (int r = 0; r < kBCPer; ++r) {
         const int item = r * kThreads + tid;
-        sBC[item / (kTileF * kWaves)][(item / kTileF) % kWaves][item % kTileF] = qbc[r];
+        const int G = (item / kTileF) % kWaves;
+        sBC[item / (kTileF * kWaves)][G][item % kTileF] =
+            G < ngroups ? qbc[r] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
     }
+  };
+
+  // ---- phases B and C of the super-tile staged by the last phase A
+  auto body = [&](const int T0, auto full_tag) {
+    constexpr bool kFull = decltype(full_tag)::value;
     __syncthreads();
     issue(T0 + kSup);
 
 #pragma unroll
     for (int i = 0; i < kSubF; ++i) {
       const int t0 = T0 + i * kTileF;
-      if (t0 >= L) break;
+      if (!kFull && t0 >= L) break;
       const float4* __restrict__ cDelta = sDelta[i * kT4];
       const float4* __restrict__ cDu = sDu[i * kT4];
       // ---- phase B over sub-tile i
@@ -264,7 +286,38 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
             }
         }
       };
-      if constexpr (kSG == 1) {
+      if constexpr (kFull) {
+        // every wave: full sub-tile, fully unrolled, static B/C offsets and
+        // buffers; carries after blocks 3 and 7 (masked-off ones go to the
+        // dummy slot).  Block k+1's LDS loads are issued right after block
+        // k's have arrived, then block k is computed.
+        const float4* __restrict__ cBC = sBC[i][w];
+        const bool hc_ok = save && ch_ok && w < ngroups;
+        const bool hc2_ok = hc_ok && 2 * w + 1 < N;
+        float* const hc = h_chunks + (((size_t)b * p.nchunks + t0 / kChunk) * N + 2 * w) * Dm + ch;
+        BC2 bcb[2];
+        float4 dlb[2], dub[2];
+        lds_bc_block(cBC, 0, bcb[0]);
+        dlb[0] = cDelta[lane ^ col_swz(0)];
+        dub[0] = cDu[lane ^ col_swz(0)];
+#pragma unroll
+        for (int k = 0; k < kT4; ++k) {
+          const int c = k & 1;
+          if (k + 1 < kT4) {
+            dlb[c ^ 1] = cDelta[(k + 1) * kBlockCh + (lane ^ col_swz(k + 1))];
+            dub[c ^ 1] = cDu[(k + 1) * kBlockCh + (lane ^ col_swz(k + 1))];
+            lds_bc_block(cBC, 4 * (k + 1), bcb[c ^ 1]);
+          }
+          float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          fwd_block(dlb[c], dub[c], bcb[c], A2[0], h[0], y);
+          sY[w][k][lane ^ col_swz(k)] = make_float4(y[0], y[1], y[2], y[3]);
+          if ((k & 3) == 3) {
+            const size_t off = (size_t)(k / 4) * N * Dm;
+            *(hc_ok ? hc + off : dummyf) = h[0][0];
+            *(hc2_ok ? hc + off + Dm : dummyf) = h[0][1];
+          }
+        }
+      } else if constexpr (kSG == 1) {
         if (w < ngroups && nT4 == kT4) {
           // full sub-tile, fully unrolled: static B/C offsets and buffers,
           // carries after blocks 3 and 7.  Block k+1's LDS and scalar loads
@@ -361,7 +414,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       // D*u and the gate
       {
         const int t = t0 + a_col;
-        if (a_ok && t < L) {
+        if (kFull || (a_ok && t < L)) {
           float y[4];
           float4 acc = sY[0][a_q][a_sw];
 #pragma unroll
@@ -377,14 +430,32 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
 #pragma unroll
             for (int j = 0; j < 4; ++j) y[j] *= gate[i][j];
           }
-          store4<T, kAligned>(out + (rb + a_ch) * L, t, L, y);
+          if constexpr (kFull) store4_nb<T, kAligned>(out + (rb + a_ch) * L, t, L, a_ok, dummy, y);
+          else store4<T, kAligned>(out + (rb + a_ch) * L, t, L, y);
         }
       }
       // the next sub-tile's phase B rewrites the slices
-      if (i + 1 < kSubF && t0 + kTileF < L) __syncthreads();
+      if (i + 1 < kSubF && (kFull || t0 + kTileF < L)) __syncthreads();
     }
-    // the next phase A rewrites only sDelta / sDu, last read by the final
-    // phase B before the barrier that preceded the final phase C
+    // the next phase A rewrites only sDelta / sDu / sBC, last read by the
+    // final phase B before the barrier that preceded the final phase C
+  };
+
+  issue(0);
+  if (kSG == 1 && kSup <= L) phase_a(0, std::true_type{});
+  else phase_a(0, std::false_type{});
+  int T0 = 0;
+  if constexpr (kSG == 1) {
+    for (; T0 + kSup <= L; T0 += kSup) {
+      body(T0, std::true_type{});
+      const int Tn = T0 + kSup;
+      if (Tn + kSup <= L) phase_a(Tn, std::true_type{});
+      else if (Tn < L) phase_a(Tn, std::false_type{});
+    }
+  }
+  for (; T0 < L; T0 += kSup) {
+    body(T0, std::false_type{});
+    if (T0 + kSup < L) phase_a(T0 + kSup, std::false_type{});
   }
 
   if (!save && h_last && ch_ok) {
@@ -427,7 +498,8 @@ static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t 
   ProfScope prof("scan_fwd", st);
   hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(kThreads), 0, st,
                      dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias,
-                     p.h_init, p.length, (const T*)p.z, (T*)p.out, p.h_chunks, p.h_last);
+                     p.h_init, p.length, (const T*)p.z, (T*)p.out, p.h_chunks, p.h_last,
+                     p.dummy);
   return hipGetLastError();
 }
 

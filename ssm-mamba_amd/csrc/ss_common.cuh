@@ -1,4 +1,5 @@
 #include <algorithm>
+#include <type_traits>
 // Device helpers shared by the selective-scan and state-update kernels (gfx950).
 //
 // Element types: the streamed tensors (u, delta, z, out, dout, du, ddelta, dz,
@@ -101,6 +102,15 @@ __device__ __forceinline__ float sigmoidf_fast(float x) {
   return fast_rcp(1.0f + fast_exp2(-x * kLog2e));
 }
 
+// softplus and its derivative (threshold 20) from one exponential:
+// e = exp(-|x|), sigmoid(x) = x >= 0 ? 1 / (1 + e) : e / (1 + e).
+__device__ __forceinline__ void softplus_and_grad_t20(float x, float& sp, float& sg) {
+  const float e = fast_exp2(-fabsf(x) * kLog2e);
+  const float r = fast_rcp(1.0f + e);
+  sp = x > 20.0f ? x : fmaxf(x, 0.0f) + log1p_pos(e);
+  sg = x > 20.0f ? 1.0f : (x >= 0.0f ? r : e * r);
+}
+
 // d softplus/dx with the reference threshold (sigmoid below 20, 1 above).
 __device__ __forceinline__ float softplus_grad_t20(float x) {
   return x > 20.0f ? 1.0f : sigmoidf_fast(x);
@@ -158,6 +168,31 @@ __device__ __forceinline__ void wave_reduce_scatter(float (&v)[K], int lane) {
   for (int i = 0; i < K / 32; ++i) v[i] = rs_fold<kDppQuadXor2>(v[i], v[i + K / 32], b1);
 #pragma unroll
   for (int i = 0; i < K / 64; ++i) v[i] = rs_fold<kDppQuadXor1>(v[i], v[i + K / 64], b0);
+}
+
+// Sum over the 64 lanes of 16 values per lane: afterwards v[0] of lane l
+// holds the total of value index l >> 2 (the four lanes of a quad hold the
+// same total).  Four reduce-scatter levels (lane bits 5..2) then two
+// all-reduce levels inside the quad; ~2.2 VALU per input value.
+__device__ __forceinline__ void wave_reduce16(float (&v)[16], int lane) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]),
+                                              false, false);
+    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]),
+                                              false, false);
+    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  const bool b3 = lane & 8, b2 = lane & 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) v[i] = rs_fold<kDppRowRor8>(v[i], v[i + 2], b3);
+  v[0] = rs_fold<kDppRowHalfMirror>(v[0], v[1], b2);
+  v[0] += dpp_mov<kDppQuadXor1>(v[0]);
+  v[0] += dpp_mov<kDppQuadXor2>(v[0]);
 }
 
 // Sum over groups of kW consecutive lanes (kW power of two <= 64); every lane

@@ -99,6 +99,50 @@ __device__ __forceinline__ void decode4(const uint2 r, float (&v)[4]) {
   v[0] = bf16_lo(r.x); v[1] = bf16_hi(r.x); v[2] = bf16_lo(r.y); v[3] = bf16_hi(r.y);
 }
 
+// Branch-free variants for the kernels' steady-state loops.  A branch around
+// a memory operation leaves a path without it, and the compiler then waits for
+// every outstanding load and store wherever it needs a loaded value; without
+// branches it can wait for exactly the loads it needs.
+//  load_raw4_nb: the row pointer must be valid (callers clamp the channel)
+//    and the step is clamped into the row; past the row end or the last
+//    channel the value is other data of the same tensor, which the callers
+//    mask (padded steps get delta = 0 and dout = 0) or never store.  No
+//    select on the loaded value: it would make the compiler wait for the
+//    load right where it is issued.
+//  store4_nb: lanes with !(ok && t < L) write to `dummy` (16 bytes, aligned,
+//    never read) instead.
+// The unaligned path keeps per-element bounds branches.
+template <typename T, bool kAligned>
+__device__ __forceinline__ typename Raw4<T>::type load_raw4_nb(const T* __restrict__ row, int t, int L,
+                                                               bool ok) {
+  using R = typename Raw4<T>::type;
+  if constexpr (kAligned) {
+    (void)ok;
+    return *reinterpret_cast<const R*>(row + min(t, L - 4));
+  } else {
+    return load_raw4<T, false>(row, t, L, ok);
+  }
+}
+
+template <typename T, bool kAligned>
+__device__ __forceinline__ void store4_nb(T* __restrict__ row, int t, int L, bool ok,
+                                          void* __restrict__ dummy, const float (&v)[4]) {
+  if constexpr (kAligned) {
+    T* dst = (ok && t < L) ? row + t : static_cast<T*>(dummy);
+    if constexpr (sizeof(T) == 4) {
+      *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+  } else {
+    if (ok) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (t + j < L) Elem<T>::store1(row + t + j, v[j]);
+    }
+  }
+}
+
 template <typename T, bool kAligned>
 __device__ __forceinline__ void store4(T* __restrict__ row, int t, int L, const float (&v)[4]) {
   if constexpr (kAligned) {

@@ -68,7 +68,13 @@ struct ScanParams {
   void* dC;
   float* dD;      // nullable
   float* dbias;   // nullable
+
+  // 256 bytes of workspace that masked-off lanes store to (never read), so
+  // the kernels' steady-state stores need no branches
+  void* dummy;
 };
+
+constexpr size_t kDummyBytes = 256;
 
 struct UpdateParams {
   int batch, dim, nstate, softplus;

@@ -32,8 +32,9 @@ def test_queries():
     assert lib.ssm_abi_version() == N.ABI_VERSION
     assert [lib.ssm_scan_nchunks(x) for x in (0, 1, 16, 17, 2048)] == [0, 1, 1, 2, 128]
     # fwd workspace: prepped B/C, fp32, rows padded to 16 steps, states padded to 4
-    assert lib.ssm_scan_fwd_workspace_bytes(8, 2048, 2048, 16) == 8 * 4 * 2048 * 8 * 4
-    assert lib.ssm_scan_fwd_workspace_bytes(1, 64, 5, 3) == 512  # 1 group x 16 steps x 8 floats
+    # prepped B/C (batch x pairs x padded steps x 4 floats) + a 256-byte store sink
+    assert lib.ssm_scan_fwd_workspace_bytes(8, 2048, 2048, 16) == 8 * 4 * 2048 * 8 * 4 + 256
+    assert lib.ssm_scan_fwd_workspace_bytes(1, 64, 5, 3) == 512 + 256  # 2 pairs x 16 steps x 4 floats
     assert lib.ssm_scan_bwd_workspace_bytes(8, 2048, 2048, 16) > 2 * 32 * 8 * 16 * 2048 * 4
 
 
