@@ -40,6 +40,14 @@ struct StepVals {  // per-position LDS values of one 4-step block
   float4 dl, du, dout;
 };
 
+// The reverse recurrence needs the decays a_t of the tile: keep the 32 values
+// from the recompute in registers, or recompute them (one mul and one exp per
+// state and step) and save the registers.
+#ifndef SSM_BWD_RECOMPUTE_DECAY
+#define SSM_BWD_RECOMPUTE_DECAY 0
+#endif
+constexpr bool kRecomputeDecay = SSM_BWD_RECOMPUTE_DECAY != 0;
+
 // Recompute one 4-step block: decays a and states H for the wave's 2 states.
 __device__ __forceinline__ void bwd_recompute_block(int jq, const StepVals& sv, const BC2& v,
                                                     const float (&A2)[2], const float (&Hc)[2],
@@ -52,20 +60,24 @@ __device__ __forceinline__ void bwd_recompute_block(int jq, const StepVals& sv, 
     const int i = 4 * jq + j;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      a[s][i] = fast_exp2(dlv[j] * A2[s]);
+      const float at = fast_exp2(dlv[j] * A2[s]);
+      if constexpr (!kRecomputeDecay) a[s][i] = at;
       const float hp = i ? H[s][i - 1] : Hc[s];
-      H[s][i] = fmaf(a[s][i], hp, duv[j] * v.B(j, s));
+      H[s][i] = fmaf(at, hp, duv[j] * v.B(j, s));
       y[j] = fmaf(v.C(j, s), H[s][i], y[j]);
     }
   }
 }
 
-// Reverse recurrence over one 4-step block (steps 4jq+3 .. 4jq).
+// Reverse recurrence over one 4-step block (steps 4jq+3 .. 4jq).  vals gets
+// the block's per-channel terms of dB (index s*4 + j) and dC (8 + s*4 + j),
+// to be summed over the 64 channels of the wave.
 __device__ __forceinline__ void bwd_reverse_block(int jq, const StepVals& sv, const BC2& v,
-                                                  const float (&Av)[2], const float (&Hc)[2],
+                                                  const float (&Av)[2], const float (&A2)[2],
+                                                  const float (&Hc)[2],
                                                   const float (&a)[2][kChunk],
                                                   const float (&H)[2][kChunk], float (&gam)[2],
-                                                  float (&dA)[2], float (&vals)[4 * kChunk],
+                                                  float (&dA)[2], float (&vals)[16],
                                                   float (&gB)[4], float (&gD)[4]) {
   const float dlv[4] = {sv.dl.x, sv.dl.y, sv.dl.z, sv.dl.w};
   const float duv[4] = {sv.du.x, sv.du.y, sv.du.z, sv.du.w};
@@ -79,12 +91,13 @@ __device__ __forceinline__ void bwd_reverse_block(int jq, const StepVals& sv, co
       const float Gt = fmaf(dov[j], v.C(j, s), gam[s]);
       sB = fmaf(Gt, v.B(j, s), sB);
       const float hp = i ? H[s][i - 1] : Hc[s];
-      const float ng = a[s][i] * Gt;  // gamma_{t-1}
+      const float at = kRecomputeDecay ? fast_exp2(dlv[j] * A2[s]) : a[s][i];
+      const float ng = at * Gt;  // gamma_{t-1}
       const float q = ng * hp;        // G_t a_t h_{t-1}
       sD = fmaf(Av[s], q, sD);
       dA[s] = fmaf(dlv[j], q, dA[s]);
-      vals[s * kChunk + i] = Gt * duv[j];               // dB partial
-      vals[2 * kChunk + s * kChunk + i] = dov[j] * H[s][i];  // dC partial
+      vals[s * 4 + j] = Gt * duv[j];            // dB term
+      vals[8 + s * 4 + j] = dov[j] * H[s][i];   // dC term
       gam[s] = ng;
     }
     gB[j] = sB;
@@ -111,7 +124,8 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const T* __restrict__ zp, const float* __restrict__ h_chunks, const T* __restrict__ dyp,
     const float* __restrict__ dh_last, T* __restrict__ dup, T* __restrict__ ddp,
     T* __restrict__ dzp, float* __restrict__ dh_init, float* __restrict__ ws_bc,
-    float* __restrict__ ws_A, float* __restrict__ ws_D, float* __restrict__ ws_bias) {
+    float* __restrict__ ws_A, float* __restrict__ ws_D, float* __restrict__ ws_bias,
+    void* __restrict__ dummy) {
   using R4 = typename Raw4<T>::type;
   constexpr int kT4 = kTileB / 4;         // 4-step columns per tile (4)
   constexpr int kItems = kBlockCh * kT4;  // (row, column) items per tile (256)
@@ -122,18 +136,19 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
 
   __shared__ float4 sDelta[kT4][kBlockCh];  // delta (0 at padded steps)
   __shared__ float4 sDu[kT4][kBlockCh];     // delta * u
+  __shared__ float4 sSg[kT4][kBlockCh];     // softplus'(x) (0 at padded steps)
   // sDout and sU are written in phase A by one thread group and read in
   // phase C by the other, with no barrier between a tile's phase C and the
   // next tile's phase A: they alternate between two buffers by tile parity
   __shared__ float4 sDout[2][kT4][kBlockCh];  // masked dout (after the z gate)
   __shared__ float4 sU[2][kT4][kBlockCh];
-  __shared__ float4 sSg[kT4][kBlockCh];     // softplus'(x) (0 at padded steps)
   // one slice per wave of the per-position sums over that wave's states,
   // added in a fixed order in phase C (deterministic result)
   __shared__ float4 sGB[kWaves][kT4][kBlockCh];  // sum_n G B
   __shared__ float4 sDD[kWaves][kT4][kBlockCh];  // sum_n A G a h_{t-1}
   __shared__ float4 sY[kHasZ ? kWaves : 1][kT4][kBlockCh];  // sum_n C h
-  // the tile's prepped B/C rows of every state pair: [G][step][s][B, C]
+  // the tile's prepped B/C rows of every state pair (zero past the last
+  // pair): [G][step][s][B, C]
   __shared__ float4 sBC[kMaxPairs][kTileB];
 
   const int tid = threadIdx.x;
@@ -147,6 +162,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   const int Lp = bc_row_len(L);
   const size_t rb = (size_t)b * Dm;
   const size_t nBC = (size_t)p.batch * N * L;
+  float* const dummyf = static_cast<float*>(dummy);
 
   int vlo, vhi;
   valid_window(length, p.pad_right, b, L, vlo, vhi);
@@ -180,134 +196,111 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   const int a_sw = a_row ^ bcol_swz(a_q);
   const int a_ch = d0 + a_row;
   const bool a_ok = a_ch < Dm;
+  const int a_chc = min(a_ch, Dm - 1);
   const float Dv = (a_ok && Dp) ? Dp[a_ch] : 0.0f;
   const float Bias = (a_ok && biasp) ? biasp[a_ch] : 0.0f;
-  const T* __restrict__ row1 = (grp1 ? dyp : u) + (rb + a_ch) * L;
-  const T* __restrict__ row2 = (grp1 ? zp : dl) + (rb + a_ch) * L;
   const bool load2 = !grp1 || kHasZ;
+  const T* __restrict__ row1 = (grp1 ? dyp : u) + (rb + a_chc) * L;
+  const T* __restrict__ row2 = load2 ? (grp1 ? zp : dl) + (rb + a_chc) * L : row1;
   const bool softplus = p.softplus != 0;
   float accD = 0.0f, accB = 0.0f;
 
-  const int ntiles = (L + kTileB - 1) / kTileB;
-  // raw rows of the next tile to process (walking backwards), in flight
-  // Every prefetch below is an unconditional load from a clamped, valid
-  // address (with a select for values that must be zero): branches around
-  // loads make the compiler wait for all outstanding memory operations
-  // (stores included) before them and move them to the loop latch.
-  const T* __restrict__ row2s = load2 ? row2 : row1;
-  R4 n1, n2;
-  auto issue_tile_loads = [&](int tile) {
-    const int t = tile * kTileB + a_col;
-    n1 = load_raw4<T, kAligned>(row1, t, L, a_ok);
-    n2 = load_raw4<T, kAligned>(row2s, t, L, a_ok);
-  };
-  // state saved by the forward just before a tile (per group and state)
+  // Prefetch of a tile's inputs.  Every load is unconditional from a
+  // clamped, valid address (masks are applied where the values are used):
+  // a branch around a load, or a select on a value right after it, makes the
+  // compiler wait for outstanding memory operations there.
+  R4 n1, n2;            // raw row pieces (group 0: u, delta; group 1: dout, z)
+  float4 nbc;           // one float4 of the tile's B/C block (pair bc_G, step bc_i)
+  float hcn[kSG][2];    // states saved by the forward before the tile
+  const int bc_G = tid / kTileB;
+  const int bc_i = tid % kTileB;
+  const bool bc_act = bc_G < kMaxPairs;
+  const int bc_Gc = min(bc_G, ngroups - 1);
   const int chc = min(ch, Dm - 1);
-  auto load_hc = [&](int tile, float (&hc)[kSG][2]) {
+  auto issue = [&](int tile) {
+    const int t = tile * kTileB + a_col;
+    n1 = load_raw4_nb<T, kAligned>(row1, t, L, a_ok);
+    n2 = load_raw4_nb<T, kAligned>(row2, t, L, a_ok);
+    nbc = reinterpret_cast<const float4*>(bc)[((size_t)b * ngroups + bc_Gc) * Lp + tile * kTileB + bc_i];
+#pragma unroll
+    for (int g = 0; g < kSG; ++g)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int nc = min((g * kWaves + w) * 2 + s, N - 1);
+        const float* src = tile > 0
+            ? h_chunks + (((size_t)b * p.nchunks + (tile - 1)) * N + nc) * Dm + chc
+            : (h_init ? h_init + (rb + chc) * N + nc : h_chunks);
+        hcn[g][s] = *src;
+      }
+  };
+
+  float hc[kSG][2];
+  float dzf[4];  // group 1: dy_masked * silu'(z), times out in phase C
+  // ---- phase A: stage a tile's per-position quantities and B/C in LDS, and
+  // take its saved states
+  auto phase_a = [&](const int tile) {
+    const int t0 = tile * kTileB;
+    const int par = tile & 1;
+    float v1[4], v2[4];
+    decode4(n1, v1);
+    decode4(n2, v2);
+    if (!grp1) {  // u = v1, delta_raw = v2
+      float de[4], du[4], sg[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float x = v2[j] + Bias;
+        float dt = x, g = 1.0f;
+        if (softplus) softplus_and_grad_t20(x, dt, g);
+        const int tt = t0 + a_col + j;
+        const bool valid = a_ok && tt >= vlo && tt < vhi;
+        de[j] = valid ? dt : 0.0f;
+        du[j] = de[j] * v1[j];
+        sg[j] = valid ? g : 0.0f;
+      }
+      sDelta[a_q][a_sw] = make_float4(de[0], de[1], de[2], de[3]);
+      sDu[a_q][a_sw] = make_float4(du[0], du[1], du[2], du[3]);
+      sU[par][a_q][a_sw] = make_float4(v1[0], v1[1], v1[2], v1[3]);
+      sSg[a_q][a_sw] = make_float4(sg[0], sg[1], sg[2], sg[3]);
+    } else {  // dy = v1, z = v2
+      float dov[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tt = t0 + a_col + j;
+        const bool valid = a_ok && tt >= vlo && tt < vhi;
+        const float dym = valid ? v1[j] : 0.0f;
+        if constexpr (kHasZ) {
+          const float sz = sigmoidf_fast(v2[j]);
+          dov[j] = dym * (v2[j] * sz);
+          dzf[j] = dym * (sz * fmaf(v2[j], 1.0f - sz, 1.0f));
+        } else {
+          dov[j] = dym;
+          dzf[j] = 0.0f;
+        }
+      }
+      sDout[par][a_q][a_sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
+    }
+    if (bc_act)
+      sBC[bc_G][bc_i] = bc_G < ngroups ? nbc : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int g = 0; g < kSG; ++g)
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const int n = (g * kWaves + w) * 2 + s;
-        const int nc = min(n, N - 1);
-        const float* src = tile > 0
-            ? h_chunks + (((size_t)b * p.nchunks + (tile - 1)) * N + nc) * Dm + chc
-            : (h_init ? h_init + (rb + chc) * N + nc : h_chunks);
-        const float v = *src;
-        hc[g][s] = (ch_ok && n < N && (tile > 0 || h_init)) ? v : 0.0f;
+        hc[g][s] = (ch_ok && n < N && (tile > 0 || h_init)) ? hcn[g][s] : 0.0f;
       }
   };
-  // thread -> one float4 of the tile's B/C block (pair G, step i)
-  const int bc_G = tid / kTileB;
-  const int bc_i = tid % kTileB;
-  const bool bc_act = bc_G < ngroups;
-  const int bc_Gc = min(bc_G, ngroups - 1);
-  float4 nbc;
-  auto load_bc_tile = [&](int tile) {
-    nbc = reinterpret_cast<const float4*>(bc)[((size_t)b * ngroups + bc_Gc) * Lp + tile * kTileB + bc_i];
-  };
-  issue_tile_loads(ntiles - 1);
-  load_bc_tile(ntiles - 1);
-  float hcn[kSG][2];
-  load_hc(ntiles - 1, hcn);
 
-  for (int tile = ntiles - 1; tile >= 0; --tile) {
+  // ---- phase B: recompute the tile's states, then the reverse recurrence
+  auto phase_b = [&](const int tile) {
     const int t0 = tile * kTileB;
     const int par = tile & 1;
-    float hc[kSG][2];
-#pragma unroll
-    for (int g = 0; g < kSG; ++g) hc[g][0] = hcn[g][0], hc[g][1] = hcn[g][1];
-    // ---- phase A: stage per-position quantities
-    float dzf[4];  // group 1: dy_masked * silu'(z), times out in phase C
-    {
-      float v1[4], v2[4];
-      decode4(n1, v1);
-      if (load2) decode4(n2, v2);
-      if (!grp1) {  // u = v1, delta_raw = v2
-        float de[4], du[4], sg[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float x = v2[j] + Bias;
-          float dt = x, g = 1.0f;
-          if (softplus) softplus_and_grad_t20(x, dt, g);
-          const int tt = t0 + a_col + j;
-          const bool valid = tt >= vlo && tt < vhi;
-          de[j] = valid ? dt : 0.0f;
-          du[j] = de[j] * v1[j];
-          sg[j] = valid ? g : 0.0f;
-        }
-        sDelta[a_q][a_sw] = make_float4(de[0], de[1], de[2], de[3]);
-        sDu[a_q][a_sw] = make_float4(du[0], du[1], du[2], du[3]);
-        sU[par][a_q][a_sw] = make_float4(v1[0], v1[1], v1[2], v1[3]);
-        sSg[a_q][a_sw] = make_float4(sg[0], sg[1], sg[2], sg[3]);
-      } else {  // dy = v1, z = v2
-        float dov[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int tt = t0 + a_col + j;
-          const bool valid = tt >= vlo && tt < vhi;
-          const float dym = valid ? v1[j] : 0.0f;
-          if constexpr (kHasZ) {
-            const float sz = sigmoidf_fast(v2[j]);
-            dov[j] = dym * (v2[j] * sz);
-            dzf[j] = dym * (sz * fmaf(v2[j], 1.0f - sz, 1.0f));
-          } else {
-            dov[j] = dym;
-            dzf[j] = 0.0f;
-          }
-        }
-        sDout[par][a_q][a_sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
-      }
-      if (bc_act) sBC[bc_G][bc_i] = nbc;
-    }
-    __syncthreads();
-    {  // the previous tile's rows, B/C and saved state stream in meanwhile
-       // (at tile 0 the tile itself is re-read, unused)
-      const int tp = max(tile - 1, 0);
-      issue_tile_loads(tp);
-      load_bc_tile(tp);
-      load_hc(tp, hcn);
-      sched_fence();
-    }
-
-    // ---- phase B
 #pragma unroll
     for (int g = 0; g < kSG; ++g) {
       const int G = g * kWaves + w;
-      if (G >= ngroups) {  // wave-uniform; a wave with no states leaves zeros
-        if (g == 0) {
-          const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-          for (int q = 0; q < kT4; ++q) {
-            sGB[w][q][lane] = zero;
-            sDD[w][q][lane] = zero;
-            if constexpr (kHasZ) sY[w][q][lane] = zero;
-          }
-        }
+      if (g > 0 && G >= ngroups) {  // wave-uniform (pair 0..7 always runs: zero B/C)
         continue;
       }
       float a[2][kChunk], H[2][kChunk];
-      float vals[4 * kChunk];
       StepVals X, Y;
       BC2 bX, bY;
       // slice update: the first group writes, later groups add
@@ -325,11 +318,21 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         bwd_recompute_block(jq, sv, v, A2[g], hc[g], a, H, y);
         if constexpr (kHasZ) put4(sY[w], jq, y);
       };
+      // the value of lane l after the reduction: index l >> 2 of the block's
+      // 16 (kind = dB/dC, state, step); quads hold the same value
+      const int vi = lane >> 2;
+      const int rkind = vi >> 3, rs = (vi >> 2) & 1, rj = vi & 3;
+      const int rn = G * 2 + rs;
+      float* const wsb = ws_bc + ((size_t)rkind * p.nblk + blk) * nBC + ((size_t)b * N + rn) * L;
       auto rev = [&](int jq, const StepVals& sv, const BC2& v) {
-        float gB[4], gD[4];
-        bwd_reverse_block(jq, sv, v, Av[g], hc[g], a, H, gam[g], dA[g], vals, gB, gD);
+        float gB[4], gD[4], vals[16];
+        bwd_reverse_block(jq, sv, v, Av[g], A2[g], hc[g], a, H, gam[g], dA[g], vals, gB, gD);
         put4(sGB[w], jq, gB);
         put4(sDD[w], jq, gD);
+        // sum over the 64 channels of this block
+        wave_reduce16(vals, lane);
+        const int t = t0 + 4 * jq + rj;
+        *((rn < N && t < L) ? wsb + t : dummyf) = vals[0];
       };
       auto ld = [&](int jq, StepVals& sv, BC2& v, bool with_dout) {
         const int li = lane ^ bcol_swz(jq);
@@ -352,30 +355,25 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       ld(2, X, bX, true); rev(2, X, bX);
       ld(1, Y, bY, true); rev(1, Y, bY);
       ld(0, X, bX, true); rev(0, X, bX);
-      // sum over the 64 channels of this block: lane l holds value index l
-      wave_reduce_scatter<4 * kChunk>(vals, lane);
-      {
-        const int kind = lane >> 5;
-        const int s = (lane >> 4) & 1;
-        const int i = lane & 15;
-        const int n = G * 2 + s;
-        const int t = t0 + i;
-        if (n < N && t < L)
-          ws_bc[((size_t)kind * p.nblk + blk) * nBC + ((size_t)b * N + n) * L + t] = vals[0];
-      }
     }
-    __syncthreads();
+  };
 
-    // ---- phase C: per-position gradients
+  // ---- phase C: per-position gradients.  Both groups issue two stores
+  // (group 1: dz and one to the dummy slot) so every path has the same
+  // memory-operation count.
+  auto phase_c = [&](const int tile) {
+    const int t0 = tile * kTileB;
+    const int par = tile & 1;
+    const int t = t0 + a_col;
     if (!grp1) {
       float4 gb = sGB[0][a_q][a_sw];
       float4 gd = sDD[0][a_q][a_sw];
 #pragma unroll
       for (int ww = 1; ww < kWaves; ++ww) {
-        const float4 v1 = sGB[ww][a_q][a_sw];
-        const float4 v2 = sDD[ww][a_q][a_sw];
-        gb.x += v1.x; gb.y += v1.y; gb.z += v1.z; gb.w += v1.w;
-        gd.x += v2.x; gd.y += v2.y; gd.z += v2.z; gd.w += v2.w;
+        const float4 q1 = sGB[ww][a_q][a_sw];
+        const float4 q2 = sDD[ww][a_q][a_sw];
+        gb.x += q1.x; gb.y += q1.y; gb.z += q1.z; gb.w += q1.w;
+        gd.x += q2.x; gd.y += q2.y; gd.z += q2.z; gd.w += q2.w;
       }
       const float gbv[4] = {gb.x, gb.y, gb.z, gb.w};
       const float gdv[4] = {gd.x, gd.y, gd.z, gd.w};
@@ -390,31 +388,46 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         const float dd = fmaf(uu[j], gbv[j], gdv[j]) * sg[j];  // sg is 0 at padded steps
         duo[j] = fmaf(Dv, dov[j], de[j] * gbv[j]);
         ddo[j] = dd;
-        accD = fmaf(dov[j], uu[j], accD);
+        accD = fmaf(dov[j], uu[j], accD);  // dov is 0 at padded steps
         accB += dd;
       }
-      const int t = t0 + a_col;
-      if (a_ok && t < L) {
-        store4<T, kAligned>(dup + (rb + a_ch) * L, t, L, duo);
-        store4<T, kAligned>(ddp + (rb + a_ch) * L, t, L, ddo);
-      }
-    } else if constexpr (kHasZ) {
-      float4 ys = sY[0][a_q][a_sw];
+      store4_nb<T, kAligned>(dup + (rb + a_ch) * L, t, L, a_ok, dummy, duo);
+      store4_nb<T, kAligned>(ddp + (rb + a_ch) * L, t, L, a_ok, dummy, ddo);
+    } else {
+      float dzo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (kHasZ) {
+        float4 ys = sY[0][a_q][a_sw];
 #pragma unroll
-      for (int ww = 1; ww < kWaves; ++ww) {
-        const float4 v3 = sY[ww][a_q][a_sw];
-        ys.x += v3.x; ys.y += v3.y; ys.z += v3.z; ys.w += v3.w;
-      }
-      const float ysv[4] = {ys.x, ys.y, ys.z, ys.w};
-      float uu[4], dzo[4];
-      f4_to(sU[par][a_q][a_sw], uu);
+        for (int ww = 1; ww < kWaves; ++ww) {
+          const float4 q3 = sY[ww][a_q][a_sw];
+          ys.x += q3.x; ys.y += q3.y; ys.z += q3.z; ys.w += q3.w;
+        }
+        const float ysv[4] = {ys.x, ys.y, ys.z, ys.w};
+        float uu[4];
+        f4_to(sU[par][a_q][a_sw], uu);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dzo[j] = dzf[j] * fmaf(Dv, uu[j], ysv[j]);
-      const int t = t0 + a_col;
-      if (a_ok && t < L) store4<T, kAligned>(dzp + (rb + a_ch) * L, t, L, dzo);
+        for (int j = 0; j < 4; ++j) dzo[j] = dzf[j] * fmaf(Dv, uu[j], ysv[j]);
+      }
+      store4_nb<T, kAligned>(dzp + (rb + a_ch) * L, t, L, kHasZ && a_ok, dummy, dzo);
+      store4_nb<T, kAligned>(dzp, t, L, false, dummy, dzo);
     }
-    // the next tile's phase B overwrites the slices only after the barrier
-    // that ends its phase A, so no barrier is needed here
+  };
+
+  // Rotated loop: a tile's phase A (which waits for its prefetched inputs)
+  // runs at the end of the previous iteration, in the same iteration as the
+  // loads and the stores issued after them, so the waits count exactly.
+  const int ntiles = (L + kTileB - 1) / kTileB;
+  issue(ntiles - 1);
+  phase_a(ntiles - 1);
+  for (int tile = ntiles - 1; tile >= 0; --tile) {
+    __syncthreads();
+    issue(max(tile - 1, 0));  // at tile 0 the tile itself is re-read, unused
+    phase_b(tile);
+    __syncthreads();
+    phase_c(tile);
+    if (tile > 0) phase_a(tile - 1);
+    // the next phase B overwrites the slices only after the barrier at the
+    // top of the next iteration
   }
 
   // ---- per-row partials
@@ -489,7 +502,7 @@ static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t 
                      dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias,
                      p.h_init, p.length, (const T*)p.z, p.h_chunks_in, (const T*)p.dout,
                      p.dh_last, (T*)p.du, (T*)p.ddelta, (T*)p.dz, p.dh_init, p.ws_bc, p.ws_A,
-                     p.ws_D, p.ws_bias);
+                     p.ws_D, p.ws_bias, p.dummy);
   return hipGetLastError();
 }
 

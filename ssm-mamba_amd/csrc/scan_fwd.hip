@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
           const float x = dv[j] + Bias;
           const float dt = softplus ? softplus_t20(x) : x;
           const int tt = t0 + a_col + j;
-          const bool valid = tt >= vlo && tt < vhi;
+          const bool valid = a_ok && tt >= vlo && tt < vhi;
           de[j] = valid ? dt : 0.0f;
           du[j] = de[j] * uv[j];
         }

@@ -106,7 +106,8 @@ __device__ __forceinline__ void decode4(const uint2 r, float (&v)[4]) {
 //  load_raw4_nb: the row pointer must be valid (callers clamp the channel)
 //    and the step is clamped into the row; past the row end or the last
 //    channel the value is other data of the same tensor, which the callers
-//    mask (padded steps get delta = 0 and dout = 0) or never store.  No
+//    must mask (steps outside the valid window or past the last channel get
+//    delta = 0 and dout = 0, so they add nothing to any sum) or never store.  No
 //    select on the loaded value: it would make the compiler wait for the
 //    load right where it is issued.
 //  store4_nb: lanes with !(ok && t < L) write to `dummy` (16 bytes, aligned,
