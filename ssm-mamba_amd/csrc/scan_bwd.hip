@@ -48,8 +48,13 @@ struct StepVals {  // per-position LDS values of one 4-step block
 #endif
 constexpr bool kRecomputeDecay = SSM_BWD_RECOMPUTE_DECAY != 0;
 
+// B/C of a 4-step block for the wave's state pair, as a block register
+// (lane l holds value l & 15 of the prepped block [j][s][B, C]).
+__device__ __forceinline__ int kB(int j, int s) { return j * 4 + s * 2; }
+__device__ __forceinline__ int kC(int j, int s) { return j * 4 + s * 2 + 1; }
+
 // Recompute one 4-step block: decays a and states H for the wave's 2 states.
-__device__ __forceinline__ void bwd_recompute_block(int jq, const StepVals& sv, const BC2& v,
+__device__ __forceinline__ void bwd_recompute_block(int jq, const StepVals& sv, float blk,
                                                     const float (&A2)[2], const float (&Hc)[2],
                                                     float (&a)[2][kChunk], float (&H)[2][kChunk],
                                                     float (&y)[4]) {
@@ -63,8 +68,8 @@ __device__ __forceinline__ void bwd_recompute_block(int jq, const StepVals& sv, 
       const float at = fast_exp2(dlv[j] * A2[s]);
       if constexpr (!kRecomputeDecay) a[s][i] = at;
       const float hp = i ? H[s][i - 1] : Hc[s];
-      H[s][i] = fmaf(at, hp, duv[j] * v.B(j, s));
-      y[j] = fmaf(v.C(j, s), H[s][i], y[j]);
+      H[s][i] = fmaf(at, hp, bc_mul(kB(j, s), blk, duv[j]));
+      y[j] = s == 0 ? bc_mul(kC(j, s), blk, H[s][i]) : bc_fmac(kC(j, s), y[j], blk, H[s][i]);
     }
   }
 }
@@ -72,7 +77,7 @@ __device__ __forceinline__ void bwd_recompute_block(int jq, const StepVals& sv, 
 // Reverse recurrence over one 4-step block (steps 4jq+3 .. 4jq).  vals gets
 // the block's per-channel terms of dB (index s*4 + j) and dC (8 + s*4 + j),
 // to be summed over the 64 channels of the wave.
-__device__ __forceinline__ void bwd_reverse_block(int jq, const StepVals& sv, const BC2& v,
+__device__ __forceinline__ void bwd_reverse_block(int jq, const StepVals& sv, float blk,
                                                   const float (&Av)[2], const float (&A2)[2],
                                                   const float (&Hc)[2],
                                                   const float (&a)[2][kChunk],
@@ -88,8 +93,8 @@ __device__ __forceinline__ void bwd_reverse_block(int jq, const StepVals& sv, co
     float sB = 0.0f, sD = 0.0f;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const float Gt = fmaf(dov[j], v.C(j, s), gam[s]);
-      sB = fmaf(Gt, v.B(j, s), sB);
+      const float Gt = bc_fmac(kC(j, s), gam[s], blk, dov[j]);  // gamma + dout C
+      sB = s == 0 ? bc_mul(kB(j, s), blk, Gt) : bc_fmac(kB(j, s), sB, blk, Gt);
       const float hp = i ? H[s][i - 1] : Hc[s];
       const float at = kRecomputeDecay ? fast_exp2(dlv[j] * A2[s]) : a[s][i];
       const float ng = at * Gt;  // gamma_{t-1}
@@ -147,9 +152,6 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   __shared__ float4 sGB[kWaves][kT4][kBlockCh];  // sum_n G B
   __shared__ float4 sDD[kWaves][kT4][kBlockCh];  // sum_n A G a h_{t-1}
   __shared__ float4 sY[kHasZ ? kWaves : 1][kT4][kBlockCh];  // sum_n C h
-  // the tile's prepped B/C rows of every state pair (zero past the last
-  // pair): [G][step][s][B, C]
-  __shared__ float4 sBC[kMaxPairs][kTileB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -159,6 +161,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   const int d0 = blk * kBlockCh;
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
   const int ngroups = (N + 1) / 2;
+  const int npair = bc_pairs(N);
   const int Lp = bc_row_len(L);
   const size_t rb = (size_t)b * Dm;
   const size_t nBC = (size_t)p.batch * N * L;
@@ -210,18 +213,20 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   // a branch around a load, or a select on a value right after it, makes the
   // compiler wait for outstanding memory operations there.
   R4 n1, n2;            // raw row pieces (group 0: u, delta; group 1: dout, z)
-  float4 nbc;           // one float4 of the tile's B/C block (pair bc_G, step bc_i)
   float hcn[kSG][2];    // states saved by the forward before the tile
-  const int bc_G = tid / kTileB;
-  const int bc_i = tid % kTileB;
-  const bool bc_act = bc_G < kMaxPairs;
-  const int bc_Gc = min(bc_G, ngroups - 1);
+  float bcn[kSG][kT4];  // the tile's B/C blocks of the wave's pairs (block registers)
   const int chc = min(ch, Dm - 1);
   auto issue = [&](int tile) {
     const int t = tile * kTileB + a_col;
     n1 = load_raw4_nb<T, kAligned>(row1, t, L, a_ok);
     n2 = load_raw4_nb<T, kAligned>(row2, t, L, a_ok);
-    nbc = reinterpret_cast<const float4*>(bc)[((size_t)b * ngroups + bc_Gc) * Lp + tile * kTileB + bc_i];
+#pragma unroll
+    for (int g = 0; g < kSG; ++g) {
+      const int Gc = min(g * kWaves + w, npair - 1);
+#pragma unroll
+      for (int jq = 0; jq < kT4; ++jq)
+        bcn[g][jq] = bc[bc_offset(b, Gc, npair, Lp, tile * kTileB + 4 * jq) + (lane & 15)];
+    }
 #pragma unroll
     for (int g = 0; g < kSG; ++g)
 #pragma unroll
@@ -235,9 +240,10 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   };
 
   float hc[kSG][2];
+  float bcc[kSG][kT4];
   float dzf[4];  // group 1: dy_masked * silu'(z), times out in phase C
-  // ---- phase A: stage a tile's per-position quantities and B/C in LDS, and
-  // take its saved states
+  // ---- phase A: stage a tile's per-position quantities in LDS and take its
+  // saved states and B/C blocks
   auto phase_a = [&](const int tile) {
     const int t0 = tile * kTileB;
     const int par = tile & 1;
@@ -279,8 +285,10 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       }
       sDout[par][a_q][a_sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
     }
-    if (bc_act)
-      sBC[bc_G][bc_i] = bc_G < ngroups ? nbc : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int g = 0; g < kSG; ++g)
+#pragma unroll
+      for (int jq = 0; jq < kT4; ++jq) bcc[g][jq] = bcn[g][jq];
 #pragma unroll
     for (int g = 0; g < kSG; ++g)
 #pragma unroll
@@ -302,7 +310,6 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       }
       float a[2][kChunk], H[2][kChunk];
       StepVals X, Y;
-      BC2 bX, bY;
       // slice update: the first group writes, later groups add
       auto put4 = [&](float4 (&slice)[kT4][kBlockCh], int q, const float (&v)[4]) {
         float4& dst = slice[q][lane ^ bcol_swz(q)];
@@ -313,9 +320,9 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
           dst = make_float4(o.x + v[0], o.y + v[1], o.z + v[2], o.w + v[3]);
         }
       };
-      auto fwd = [&](int jq, const StepVals& sv, const BC2& v) {
-        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        bwd_recompute_block(jq, sv, v, A2[g], hc[g], a, H, y);
+      auto fwd = [&](int jq, const StepVals& sv) {
+        float y[4];
+        bwd_recompute_block(jq, sv, bcc[g][jq], A2[g], hc[g], a, H, y);
         if constexpr (kHasZ) put4(sY[w], jq, y);
       };
       // the value of lane l after the reduction: index l >> 2 of the block's
@@ -324,9 +331,10 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       const int rkind = vi >> 3, rs = (vi >> 2) & 1, rj = vi & 3;
       const int rn = G * 2 + rs;
       float* const wsb = ws_bc + ((size_t)rkind * p.nblk + blk) * nBC + ((size_t)b * N + rn) * L;
-      auto rev = [&](int jq, const StepVals& sv, const BC2& v) {
+      auto rev = [&](int jq, const StepVals& sv) {
         float gB[4], gD[4], vals[16];
-        bwd_reverse_block(jq, sv, v, Av[g], A2[g], hc[g], a, H, gam[g], dA[g], vals, gB, gD);
+        bwd_reverse_block(jq, sv, bcc[g][jq], Av[g], A2[g], hc[g], a, H, gam[g], dA[g], vals, gB,
+                          gD);
         put4(sGB[w], jq, gB);
         put4(sDD[w], jq, gD);
         // sum over the 64 channels of this block
@@ -334,27 +342,22 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         const int t = t0 + 4 * jq + rj;
         *((rn < N && t < L) ? wsb + t : dummyf) = vals[0];
       };
-      auto ld = [&](int jq, StepVals& sv, BC2& v, bool with_dout) {
+      auto ld = [&](int jq, StepVals& sv, bool with_dout) {
         const int li = lane ^ bcol_swz(jq);
         sv.dl = sDelta[jq][li];
         sv.du = sDu[jq][li];
         if (with_dout) sv.dout = sDout[par][jq][li];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {  // broadcast reads (same address in every lane)
-          const float4 q = sBC[G][4 * jq + j];
-          v.v[4 * j] = q.x; v.v[4 * j + 1] = q.y; v.v[4 * j + 2] = q.z; v.v[4 * j + 3] = q.w;
-        }
       };
       // fixed schedule F0 F1 F2 F3 R3 R2 R1 R0 (recompute, then reverse); LDS
       // reads return in order, so the compiler overlaps them with the math
-      ld(0, X, bX, false); fwd(0, X, bX);
-      ld(1, Y, bY, false); fwd(1, Y, bY);
-      ld(2, X, bX, false); fwd(2, X, bX);
-      ld(3, Y, bY, true);  fwd(3, Y, bY);
-      rev(3, Y, bY);
-      ld(2, X, bX, true); rev(2, X, bX);
-      ld(1, Y, bY, true); rev(1, Y, bY);
-      ld(0, X, bX, true); rev(0, X, bX);
+      ld(0, X, false); fwd(0, X);
+      ld(1, Y, false); fwd(1, Y);
+      ld(2, X, false); fwd(2, X);
+      ld(3, Y, true);  fwd(3, Y);
+      rev(3, Y);
+      ld(2, X, true); rev(2, X);
+      ld(1, Y, true); rev(1, Y);
+      ld(0, X, true); rev(0, X);
     }
   };
 

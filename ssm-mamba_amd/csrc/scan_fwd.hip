@@ -36,17 +36,17 @@ namespace ssm {
 // steps); rows are bc_row_len(L) steps long.
 template <typename T>
 __global__ __launch_bounds__(256) void bc_prep_kernel(const int batch, const int N, const int L,
-                                                      const int ngroups, const int Lp,
+                                                      const int npair, const int Lp,
                                                       const T* __restrict__ Bp,
                                                       const T* __restrict__ Cp,
                                                       float* __restrict__ bc) {
-  const size_t total = (size_t)batch * ngroups * Lp;
+  const size_t total = (size_t)batch * npair * Lp;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
     const int t = (int)(i % Lp);
     const size_t bg = i / Lp;
-    const int G = (int)(bg % ngroups);
-    const int b = (int)(bg / ngroups);
+    const int G = (int)(bg % npair);
+    const int b = (int)(bg / npair);
     float v[4];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -125,6 +125,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   const int d0 = blockIdx.x * kBlockCh;
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
   const int ngroups = (N + 1) / 2;
+  const int npair = bc_pairs(N);
   const int Lp = bc_row_len(L);
   const size_t rb = (size_t)b * Dm;
 
@@ -197,8 +198,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
         // clamped into the pair's prepped row (rows are padded to 16 steps;
         // steps past it are never read by phase B)
         const int t = min(min(T0, last_t0) + sub * kTileF + step, Lp - 1);
-        const int Gc = min(G, ngroups - 1);
-        qbc[r] = bc4[((size_t)b * ngroups + Gc) * Lp + t];
+        qbc[r] = bc4[((size_t)b * npair + G) * Lp + t];
       }
     }
   };
@@ -245,14 +245,12 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       }
     }
     if constexpr (kSG == 1) {
-      // pairs past the last one get zero B and C, so their waves run the
-      // common path and contribute nothing
+      // pairs past the last one have zero B and C (prepped layout), so their
+      // waves run the common path and contribute nothing
 #pragma unroll
       for (int r = 0; r < kBCPer; ++r) {
         const int item = r * kThreads + tid;
-        const int G = (item / kTileF) % kWaves;
-        sBC[item / (kTileF * kWaves)][G][item % kTileF] =
-            G < ngroups ? qbc[r] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        sBC[item / (kTileF * kWaves)][(item / kTileF) % kWaves][item % kTileF] = qbc[r];
       }
     }
   };
@@ -400,7 +398,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
             const int G = g * kWaves + w;
             if (G < ngroups) {
               BC2 v;
-              load_bc_block(bc, bc_offset(b, G, ngroups, Lp, tb), v);
+              load_bc_block(bc, bc_offset(b, G, npair, Lp, tb), v);
               fwd_block(dl4, du4, v, A2[g], h[g], y);
             }
           }
@@ -472,23 +470,22 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
 // ---------------------------------------------------------------- launch
 
 size_t bc_prep_floats(int batch, int nstate, int seqlen) {
-  const size_t ngroups = (nstate + 1) / 2;
-  return (size_t)batch * ngroups * bc_row_len(seqlen) * 4;
+  return (size_t)batch * bc_pairs(nstate) * bc_row_len(seqlen) * 4;
 }
 
 hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t st) {
-  const int ngroups = (p.nstate + 1) / 2;
+  const int npair = bc_pairs(p.nstate);
   const int Lp = bc_row_len(p.seqlen);
-  const size_t total = (size_t)p.batch * ngroups * Lp;
+  const size_t total = (size_t)p.batch * npair * Lp;
   const int blocks = (int)std::min<size_t>((total + 255) / 256, 65535);
   ProfScope prof("bc_prep", st);
   if (dtype == 1)
     hipLaunchKernelGGL(bc_prep_kernel<__hip_bfloat16>, dim3(blocks), dim3(256), 0, st, p.batch,
-                       p.nstate, p.seqlen, ngroups, Lp, (const __hip_bfloat16*)p.B,
+                       p.nstate, p.seqlen, npair, Lp, (const __hip_bfloat16*)p.B,
                        (const __hip_bfloat16*)p.C, bc);
   else
     hipLaunchKernelGGL(bc_prep_kernel<float>, dim3(blocks), dim3(256), 0, st, p.batch, p.nstate,
-                       p.seqlen, ngroups, Lp, (const float*)p.B, (const float*)p.C, bc);
+                       p.seqlen, npair, Lp, (const float*)p.B, (const float*)p.C, bc);
   return hipGetLastError();
 }
 

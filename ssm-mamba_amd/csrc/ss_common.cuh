@@ -195,6 +195,45 @@ __device__ __forceinline__ void wave_reduce16(float (&v)[16], int lane) {
   v[0] += dpp_mov<kDppQuadXor2>(v[0]);
 }
 
+// ---------------------------------------------------------------- row broadcasts
+// A "block register" holds 16 wave-uniform values, value k in lane k of every
+// 16-lane row (lane l holds value l & 15).  DPP row_newbcast:k (gfx90a and
+// later) reads value k in every lane as an instruction operand, so a block
+// of 16 values costs one VGPR and one 4-byte load per lane instead of 16
+// registers or 128-bit broadcast LDS reads.  k must fold to a constant.
+#define SSM_ROW16(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15)
+
+// value k * x: the compiler folds the DPP move into v_mul_f32_dpp
+__device__ __forceinline__ float bc_mul(int k, float blk, float x) {
+  int v = 0;
+  switch (k) {
+#define SSM_BC_MUL(n) \
+  case n: v = __builtin_amdgcn_update_dpp(0, __float_as_int(blk), 0x150 + n, 0xF, 0xF, true); break;
+    SSM_ROW16(SSM_BC_MUL)
+#undef SSM_BC_MUL
+  }
+  return __int_as_float(v) * x;
+}
+
+// acc + value k * x as one v_fmac_f32_dpp.  The compiler does not fold a DPP
+// operand into v_fmac on this architecture, hence the inline instruction;
+// its s_nop provides the two wait states a DPP read of blk needs after a
+// VALU write of blk (the compiler does not see the DPP inside the asm).
+__device__ __forceinline__ float bc_fmac(int k, float acc, float blk, float x) {
+  switch (k) {
+#define SSM_BC_FMAC(n)                                                                         \
+  case n:                                                                                     \
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:" #n                                \
+        " row_mask:0xf bank_mask:0xf bound_ctrl:1"                                             \
+        : "+v"(acc)                                                                           \
+        : "v"(blk), "v"(x));                                                                  \
+    break;
+    SSM_ROW16(SSM_BC_FMAC)
+#undef SSM_BC_FMAC
+  }
+  return acc;
+}
+
 // Sum over groups of kW consecutive lanes (kW power of two <= 64); every lane
 // of a group gets the group sum.
 template <int kW>

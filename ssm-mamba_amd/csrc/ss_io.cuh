@@ -59,8 +59,13 @@ __device__ __forceinline__ void load_bc_block(const float* __restrict__ bc, size
 // block the kernels touch (up to the end of the last chunk) is inside the row.
 __host__ __device__ inline int bc_row_len(int L) { return (L + 15) & ~15; }
 
-__device__ __forceinline__ size_t bc_offset(int b, int G, int ngroups, int Lp, int t) {
-  return (((size_t)b * ngroups + G) * Lp + t) * 4;
+// State pairs in the prepped layout: ceil(N / 2) rounded up to a multiple of
+// the 8 waves of a workgroup; pairs past N hold zeros, so every wave of a
+// dispatch bucket can read a (zero) block without a branch.
+__host__ __device__ inline int bc_pairs(int N) { return (((N + 1) / 2) + 7) & ~7; }
+
+__device__ __forceinline__ size_t bc_offset(int b, int G, int npair, int Lp, int t) {
+  return (((size_t)b * npair + G) * Lp + t) * 4;
 }
 
 // 4 consecutive elements of a row as raw bits (8 B of bf16 or 16 B of fp32).

@@ -34,7 +34,8 @@ def test_queries():
     # fwd workspace: prepped B/C, fp32, rows padded to 16 steps, states padded to 4
     # prepped B/C (batch x pairs x padded steps x 4 floats) + a 256-byte store sink
     assert lib.ssm_scan_fwd_workspace_bytes(8, 2048, 2048, 16) == 8 * 4 * 2048 * 8 * 4 + 256
-    assert lib.ssm_scan_fwd_workspace_bytes(1, 64, 5, 3) == 512 + 256  # 2 pairs x 16 steps x 4 floats
+    # pairs padded to a multiple of 8: 8 pairs x 16 steps x 4 floats, + the sink
+    assert lib.ssm_scan_fwd_workspace_bytes(1, 64, 5, 3) == 8 * 16 * 4 * 4 + 256
     assert lib.ssm_scan_bwd_workspace_bytes(8, 2048, 2048, 16) > 2 * 32 * 8 * 16 * 2048 * 4
 
 
