@@ -13,7 +13,9 @@ arithmetic), inputs resident in HBM.  Prints ONE JSON line:
               of the same workload, in equivalent GB/s
 
 plus the decode step (config 2, cold = Infinity Cache flushed between steps,
-and warm), config 0 forward and config 3 forward+backward.
+and warm), config 0 forward, config 3 forward+backward and config 4 end to end
+(48-layer causal LM: prefill and greedy-decode tokens/s, share of time in the
+scan / update kernels; also alone with --e2e).
 """
 from __future__ import annotations
 
@@ -163,6 +165,115 @@ def decode_eager(su, dev, steps):
         su.apply_ext(x, A, B, C, D, dt, bias, states[k % 16], z=z, inplace=True, out=out)
 
 
+def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
+    """Config 4, end to end: the causal LM of ssm_mamba_amd.causal_lm at 48
+    layers, d_model 1024 (d_inner 2048, N 16, conv 4, dt_rank 64), vocab 50280,
+    bf16 weights with random init, eval mode.  Prefill = one forward over 4 x
+    2048 random token ids (id 0 is the pad id, so rows may be shorter and take
+    the left-padding length path), caching the decode state; decode = exactly
+    `decode_steps` greedy steps (48 layers + norm + LM head + pick each), the
+    step captured once in a HIP graph and replayed.  Returns tokens/s for both
+    and the share of time in the scan / state-update kernels: for the prefill
+    from the library's per-kernel HIP events, for the decode from a graph of
+    the step's 48 state updates alone on the same buffers."""
+    import torch
+
+    from ssm_mamba_amd import _native as N
+    from ssm_mamba_amd import selective_update as su
+    from ssm_mamba_amd.causal_lm import CausalLM, CausalLMConfig
+
+    torch.manual_seed(4)
+    cfg = CausalLMConfig(vocab_size=50280, model_dim=1024, state_dim=16, num_layers=48,
+                         device=str(dev))
+    model = CausalLM(cfg).to(dev, torch.bfloat16).eval()
+    n_params = sum(p.numel() for p in model.parameters())
+    batch, seqlen = 4, 2048
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, cfg.vocab_size, (batch, seqlen), generator=g).to(dev)
+    lengths = (ids != cfg.pad_token_id).sum(dim=1)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    dec = model.decoder(batch, decode_steps + 1)
+    with torch.no_grad():
+        dec.capture()
+        dec.prefill(ids, lengths)
+        dec.replay(2)
+        torch.cuda.synchronize()
+        pre = []
+        for _ in range(reps):
+            e0, e1 = ev(), ev()
+            e0.record()
+            model(ids, lengths, use_cache=True)
+            e1.record()
+            torch.cuda.synchronize()
+            pre.append(e0.elapsed_time(e1))
+        pre_ms = sorted(pre)[len(pre) // 2]
+        N.profile_begin()
+        model(ids, lengths, use_cache=True)
+        prof = N.profile_end()
+        scan_ms = sum(v[1] for k, v in prof.items() if k in ("scan_fwd", "bc_prep"))
+
+        dec.prefill(ids, lengths)
+        torch.cuda.synchronize()
+        e0, e1 = ev(), ev()
+        e0.record()
+        dec.replay(decode_steps)
+        e1.record()
+        torch.cuda.synchronize()
+        dec_ms = e0.elapsed_time(e1)
+        new_tokens = dec.tokens[:, :decode_steps + 1].clone()
+
+        # the step's 48 state updates alone, on the model's own buffers
+        inner, nstate = 2 * cfg.model_dim, cfg.state_dim
+        x = torch.randn(batch, inner, device=dev).bfloat16()
+        Bv = torch.randn(batch, nstate, device=dev).bfloat16()
+        layers = [l.ssm for l in model.layers]
+        A = [-torch.exp(m.log_A.float()) for m in layers]
+        Ds = [m.D.float() for m in layers]
+        bs = [m.delta_proj.bias.float() for m in layers]
+        out = torch.empty(batch, inner, device=dev, dtype=torch.bfloat16)
+
+        def updates():
+            for m, a, d, b in zip(layers, A, Ds, bs):
+                su.apply_ext(x, a, Bv, Bv, d, x, b, m._ssm_hiddens, z=x, inplace=True, out=out)
+
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            updates()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        ug = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(ug):
+            updates()
+        ug.replay()
+        torch.cuda.synchronize()
+        e0, e1 = ev(), ev()
+        e0.record()
+        for _ in range(decode_steps):
+            ug.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        upd_ms = e0.elapsed_time(e1)
+    res = {
+        "config": "48 layers, d_model 1024, d_inner 2048, N 16, d_conv 4, dt_rank 64, vocab 50280, "
+                  "bf16 weights (random init), eval; prefill 4 x 2048 (pad id 0 -> lengths), then "
+                  f"{decode_steps} greedy steps replayed from one HIP graph",
+        "params": n_params,
+        "prompt_lengths": lengths.tolist(),
+        "prefill_ms": round(pre_ms, 3),
+        "prefill_tokens_per_s": round(batch * seqlen / (pre_ms * 1e-3), 1),
+        "prefill_scan_share": round(scan_ms / pre_ms, 4),
+        "prefill_scan_ms": round(scan_ms, 3),
+        "decode_ms_per_step": round(dec_ms / decode_steps, 4),
+        "decode_tokens_per_s": round(batch * decode_steps / (dec_ms * 1e-3), 1),
+        "decode_update_share": round(upd_ms / dec_ms, 4),
+        "decode_update_us_per_step": round(1e3 * upd_ms / decode_steps, 2),
+        "first_new_tokens": new_tokens[0, :8].tolist(),
+    }
+    del model, dec
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(seconds: float):
     """Times the CPU oracle (fp32 torch) forward+backward on the config-1 shape
     with a reduced channel count, sized to run about `seconds`."""
@@ -223,6 +334,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-extra", action="store_true", help="only the config-1 step")
+    ap.add_argument("--e2e", action="store_true",
+                    help="only config 4 end to end (causal LM prefill + 128 decode steps); "
+                         "prints its own JSON line")
     ap.add_argument("--profile-run", action="store_true",
                     help="for rocprofv3 counter runs: one 256 MiB device-to-device copy (reference for "
                          "the byte counters), config-1 fwd+bwd (--steps times), 32 eager config-2 "
@@ -244,6 +358,9 @@ def main():
     N.lib()
     batch, dim, seqlen, nstate = 8, 2048, 2048, 16
     x = inputs(batch, dim, seqlen, nstate, torch.bfloat16, dev, seed=1)
+    if args.e2e:
+        print(json.dumps({"e2e": time_e2e(dev)}), flush=True)
+        return
     if args.profile_run:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -311,6 +428,10 @@ def main():
                                   "GBs": round((f3 + b3) / (ms3 * 1e-3) / 1e9, 1),
                                   "kernels_ms": {k: round(v, 4) for k, v in k3.items()}}
         del x3
+        try:
+            res["e2e"] = time_e2e(dev)
+        except Exception as exc:  # reported, not fatal to the headline line
+            res["e2e"] = {"error": f"{type(exc).__name__}: {exc}"}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(res), flush=True)

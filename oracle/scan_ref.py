@@ -89,8 +89,11 @@ def valid_mask(batch: int, seqlen: int, length: Optional[torch.Tensor],
     return t >= (seqlen - ln)
 
 
-def _prep(u, delta, A, B, C, D, delta_bias, h_init, z, dtype):
-    cv = lambda x: None if x is None else x.detach().to("cpu", dtype)
+def _prep(u, delta, A, B, C, D, delta_bias, h_init, z, dtype, keep_graph=False):
+    if keep_graph:
+        cv = lambda x: None if x is None else x.to("cpu", dtype)
+    else:
+        cv = lambda x: None if x is None else x.detach().to("cpu", dtype)
     u, delta, A, B, C, D, delta_bias, h_init, z = map(
         cv, (u, delta, A, B, C, D, delta_bias, h_init, z))
     batch, dim, seqlen = u.shape
@@ -103,8 +106,9 @@ def _prep(u, delta, A, B, C, D, delta_bias, h_init, z, dtype):
 
 def scan_fwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
              length=None, padding_right=True, z=None, delta_softplus=True,
-             chunk: Optional[int] = CHUNK, dtype=torch.float64):
-    """Reference forward.  Returns a dict with
+             chunk: Optional[int] = CHUNK, dtype=torch.float64, keep_graph: bool = False):
+    """Reference forward (differentiable by autograd when ``keep_graph``; the
+    inputs are detached otherwise).  Returns a dict with
 
     * ``out``   (B,D,L) pre-gate output D*u + sum_n C*h,
     * ``y``     (B,D,L) out * silu(z) (== out without z),
@@ -112,7 +116,7 @@ def scan_fwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
     * ``h_chunks`` (B,D,nchunks,N) state at the end of each ``chunk`` steps.
     """
     u, delta, A, B, C, D, delta_bias, h_init, z = _prep(
-        u, delta, A, B, C, D, delta_bias, h_init, z, dtype)
+        u, delta, A, B, C, D, delta_bias, h_init, z, dtype, keep_graph)
     batch, dim, seqlen = u.shape
     nstate = A.shape[1]
     x = delta + delta_bias[None, :, None]

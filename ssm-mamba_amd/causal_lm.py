@@ -1,0 +1,509 @@
+"""Mamba causal language model over the MI355X selective-scan operators.
+
+Module tree, parameter names, shapes, initialisation and the public methods
+follow the reference, so a reference ``state_dict`` loads unchanged and
+callers see the same API:
+
+* ``RMSNorm``        -- ``modules/rms_norm.py:4-31`` (scale ``1 + weight``);
+* ``Mamba``          -- ``modules/mamba.py:9-243`` (``forward`` :82-187,
+  ``step`` :189-243);
+* ``Block``          -- ``modules/block.py:8-87``;
+* ``CausalLMConfig`` / ``CausalLM`` -- ``models/causal_lm.py:9-134``.
+
+Layout.  Inside the layer stack activations stay channel-major,
+(batch, channels, seq_len), which is the layout the scan kernels stream.
+Every projection is computed as ``W @ X`` on channel-major ``X`` (one batched
+GEMM with the weight broadcast over the batch), so the reference's per-layer
+permute copies (``modules/mamba.py:104-111,156-163,181``) do not exist here:
+the sequence is transposed once after the embedding and once before the LM
+head.  The z gate is fused into the scan / state-update kernels.
+
+Decode.  ``Mamba.step`` updates the per-layer caches in place (conv window and
+fp32 SSM state), so a whole token step -- all layers, final norm, LM head and
+the greedy pick -- can be captured once in a HIP graph and replayed per token
+(``GreedyDecoder``).  ``CausalLM.generate`` returns exactly the reference's
+sequences (``models/causal_lm.py:98-133``), including its EOS handling.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Literal, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .ops import selective_scan_fn, selective_state_update
+
+__all__ = ["RMSNorm", "Mamba", "Block", "CausalLMConfig", "CausalLM", "GreedyDecoder"]
+
+
+def _proj_cm(weight: torch.Tensor, x: torch.Tensor, bias: Optional[torch.Tensor] = None):
+    """``weight @ x`` for channel-major x (batch, in, L) -> (batch, out, L):
+    one batched GEMM, weight broadcast over the batch, contiguous result."""
+    y = torch.matmul(weight, x)
+    if bias is not None:
+        y.add_(bias[:, None])
+    return y
+
+
+def causal_conv_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]):
+    """silu(causal depthwise conv1d(x)) over channel-major x (batch, channels, L):
+    ``modules/mamba.py:138-139`` (left zero padding of k-1, keep the first L)."""
+    k = weight.shape[-1]
+    seqlen = x.shape[-1]
+    return F.silu(F.conv1d(x, weight, bias, padding=k - 1, groups=x.shape[1])[..., :seqlen])
+
+
+class RMSNorm(nn.Module):
+    """x * rsqrt(mean(x^2) + eps) * (1 + weight), computed in float32 and cast
+    back to x's dtype (``modules/rms_norm.py:4-31``).  ``dim`` selects the
+    normalised axis (-1 for token-major input, 1 for channel-major)."""
+
+    def __init__(self, dim: int, eps: float = 1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.zeros(dim))
+
+    def forward(self, x: torch.Tensor, dim: int = -1) -> torch.Tensor:
+        xf = x.float()
+        d = dim % x.dim()
+        scale = torch.rsqrt(xf.pow(2).mean(d, keepdim=True) + self.eps)
+        w = 1.0 + self.weight.float()
+        if d != x.dim() - 1:
+            w = w.view(-1, *([1] * (x.dim() - 1 - d)))
+        return (xf * scale * w).type_as(x)
+
+
+class Mamba(nn.Module):
+    """Selective-SSM mixer (``modules/mamba.py:9-243``)."""
+
+    def __init__(
+        self,
+        model_dim: int = 512,
+        state_dim: int = 16,
+        conv_kernel: int = 4,
+        expansion_factor: int = 2,
+        delta_rank: int | str = "auto",
+        delta_min: float = 0.001,
+        delta_max: float = 0.1,
+        delta_init: Literal["random", "constant"] = "random",
+        delta_scale: float = 1.0,
+        delta_init_floor: float = 1e-4,
+        conv_bias: bool = False,
+        bias: bool = False,
+        device: str | None = None,
+    ):
+        super().__init__()
+        self.model_dim = model_dim
+        self.state_dim = state_dim
+        self.inner_dim = expansion_factor * model_dim
+        self.conv_kernel = conv_kernel
+        self.delta_rank = math.ceil(model_dim / 16) if delta_rank == "auto" else delta_rank
+        self.conv_bias = conv_bias
+        inner, rank, nstate = self.inner_dim, self.delta_rank, state_dim
+
+        self.input_proj = nn.Linear(model_dim, 2 * inner, bias=bias, device=device)
+        self.conv = nn.Conv1d(inner, inner, kernel_size=conv_kernel, padding=conv_kernel - 1,
+                              groups=inner, bias=conv_bias, device=device)
+        self.ssm_param_proj = nn.Linear(inner, rank + 2 * nstate, bias=False, device=device)
+        self.delta_proj = nn.Linear(rank, inner, bias=True, device=device)
+
+        # Initialisation of the step-size projection (modules/mamba.py:52-69):
+        # weight constant or uniform at rank^-0.5 * scale; bias = softplus^-1
+        # of a log-uniform step in [delta_min, delta_max], floored.
+        std = rank ** -0.5 * delta_scale
+        with torch.no_grad():
+            if delta_init == "constant":
+                self.delta_proj.weight.fill_(std)
+            elif delta_init == "random":
+                self.delta_proj.weight.uniform_(-std, std)
+            else:
+                raise NotImplementedError
+            lo, hi = math.log(delta_min), math.log(delta_max)
+            dt = torch.exp(torch.rand(inner, device=device) * (hi - lo) + lo)
+            dt = dt.clamp(min=delta_init_floor)
+            self.delta_proj.bias.copy_(dt + torch.log(-torch.expm1(-dt)))
+
+        # S4D-real A = -(1..N) per channel, stored as its log (modules/mamba.py:71-73)
+        steps = torch.arange(1, nstate + 1, dtype=torch.float32, device=device)
+        self.log_A = nn.Parameter(torch.log(steps).repeat(inner, 1))
+        self.D = nn.Parameter(torch.ones(inner, device=device))
+        self.out_proj = nn.Linear(inner, model_dim, bias=bias, device=device)
+
+        self._ssm_hiddens: Optional[torch.Tensor] = None   # (batch, inner, N) float32
+        self._conv_context: Optional[torch.Tensor] = None  # (batch, inner, k-1)
+
+    # ---- caches ---------------------------------------------------------
+    def allocate_cache(self, batch: int, device=None, dtype=None) -> None:
+        """Pre-allocate the decode caches.  Later prefills with use_cache=True
+        write into these buffers in place, so their addresses stay fixed (a
+        captured decode graph stays valid across prompts of this batch size)."""
+        w = self.input_proj.weight
+        device = w.device if device is None else device
+        dtype = w.dtype if dtype is None else dtype
+        ctx_shape = (batch, self.inner_dim, self.conv_kernel - 1)
+        ssm_shape = (batch, self.inner_dim, self.state_dim)
+        ctx, ssm = self._conv_context, self._ssm_hiddens
+        if not (ctx is not None and tuple(ctx.shape) == ctx_shape and ctx.dtype == dtype
+                and ctx.device == torch.device(device)):
+            self._conv_context = torch.zeros(ctx_shape, device=device, dtype=dtype)
+        if not (ssm is not None and tuple(ssm.shape) == ssm_shape and ssm.is_contiguous()
+                and ssm.dtype == torch.float32
+                and ssm.device == torch.device(device)):
+            self._ssm_hiddens = torch.zeros(ssm_shape, device=device, dtype=torch.float32)
+
+    @staticmethod
+    def _keep(old: Optional[torch.Tensor], new: torch.Tensor) -> torch.Tensor:
+        if (old is not None and old.shape == new.shape and old.dtype == new.dtype
+                and old.device == new.device):
+            old.copy_(new)
+            return old
+        return new.clone(memory_format=torch.contiguous_format)
+
+    def _store_conv_context(self, xs: torch.Tensor, lengths: Optional[torch.Tensor]) -> None:
+        """The k-1 pre-conv inputs ending at position lengths-1, zero where the
+        window starts before the sequence (``modules/mamba.py:113-135``)."""
+        batch, inner, seqlen = xs.shape
+        k1 = self.conv_kernel - 1
+        if lengths is None:
+            lengths = torch.full((batch,), seqlen, device=xs.device, dtype=torch.long)
+        idx = lengths[:, None] - k1 + torch.arange(k1, device=xs.device)
+        ctx = xs.gather(2, idx.clamp(min=0)[:, None, :].expand(batch, inner, k1))
+        ctx = ctx * (idx >= 0)[:, None, :].to(ctx.dtype)
+        self._conv_context = self._keep(self._conv_context, ctx.detach())
+
+    # ---- prefill / training ----------------------------------------------
+    def forward(self, hidden_states: torch.Tensor, ssm_hiddens: Optional[torch.Tensor] = None,
+                lengths: Optional[torch.Tensor] = None, use_cache: bool = False):
+        """hidden_states (batch, seq_len, model_dim) -> ((batch, seq_len,
+        model_dim), last_ssm_hiddens (batch, inner, N)), as
+        ``modules/mamba.py:82-187``."""
+        y, last = self.forward_cm(hidden_states.transpose(1, 2).contiguous(), ssm_hiddens,
+                                  lengths, use_cache)
+        return y.transpose(1, 2).contiguous(), last
+
+    def forward_cm(self, x: torch.Tensor, ssm_hiddens: Optional[torch.Tensor] = None,
+                   lengths: Optional[torch.Tensor] = None, use_cache: bool = False):
+        """Channel-major forward: x (batch, model_dim, L) -> (batch, model_dim, L)
+        and the last SSM state."""
+        inner, rank, nstate = self.inner_dim, self.delta_rank, self.state_dim
+        w_in, b_in = self.input_proj.weight, self.input_proj.bias
+        xs = _proj_cm(w_in[:inner], x, None if b_in is None else b_in[:inner])
+        z = _proj_cm(w_in[inner:], x, None if b_in is None else b_in[inner:])
+        if use_cache:
+            self._store_conv_context(xs, lengths)
+        xc = causal_conv_silu(xs, self.conv.weight, self.conv.bias)
+        params = torch.matmul(self.ssm_param_proj.weight, xc)       # (batch, R + 2N, L)
+        delta = torch.matmul(self.delta_proj.weight, params[:, :rank].contiguous())
+        Bm = params[:, rank:rank + nstate].contiguous()
+        Cm = params[:, rank + nstate:].contiguous()
+        A = -torch.exp(self.log_A.float())
+        # padding_side "left" is the reference's default at this call
+        # (modules/mamba.py:170-175 passes no padding argument)
+        y, last = selective_scan_fn(xc, delta, A, Bm, Cm, self.D, z=z,
+                                    delta_bias=self.delta_proj.bias, return_last_state=True,
+                                    h_init=ssm_hiddens, length=lengths, padding_side="left")
+        if use_cache:
+            self._ssm_hiddens = self._keep(self._ssm_hiddens, last.detach())
+        out = _proj_cm(self.out_proj.weight, y, self.out_proj.bias)
+        return out, last
+
+    # ---- decode ----------------------------------------------------------
+    def step(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        """One token (batch, model_dim) -> (batch, model_dim); updates the conv
+        window and the SSM state in place (``modules/mamba.py:189-243``)."""
+        if self._conv_context is None or self._ssm_hiddens is None:
+            raise RuntimeError("Mamba.step needs the caches of a forward(use_cache=True) "
+                               "or allocate_cache()")
+        inner, rank, nstate = self.inner_dim, self.delta_rank, self.state_dim
+        w_in, b_in = self.input_proj.weight, self.input_proj.bias
+        xs = F.linear(hidden_states, w_in[:inner], None if b_in is None else b_in[:inner])
+        z = F.linear(hidden_states, w_in[inner:], None if b_in is None else b_in[inner:])
+        ctx = self._conv_context
+        window = torch.cat([ctx, xs[..., None]], dim=-1)              # (batch, inner, k)
+        xc = (window * self.conv.weight[:, 0, :]).sum(dim=-1)
+        if self.conv.bias is not None:
+            xc = xc + self.conv.bias
+        xc = F.silu(xc)
+        ctx.copy_(window[..., 1:])
+        params = F.linear(xc, self.ssm_param_proj.weight)             # (batch, R + 2N)
+        delta = F.linear(params[:, :rank], self.delta_proj.weight)
+        A = -torch.exp(self.log_A.float())
+        out = selective_state_update(self._ssm_hiddens, xc, delta, A,
+                                     params[:, rank:rank + nstate], params[:, rank + nstate:],
+                                     self.D, z=z, dt_bias=self.delta_proj.bias)
+        return F.linear(out, self.out_proj.weight, self.out_proj.bias)
+
+
+class Block(nn.Module):
+    """Pre-norm residual block: x + dropout(mamba(norm(x))) (``modules/block.py:8-87``)."""
+
+    def __init__(
+        self,
+        model_dim: int = 512,
+        state_dim: int = 16,
+        expansion_factor: int = 2,
+        conv_kernel: int = 4,
+        conv_bias: bool = False,
+        bias: bool = False,
+        delta_rank: int | str = "auto",
+        delta_min: float = 0.001,
+        delta_max: float = 0.1,
+        delta_init: str = "random",
+        delta_scale: float = 1.0,
+        delta_init_floor: float = 1e-4,
+        dropout_rate: float = 0.15,
+        device: str | None = None,
+    ):
+        super().__init__()
+        self.norm = RMSNorm(model_dim)
+        self.ssm = Mamba(model_dim=model_dim, state_dim=state_dim,
+                         expansion_factor=expansion_factor, bias=bias, conv_kernel=conv_kernel,
+                         conv_bias=conv_bias, delta_rank=delta_rank, delta_min=delta_min,
+                         delta_max=delta_max, delta_init=delta_init, delta_scale=delta_scale,
+                         delta_init_floor=delta_init_floor, device=device)
+        self.dropout = nn.Dropout(dropout_rate)
+
+    def forward(self, hidden_states: torch.Tensor, lengths: Optional[torch.Tensor] = None,
+                ssm_hiddens: Optional[torch.Tensor] = None, use_cache: bool = False):
+        """(batch, seq_len, model_dim) -> ((batch, seq_len, model_dim), last state)."""
+        y, last = self.forward_cm(hidden_states.transpose(1, 2).contiguous(), lengths,
+                                  ssm_hiddens, use_cache)
+        return y.transpose(1, 2).contiguous(), last
+
+    def forward_cm(self, x: torch.Tensor, lengths: Optional[torch.Tensor] = None,
+                   ssm_hiddens: Optional[torch.Tensor] = None, use_cache: bool = False):
+        y, last = self.ssm.forward_cm(self.norm(x, dim=1), ssm_hiddens=ssm_hiddens,
+                                      lengths=lengths, use_cache=use_cache)
+        return x + self.dropout(y), last
+
+    def step(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        return hidden_states + self.ssm.step(self.norm(hidden_states))
+
+
+@dataclass
+class CausalLMConfig:
+    """Same fields and defaults as ``models/causal_lm.py:9-30``."""
+    vocab_size: int = 32000
+    model_dim: int = 512
+    state_dim: int = 16
+    expansion_factor: int = 2
+    conv_kernel: int = 4
+    conv_bias: bool = False
+    bias: bool = False
+    delta_rank: int | str = "auto"
+    delta_min: float = 0.001
+    delta_max: float = 0.1
+    delta_init: Literal["random", "constant"] = "random"
+    delta_scale: float = 1.0
+    delta_init_floor: float = 1e-4
+    dropout_rate: float = 0.15
+    num_layers: int = 5
+    tie_embeddings: bool = True
+    device: str | None = None
+    pad_token_id: int = 0
+    bos_token_id: int = 1
+    eos_token_id: int = 2
+
+
+def _greedy_pick(logits: torch.Tensor, temperature: float) -> torch.Tensor:
+    """argmax of softmax(logits / temperature), as ``models/causal_lm.py:117-120``."""
+    if temperature != 1.0:
+        logits = logits / temperature
+    return torch.softmax(logits, dim=-1).argmax(dim=-1)
+
+
+class CausalLM(nn.Module):
+    """Embedding -> Blocks -> RMSNorm -> LM head (``models/causal_lm.py:32-134``)."""
+
+    def __init__(self, config: CausalLMConfig | None = None):
+        super().__init__()
+        if config is None:
+            config = CausalLMConfig()
+        self.config = config
+        c = config
+        self.embedding = nn.Embedding(c.vocab_size, c.model_dim, device=c.device)
+        self.layers = nn.ModuleList([
+            Block(model_dim=c.model_dim, state_dim=c.state_dim,
+                  expansion_factor=c.expansion_factor, conv_kernel=c.conv_kernel,
+                  conv_bias=c.conv_bias, bias=c.bias, delta_rank=c.delta_rank,
+                  delta_min=c.delta_min, delta_max=c.delta_max, delta_init=c.delta_init,
+                  delta_scale=c.delta_scale, delta_init_floor=c.delta_init_floor,
+                  dropout_rate=c.dropout_rate, device=c.device)
+            for _ in range(c.num_layers)
+        ])
+        self.norm = RMSNorm(c.model_dim)
+        self.lm_head = nn.Linear(c.model_dim, c.vocab_size, bias=False, device=c.device)
+        if c.tie_embeddings:
+            self.lm_head.weight = self.embedding.weight
+        self._decoders = {}
+
+    def allocate_cache(self, batch: int) -> None:
+        for layer in self.layers:
+            layer.ssm.allocate_cache(batch)
+
+    def forward(self, input_ids: torch.Tensor, lengths: Optional[torch.Tensor] = None,
+                use_cache: bool = False) -> torch.Tensor:
+        """input_ids (batch, seq_len) -> logits (batch, seq_len, vocab)."""
+        x = self.embedding(input_ids).transpose(1, 2).contiguous()
+        for layer in self.layers:
+            x, _ = layer.forward_cm(x, lengths=lengths, use_cache=use_cache)
+        x = self.norm(x.transpose(1, 2).contiguous())
+        return self.lm_head(x)
+
+    def step(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """input_ids (batch,) -> logits (batch, vocab), advancing every cache."""
+        x = self.embedding(input_ids)
+        for layer in self.layers:
+            x = layer.step(x)
+        return self.lm_head(self.norm(x))
+
+    def decoder(self, batch: int, max_new_tokens: int, temperature: float = 1.0) -> "GreedyDecoder":
+        key = (batch, max_new_tokens, float(temperature))
+        dec = self._decoders.get(key)
+        if dec is None:
+            dec = GreedyDecoder(self, batch, max_new_tokens, temperature)
+            self._decoders[key] = dec
+        return dec
+
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 100,
+                 temperature: float = 1.0, use_graph: Optional[bool] = None) -> torch.Tensor:
+        """Greedy generation with the reference's semantics
+        (``models/causal_lm.py:98-133``): prompt lengths count the non-pad
+        tokens, the first new token comes from the logits at lengths-1,
+        generation stops once every row has produced EOS, and every position
+        from a row's first EOS on is set to EOS.  With ``use_graph`` (default on
+        a GPU) each token step is one HIP-graph replay."""
+        if use_graph is None:
+            use_graph = input_ids.is_cuda
+        with torch.no_grad():
+            if use_graph and max_new_tokens > 0:
+                new = self.decoder(input_ids.shape[0], max_new_tokens, temperature).generate(input_ids)
+            else:
+                new = self._generate_eager(input_ids, max_new_tokens, temperature)
+            eos = self.config.eos_token_id
+            seq = torch.cat([input_ids, new], dim=1)
+            after_eos = (seq == eos).to(torch.int32).cumsum(dim=1) >= 1
+            return torch.where(after_eos, torch.full_like(seq, eos), seq)
+
+    def _generate_eager(self, input_ids, max_new_tokens, temperature):
+        batch = input_ids.shape[0]
+        dev = input_ids.device
+        lengths = (input_ids != self.config.pad_token_id).sum(dim=1)
+        logits = self.forward(input_ids, lengths, use_cache=True)
+        logits = logits[torch.arange(batch, device=dev), lengths - 1]
+        finished = torch.zeros(batch, dtype=torch.bool, device=dev)
+        out = []
+        for _ in range(max_new_tokens):
+            nxt = _greedy_pick(logits, temperature)
+            out.append(nxt)
+            finished |= nxt == self.config.eos_token_id
+            if bool(finished.all()):
+                break
+            logits = self.step(nxt)
+        if not out:
+            return input_ids.new_zeros(batch, 0)
+        return torch.stack(out, dim=1)
+
+
+class GreedyDecoder:
+    """Greedy decoding with one token step -- every layer's ``step``, the final
+    norm, the LM head and the pick -- captured in a HIP graph.
+
+    The decoder owns static buffers: the per-layer caches (allocated once, and
+    refilled in place by each prefill), the current token, the generated
+    tokens and a device-side position counter, so a replay needs no host
+    work.  Overlapping use of one model by two decoders of the same batch size
+    shares the caches; run them one after the other."""
+
+    def __init__(self, model: CausalLM, batch: int, max_new_tokens: int, temperature: float = 1.0):
+        self.model = model
+        self.batch = batch
+        self.max_new = max_new_tokens
+        self.temperature = temperature
+        dev = model.embedding.weight.device
+        self.device = dev
+        model.allocate_cache(batch)
+        # the graph bakes in these buffers' addresses: hold them, and put them
+        # back on the layers before every prefill
+        self.caches = [(layer.ssm._conv_context, layer.ssm._ssm_hiddens) for layer in model.layers]
+        self.token = torch.zeros(batch, dtype=torch.long, device=dev)
+        self.tokens = torch.zeros(batch, max(max_new_tokens, 1), dtype=torch.long, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.long, device=dev)
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    def _install(self) -> None:
+        for layer, (ctx, ssm) in zip(self.model.layers, self.caches):
+            layer.ssm._conv_context, layer.ssm._ssm_hiddens = ctx, ssm
+
+    def _body(self) -> None:
+        logits = self.model.step(self.token)
+        nxt = _greedy_pick(logits, self.temperature)
+        self.token.copy_(nxt)
+        self.tokens.index_copy_(1, self.pos.clamp(max=self.tokens.shape[1] - 1), nxt[:, None])
+        self.pos.add_(1)
+
+    def capture(self) -> None:
+        """Warm up and capture the step (the caches' contents are overwritten
+        by the next prefill)."""
+        if self.graph is not None:
+            return
+        self._install()
+        with torch.no_grad():
+            side = torch.cuda.Stream(self.device)
+            side.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(side):
+                for _ in range(2):
+                    self._body()
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._body()
+            self.graph = graph
+
+    def prefill(self, input_ids: torch.Tensor, lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Run the prompt, fill the caches and pick the first new token (stored
+        as generated token 0).  Returns the prompt logits."""
+        self._install()
+        with torch.no_grad():
+            if lengths is None:
+                lengths = (input_ids != self.model.config.pad_token_id).sum(dim=1)
+            logits = self.model.forward(input_ids, lengths, use_cache=True)
+            last = logits[torch.arange(self.batch, device=self.device), lengths - 1]
+            first = _greedy_pick(last, self.temperature)
+            self.token.copy_(first)
+            self.tokens[:, 0] = first
+            self.pos.fill_(1)
+        return logits
+
+    def replay(self, steps: int) -> None:
+        """Advance ``steps`` tokens (one model step each)."""
+        if self.graph is None:
+            self.capture()
+        self._install()
+        for _ in range(steps):
+            self.graph.replay()
+
+    def generate(self, input_ids: torch.Tensor, check_every: int = 16) -> torch.Tensor:
+        """New tokens (batch, k) of the reference's greedy loop: k is the first
+        count at which every row has produced EOS, else max_new_tokens."""
+        self.capture()
+        self.prefill(input_ids)
+        eos = self.model.config.eos_token_id
+        done = 1
+        while True:
+            seen = (self.tokens[:, :done] == eos).any(dim=1)
+            if bool(seen.all()):
+                # the first count at which every row has an EOS
+                first = torch.where(self.tokens[:, :done] == eos,
+                                    torch.arange(done, device=self.device),
+                                    torch.full_like(self.tokens[:, :done], done))
+                k = int(first.min(dim=1).values.max()) + 1
+                return self.tokens[:, :k].clone()
+            if done >= self.max_new:
+                return self.tokens[:, :self.max_new].clone()
+            n = min(check_every, self.max_new - done)
+            self.replay(n)
+            done += n

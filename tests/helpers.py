@@ -41,3 +41,31 @@ def make_case(batch, dim, seqlen, nstate, dtype, seed=0, with_z=True, h_init=Fal
 
 def to_dev(case: dict, dev) -> dict:
     return {k: (None if v is None else v.to(dev).contiguous()) for k, v in case.items()}
+
+
+def make_lm(seed=0, vocab=37, model_dim=16, state_dim=4, layers=2, bias=True, conv_bias=True,
+            tie=True):
+    """A small CausalLM (float32, CPU, eval mode, no dropout) with every
+    parameter randomised -- norm weights and biases too, so no term of the
+    model is trivially zero."""
+    from ssm_mamba_amd.causal_lm import CausalLM, CausalLMConfig
+    torch.manual_seed(seed)
+    cfg = CausalLMConfig(vocab_size=vocab, model_dim=model_dim, state_dim=state_dim,
+                         num_layers=layers, bias=bias, conv_bias=conv_bias, tie_embeddings=tie,
+                         dropout_rate=0.0)
+    with torch.device("cpu"):
+        m = CausalLM(cfg).float()
+    g = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if name.endswith("norm.weight") or (name.endswith(".bias") and "delta_proj" not in name):
+                p.copy_(0.3 * torch.randn(p.shape, generator=g))
+    return m.eval(), cfg
+
+
+def lm_state64(model):
+    """The model's state_dict as float64 CPU tensors, tied weights kept tied."""
+    sd = {k: v.detach().to("cpu", torch.float64) for k, v in model.state_dict().items()}
+    if model.lm_head.weight is model.embedding.weight:
+        sd["lm_head.weight"] = sd["embedding.weight"]
+    return sd
