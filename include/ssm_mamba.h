@@ -123,6 +123,37 @@ int ssm_selective_state_update(int64_t batch, int64_t dim, int64_t nstate, int d
                                const float* D, const float* dt_bias, const void* z,
                                int dt_softplus, void* out, void* stream);
 
+/*
+ * Causal depthwise conv1d (+ SiLU) over channel-major rows: the prefill
+ * convolution of the Mamba layer, nn.Conv1d(dim, dim, width, groups=dim,
+ * padding=width-1)(x)[..., :seqlen] followed by F.silu
+ * (modules/mamba.py:37-44,138-139), which the reference runs as two torch ops.
+ *
+ *   out[b,c,t] = act(bias[c] + sum_{j<width} weight[c,j] * x[b,c,t-(width-1)+j]),
+ *   x = 0 before t = 0; act = silu when silu != 0, else the identity.
+ * x, out (batch, dim, seqlen); weight (dim, width) (the (dim, 1, width) conv
+ * weight); bias (dim) nullable.  All of x, out, weight, bias (and the
+ * gradients below) have element type `dtype`; arithmetic is fp32.
+ * width <= 8.
+ */
+int ssm_causal_conv1d_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t width, int dtype,
+                          const void* x, const void* weight, const void* bias, int silu, void* out,
+                          void* stream);
+
+/* Device workspace (bytes) for ssm_causal_conv1d_bwd. */
+size_t ssm_causal_conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t width);
+
+/*
+ * Backward of ssm_causal_conv1d_fwd for the upstream gradient dout: writes dx
+ * (batch, dim, seqlen), dweight (dim, width) and, when non-NULL, dbias (dim)
+ * (all overwritten; bias NULL counts as zero).  The weight and bias gradients
+ * are summed over batch and time in a fixed order (deterministic).
+ */
+int ssm_causal_conv1d_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t width, int dtype,
+                          const void* x, const void* weight, const void* bias, const void* dout,
+                          int silu, void* dx, void* dweight, void* dbias, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,17 @@ SIGNATURES = {
         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,  # state, new_state, x, dt, A, B, C, D, dt_bias, z
         _i32, _p, _p,                          # dt_softplus, out, stream
     ]),
+    "ssm_causal_conv1d_fwd": (_i32, [
+        _i64, _i64, _i64, _i64, _i32,          # batch, dim, seqlen, width, dtype
+        _p, _p, _p, _i32, _p, _p,              # x, weight, bias, silu, out, stream
+    ]),
+    "ssm_causal_conv1d_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "ssm_causal_conv1d_bwd": (_i32, [
+        _i64, _i64, _i64, _i64, _i32,
+        _p, _p, _p, _p, _i32,                  # x, weight, bias, dout, silu
+        _p, _p, _p,                            # dx, dweight, dbias
+        _p, _sz, _p,                           # workspace, bytes, stream
+    ]),
 }
 
 ABI_VERSION = 1

@@ -34,6 +34,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .causal_conv1d import causal_conv1d_fn
 from .ops import selective_scan_fn, selective_state_update
 
 __all__ = ["RMSNorm", "Mamba", "Block", "CausalLMConfig", "CausalLM", "GreedyDecoder"]
@@ -41,19 +42,21 @@ __all__ = ["RMSNorm", "Mamba", "Block", "CausalLMConfig", "CausalLM", "GreedyDec
 
 def _proj_cm(weight: torch.Tensor, x: torch.Tensor, bias: Optional[torch.Tensor] = None):
     """``weight @ x`` for channel-major x (batch, in, L) -> (batch, out, L):
-    one batched GEMM, weight broadcast over the batch, contiguous result."""
-    y = torch.matmul(weight, x)
-    if bias is not None:
-        y.add_(bias[:, None])
-    return y
+    one strided-batched GEMM with the weight broadcast over the batch (batch
+    stride 0), contiguous result.  (``torch.matmul`` would fold a weight that
+    requires grad through transposed copies of x and of the result.)"""
+    x = x.contiguous()
+    w = weight.expand(x.shape[0], weight.shape[0], weight.shape[1])
+    if bias is None:
+        return torch.bmm(w, x)
+    return torch.baddbmm(bias[None, :, None].expand(x.shape[0], weight.shape[0], x.shape[2]), w, x)
 
 
 def causal_conv_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]):
-    """silu(causal depthwise conv1d(x)) over channel-major x (batch, channels, L):
-    ``modules/mamba.py:138-139`` (left zero padding of k-1, keep the first L)."""
-    k = weight.shape[-1]
-    seqlen = x.shape[-1]
-    return F.silu(F.conv1d(x, weight, bias, padding=k - 1, groups=x.shape[1])[..., :seqlen])
+    """silu(causal depthwise conv1d(x)) over channel-major x (batch, channels, L)
+    in one HIP kernel: ``modules/mamba.py:138-139`` (left zero padding of k-1,
+    keep the first L)."""
+    return causal_conv1d_fn(x, weight, bias, activation="silu")
 
 
 class RMSNorm(nn.Module):
@@ -195,8 +198,8 @@ class Mamba(nn.Module):
         if use_cache:
             self._store_conv_context(xs, lengths)
         xc = causal_conv_silu(xs, self.conv.weight, self.conv.bias)
-        params = torch.matmul(self.ssm_param_proj.weight, xc)       # (batch, R + 2N, L)
-        delta = torch.matmul(self.delta_proj.weight, params[:, :rank].contiguous())
+        params = _proj_cm(self.ssm_param_proj.weight, xc)           # (batch, R + 2N, L)
+        delta = _proj_cm(self.delta_proj.weight, params[:, :rank])
         Bm = params[:, rank:rank + nstate].contiguous()
         Cm = params[:, rank + nstate:].contiguous()
         A = -torch.exp(self.log_A.float())

@@ -19,6 +19,14 @@ hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* 
 hipError_t launch_state_update(const UpdateParams& p, int dtype, bool vecN, hipStream_t st);
 size_t bc_prep_floats(int batch, int nstate, int seqlen);
 size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen);
+int conv1d_max_width();
+hipError_t launch_causal_conv1d_fwd(int batch, int dim, int L, int K, int dtype_bf16,
+                                    const void* x, const void* w, const void* bias, int silu,
+                                    void* out, bool vec, hipStream_t st);
+hipError_t launch_causal_conv1d_bwd(int batch, int dim, int L, int K, int dtype_bf16,
+                                    const void* x, const void* w, const void* bias,
+                                    const void* dout, int silu, void* dx, void* dw, void* dbias,
+                                    float* part, bool vec, hipStream_t st);
 }  // namespace ssm
 
 namespace ssm {
@@ -119,6 +127,20 @@ ssm::ScanParams make_scan_params(int64_t batch, int64_t dim, int64_t seqlen, int
   p.length = length;
   p.z = z;
   return p;
+}
+
+int check_conv(int64_t batch, int64_t dim, int64_t seqlen, int64_t width, int dtype) {
+  if (dtype != SSM_F32 && dtype != SSM_BF16)
+    return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16 (got %d)", dtype);
+  if (batch < 1 || dim < 1 || seqlen < 1 || width < 1)
+    return fail(SSM_ERR_INVALID, "batch, dim, seqlen and width must be >= 1 (got %lld, %lld, %lld, %lld)",
+                (long long)batch, (long long)dim, (long long)seqlen, (long long)width);
+  if (width > ssm::conv1d_max_width())
+    return fail(SSM_ERR_UNSUPPORTED, "causal_conv1d supports width <= %d (got %lld)",
+                ssm::conv1d_max_width(), (long long)width);
+  if (batch * dim > INT_MAX || seqlen > INT_MAX / 2)
+    return fail(SSM_ERR_UNSUPPORTED, "batch * dim must be < 2^31 and seqlen < 2^30");
+  return SSM_OK;
 }
 
 bool scan_aligned(int dtype, int64_t seqlen, std::initializer_list<const void*> ptrs) {
@@ -315,6 +337,44 @@ int ssm_selective_state_update(int64_t batch, int64_t dim, int64_t nstate, int d
                                       : (((uintptr_t)B | (uintptr_t)C) & 7) == 0);
   return hip_status(ssm::launch_state_update(p, dtype, vecN, static_cast<hipStream_t>(stream)),
                     "selective_state_update launch");
+}
+
+size_t ssm_causal_conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t width) {
+  if (batch < 1 || dim < 1 || width < 1) return 0;
+  return round256((size_t)batch * (size_t)dim * (size_t)(width + 1) * sizeof(float));
+}
+
+int ssm_causal_conv1d_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t width, int dtype,
+                          const void* x, const void* weight, const void* bias, int silu, void* out,
+                          void* stream) {
+  int rc = check_conv(batch, dim, seqlen, width, dtype);
+  if (rc != SSM_OK) return rc;
+  if (!x || !weight || !out) return fail(SSM_ERR_INVALID, "x, weight and out must be non-NULL");
+  const bool vec = seqlen % 8 == 0 && aligned16(x) && aligned16(out);
+  return hip_status(ssm::launch_causal_conv1d_fwd((int)batch, (int)dim, (int)seqlen, (int)width,
+                                                  dtype == SSM_BF16, x, weight, bias, silu ? 1 : 0,
+                                                  out, vec, static_cast<hipStream_t>(stream)),
+                    "causal_conv1d_fwd launch");
+}
+
+int ssm_causal_conv1d_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t width, int dtype,
+                          const void* x, const void* weight, const void* bias, const void* dout,
+                          int silu, void* dx, void* dweight, void* dbias, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  int rc = check_conv(batch, dim, seqlen, width, dtype);
+  if (rc != SSM_OK) return rc;
+  if (!x || !weight || !dout || !dx || !dweight)
+    return fail(SSM_ERR_INVALID, "x, weight, dout, dx and dweight must be non-NULL");
+  const size_t need = ssm_causal_conv1d_bwd_workspace_bytes(batch, dim, width);
+  if (!workspace || workspace_bytes < need)
+    return fail(SSM_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+  const bool vec = seqlen % 8 == 0 && aligned16(x) && aligned16(dout) && aligned16(dx);
+  return hip_status(ssm::launch_causal_conv1d_bwd((int)batch, (int)dim, (int)seqlen, (int)width,
+                                                  dtype == SSM_BF16, x, weight, bias, dout,
+                                                  silu ? 1 : 0, dx, dweight, dbias,
+                                                  static_cast<float*>(workspace), vec,
+                                                  static_cast<hipStream_t>(stream)),
+                    "causal_conv1d_bwd launch");
 }
 
 }  // extern "C"
