@@ -154,6 +154,65 @@ int ssm_causal_conv1d_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t wi
                           int silu, void* dx, void* dweight, void* dbias, void* workspace,
                           size_t workspace_bytes, void* stream);
 
+/*
+ * Fused decode step of a Mamba block, for 1 <= batch <= 8 sequences.  The
+ * reference's Block.step / Mamba.step (modules/block.py:80-86,
+ * modules/mamba.py:189-243) runs about twenty torch ops per layer and token;
+ * these four calls do the same work:
+ *
+ *   ssm_decode_in_proj_conv   xz = W_in @ rmsnorm(x) [+ b_in]; conv step -> xc;
+ *                             the conv window rolls
+ *   ssm_decode_gemv           params = W_x @ xc                  (batch, rank + 2*nstate)
+ *   ssm_decode_ssm_step       state update, y = (C.h + D xc) * silu(z)
+ *   ssm_decode_gemv           x' = x + W_out @ y [+ b_out]       (residual set)
+ *
+ * Every tensor except state has element type `dtype` (weights and the norm,
+ * conv, dt and A/D parameters included); state (batch, dim, nstate) is fp32.
+ * Row-major throughout.
+ */
+
+/*
+ * y[b, o] = sum_k W[o, k] v[b, k] (+ bias[o]) (+ residual[b, o]) with
+ * v = x, or v = x * rsqrt(mean_k x^2 + norm_eps) * (1 + norm_weight) when
+ * norm_weight is non-NULL (the reference's RMSNorm, modules/rms_norm.py:11-31).
+ * W (out_dim, in_dim); x (batch, in_dim); y, residual (batch, out_dim).
+ * in_dim a multiple of 16 bytes of elements; W, x, norm_weight 16-byte aligned.
+ * Also the decode LM head (models/causal_lm.py:93-104) with the final norm.
+ */
+int ssm_decode_gemv(int64_t batch, int64_t out_dim, int64_t in_dim, int dtype, const void* weight,
+                    const void* x, const void* norm_weight, float norm_eps, const void* bias,
+                    const void* residual, void* y, void* stream);
+
+/*
+ * In-projection with the conv step (modules/mamba.py:199-214): xz (batch,
+ * 2*dim) = in_proj_weight (2*dim, in_dim) @ v [+ in_proj_bias], v = x or its
+ * RMSNorm (norm_weight non-NULL, as in ssm_decode_gemv); then for the x half
+ * xs = xz[:, :dim]: xc (batch, dim) = silu(sum_{j<width-1} conv_weight[c, j] *
+ * conv_window[b, c, j] + conv_weight[c, width-1] * xs + conv_bias[c]) and the
+ * window rolls: conv_window (batch, dim, width-1) <- [window[..., 1:], xs].
+ * conv_weight (dim, width); conv_bias nullable; 2 <= width <= 8.
+ */
+int ssm_decode_in_proj_conv(int64_t batch, int64_t dim, int64_t in_dim, int64_t width, int dtype,
+                            const void* in_proj_weight, const void* x, const void* norm_weight,
+                            float norm_eps, const void* in_proj_bias, const void* conv_weight,
+                            const void* conv_bias, void* conv_window, void* xz, void* xc,
+                            void* stream);
+
+/*
+ * Step-size projection, state update and gate (modules/mamba.py:223-240 with
+ * selective_update/kernel.cu:39-71): delta = dt_proj_weight (dim, rank) @
+ * params[:, :rank]; delta' = softplus(delta + dt_bias); A = -exp(log_A);
+ * state = exp(delta' A) state + delta' xc B with B = params[:, rank:rank+nstate];
+ * y = (sum_n C state + D xc) * silu(z), C = params[:, rank+nstate:],
+ * z = xz[:, dim:2*dim] (row stride ld_xz).  state updated in place.
+ * params (batch, rank + 2*nstate); dt_bias, D nullable; nstate in
+ * {4, 8, 16, 32, 64}.
+ */
+int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank, int dtype,
+                        const void* params, const void* dt_proj_weight, const void* dt_bias,
+                        const void* log_A, const void* D, const void* xc, const void* xz,
+                        int64_t ld_xz, float* state, void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

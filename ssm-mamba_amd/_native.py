@@ -64,6 +64,22 @@ SIGNATURES = {
         _p, _p, _p,                            # dx, dweight, dbias
         _p, _sz, _p,                           # workspace, bytes, stream
     ]),
+    "ssm_decode_gemv": (_i32, [
+        _i64, _i64, _i64, _i32,                # batch, out_dim, in_dim, dtype
+        _p, _p, _p, ctypes.c_float,            # weight, x, norm_weight, norm_eps
+        _p, _p, _p, _p,                        # bias, residual, y, stream
+    ]),
+    "ssm_decode_in_proj_conv": (_i32, [
+        _i64, _i64, _i64, _i64, _i32,          # batch, dim, in_dim, width, dtype
+        _p, _p, _p, ctypes.c_float, _p,        # in_proj_weight, x, norm_weight, norm_eps, in_proj_bias
+        _p, _p, _p, _p, _p, _p,                # conv_weight, conv_bias, window, xz, xc, stream
+    ]),
+    "ssm_decode_ssm_step": (_i32, [
+        _i64, _i64, _i64, _i64, _i32,          # batch, dim, nstate, rank, dtype
+        _p, _p, _p, _p, _p,                    # params, dt_proj_weight, dt_bias, log_A, D
+        _p, _p, _i64,                          # xc, xz, ld_xz
+        _p, _p, _p,                            # state, y, stream
+    ]),
 }
 
 ABI_VERSION = 1

@@ -34,6 +34,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import decode as _dec
 from .causal_conv1d import causal_conv1d_fn
 from .ops import selective_scan_fn, selective_state_update
 
@@ -220,6 +221,8 @@ class Mamba(nn.Module):
         if self._conv_context is None or self._ssm_hiddens is None:
             raise RuntimeError("Mamba.step needs the caches of a forward(use_cache=True) "
                                "or allocate_cache()")
+        if _dec.block_step_supported(self, hidden_states, None):
+            return _dec.block_step(self, hidden_states)
         inner, rank, nstate = self.inner_dim, self.delta_rank, self.state_dim
         w_in, b_in = self.input_proj.weight, self.input_proj.bias
         xs = F.linear(hidden_states, w_in[:inner], None if b_in is None else b_in[:inner])
@@ -283,6 +286,10 @@ class Block(nn.Module):
         return x + self.dropout(y), last
 
     def step(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        if _dec.block_step_supported(self.ssm, hidden_states, self.norm.weight):
+            # norm, mixer and residual in the four fused decode kernels
+            return _dec.block_step(self.ssm, hidden_states, self.norm.weight, self.norm.eps,
+                                   residual=True)
         return hidden_states + self.ssm.step(self.norm(hidden_states))
 
 
@@ -361,6 +368,9 @@ class CausalLM(nn.Module):
         x = self.embedding(input_ids)
         for layer in self.layers:
             x = layer.step(x)
+        if _dec.gemv_supported(self.lm_head.weight, x, self.norm.weight):
+            return _dec.gemv(self.lm_head.weight, x, norm_weight=self.norm.weight,
+                             eps=self.norm.eps)
         return self.lm_head(self.norm(x))
 
     def decoder(self, batch: int, max_new_tokens: int, temperature: float = 1.0) -> "GreedyDecoder":

@@ -20,6 +20,18 @@ hipError_t launch_state_update(const UpdateParams& p, int dtype, bool vecN, hipS
 size_t bc_prep_floats(int batch, int nstate, int seqlen);
 size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen);
 int conv1d_max_width();
+int decode_max_batch();
+hipError_t launch_decode_gemv(int bf16, const void* W, const void* x, const void* nw, float eps,
+                              const void* bias, const void* res, void* y, int B, int O, int K,
+                              hipStream_t st);
+hipError_t launch_decode_in_proj_conv(int bf16, const void* W, const void* x, const void* nw,
+                                      float eps, const void* bias, void* xz, int B, int dim, int K,
+                                      int width, void* ctx, const void* cw, const void* cb,
+                                      void* xc, hipStream_t st);
+hipError_t launch_decode_ssm_step(int bf16, const void* p, int nout, int R, const void* Wdt,
+                                  const void* dtb, const void* logA, const void* D, const void* xc,
+                                  const void* xz, int ld, float* state, void* y, int B, int dim,
+                                  int nstate, bool vecR, hipStream_t st);
 hipError_t launch_causal_conv1d_fwd(int batch, int dim, int L, int K, int dtype_bf16,
                                     const void* x, const void* w, const void* bias, int silu,
                                     void* out, bool vec, hipStream_t st);
@@ -142,6 +154,18 @@ int check_conv(int64_t batch, int64_t dim, int64_t seqlen, int64_t width, int dt
     return fail(SSM_ERR_UNSUPPORTED, "batch * dim must be < 2^31 and seqlen < 2^30");
   return SSM_OK;
 }
+
+int check_decode(int64_t batch, int dtype) {
+  if (dtype != SSM_F32 && dtype != SSM_BF16)
+    return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16 (got %d)", dtype);
+  if (batch < 1 || batch > ssm::decode_max_batch())
+    return fail(SSM_ERR_UNSUPPORTED, "decode kernels take 1 <= batch <= %d (got %lld)",
+                ssm::decode_max_batch(), (long long)batch);
+  return SSM_OK;
+}
+
+// elements of the streamed type per 16-byte access
+int elems16(int dtype) { return dtype == SSM_BF16 ? 8 : 4; }
 
 bool scan_aligned(int dtype, int64_t seqlen, std::initializer_list<const void*> ptrs) {
   const int vec = dtype == SSM_BF16 ? 8 : 4;
@@ -337,6 +361,72 @@ int ssm_selective_state_update(int64_t batch, int64_t dim, int64_t nstate, int d
                                       : (((uintptr_t)B | (uintptr_t)C) & 7) == 0);
   return hip_status(ssm::launch_state_update(p, dtype, vecN, static_cast<hipStream_t>(stream)),
                     "selective_state_update launch");
+}
+
+int ssm_decode_gemv(int64_t batch, int64_t out_dim, int64_t in_dim, int dtype, const void* weight,
+                    const void* x, const void* norm_weight, float norm_eps, const void* bias,
+                    const void* residual, void* y, void* stream) {
+  int rc = check_decode(batch, dtype);
+  if (rc != SSM_OK) return rc;
+  if (!weight || !x || !y) return fail(SSM_ERR_INVALID, "weight, x and y must be non-NULL");
+  const int e = elems16(dtype);
+  if (out_dim < 1 || in_dim < e || in_dim % e || out_dim > INT_MAX / 2 || in_dim > INT_MAX / 2)
+    return fail(SSM_ERR_UNSUPPORTED, "decode_gemv needs in_dim a positive multiple of %d (got %lld x %lld)",
+                e, (long long)out_dim, (long long)in_dim);
+  if (!aligned16(weight) || !aligned16(x) || !aligned16(norm_weight))
+    return fail(SSM_ERR_UNSUPPORTED, "decode_gemv needs 16-byte aligned weight, x and norm_weight");
+  return hip_status(ssm::launch_decode_gemv(dtype == SSM_BF16, weight, x, norm_weight, norm_eps, bias,
+                                            residual, y, (int)batch, (int)out_dim, (int)in_dim,
+                                            static_cast<hipStream_t>(stream)),
+                    "decode_gemv launch");
+}
+
+int ssm_decode_in_proj_conv(int64_t batch, int64_t dim, int64_t in_dim, int64_t width, int dtype,
+                            const void* in_proj_weight, const void* x, const void* norm_weight,
+                            float norm_eps, const void* in_proj_bias, const void* conv_weight,
+                            const void* conv_bias, void* conv_window, void* xz, void* xc,
+                            void* stream) {
+  int rc = check_decode(batch, dtype);
+  if (rc != SSM_OK) return rc;
+  if (!in_proj_weight || !x || !conv_weight || !conv_window || !xz || !xc)
+    return fail(SSM_ERR_INVALID,
+                "in_proj_weight, x, conv_weight, conv_window, xz and xc must be non-NULL");
+  const int e = elems16(dtype);
+  if (in_dim < e || in_dim % e || dim < 1 || dim > INT_MAX / 4 || in_dim > INT_MAX / 2)
+    return fail(SSM_ERR_UNSUPPORTED, "decode_in_proj_conv needs in_dim a positive multiple of %d", e);
+  if (width < 2 || width > ssm::conv1d_max_width())
+    return fail(SSM_ERR_UNSUPPORTED, "decode conv width must be in [2, %d] (got %lld)",
+                ssm::conv1d_max_width(), (long long)width);
+  if (!aligned16(in_proj_weight) || !aligned16(x) || !aligned16(norm_weight))
+    return fail(SSM_ERR_UNSUPPORTED, "decode_in_proj_conv needs 16-byte aligned weight, x and norm_weight");
+  return hip_status(ssm::launch_decode_in_proj_conv(dtype == SSM_BF16, in_proj_weight, x, norm_weight,
+                                                    norm_eps, in_proj_bias, xz, (int)batch, (int)dim,
+                                                    (int)in_dim, (int)width, conv_window, conv_weight,
+                                                    conv_bias, xc, static_cast<hipStream_t>(stream)),
+                    "decode_in_proj_conv launch");
+}
+
+int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank, int dtype,
+                        const void* params, const void* dt_proj_weight, const void* dt_bias,
+                        const void* log_A, const void* D, const void* xc, const void* xz,
+                        int64_t ld_xz, float* state, void* y, void* stream) {
+  int rc = check_decode(batch, dtype);
+  if (rc != SSM_OK) return rc;
+  if (!params || !dt_proj_weight || !log_A || !xc || !xz || !state || !y)
+    return fail(SSM_ERR_INVALID, "params, dt_proj_weight, log_A, xc, xz, state and y must be non-NULL");
+  if (!(nstate == 4 || nstate == 8 || nstate == 16 || nstate == 32 || nstate == 64))
+    return fail(SSM_ERR_UNSUPPORTED, "decode_ssm_step supports nstate in {4, 8, 16, 32, 64} (got %lld)",
+                (long long)nstate);
+  if (dim < 1 || dim > INT_MAX / 4 || rank < 1 || rank > 4096 || ld_xz < 2 * dim)
+    return fail(SSM_ERR_UNSUPPORTED, "decode_ssm_step needs dim >= 1, 1 <= rank <= 4096, ld_xz >= 2 * dim");
+  if (!aligned16(state)) return fail(SSM_ERR_UNSUPPORTED, "decode_ssm_step needs a 16-byte aligned state");
+  const int64_t nout = rank + 2 * nstate;
+  const bool vecR = rank % elems16(dtype) == 0 && aligned16(dt_proj_weight);
+  return hip_status(ssm::launch_decode_ssm_step(dtype == SSM_BF16, params, (int)nout, (int)rank,
+                                                dt_proj_weight, dt_bias, log_A, D, xc, xz, (int)ld_xz,
+                                                state, y, (int)batch, (int)dim, (int)nstate, vecR,
+                                                static_cast<hipStream_t>(stream)),
+                    "decode_ssm_step launch");
 }
 
 size_t ssm_causal_conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t width) {

@@ -1,0 +1,146 @@
+"""Host side of the fused decode-step kernels (``ssm_decode_*`` in
+include/ssm_mamba.h): one Mamba block step per token in four launches
+instead of the reference's per-op sequence (``modules/block.py:80-86``,
+``modules/mamba.py:189-243``), plus the LM-head GEMV with the final RMSNorm
+(``models/causal_lm.py:93-104``).
+
+These are inference kernels (no autograd).  ``block_step_supported`` says
+whether a layer and an input qualify; callers fall back to the op-by-op path
+otherwise.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _native as N
+
+_DTYPES = {torch.float32: N.SSM_F32, torch.bfloat16: N.SSM_BF16}
+MAX_BATCH = 8
+_STATE_SIZES = (4, 8, 16, 32, 64)
+
+# The model harness takes the fused path whenever it qualifies; set False to
+# force the op-by-op path (used to compare the two).
+ENABLED = True
+
+
+def _elems16(dtype: torch.dtype) -> int:
+    return 16 // torch.empty((), dtype=dtype).element_size()
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _aligned(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0
+
+
+def gemv(weight: torch.Tensor, x: torch.Tensor, norm_weight: Optional[torch.Tensor] = None,
+         eps: float = 1e-6, bias: Optional[torch.Tensor] = None,
+         residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = W @ v (+ bias) (+ residual) for x (batch, in) with v = x or, given
+    norm_weight, the reference RMSNorm of x (scale 1 + norm_weight)."""
+    batch, k = x.shape
+    o = weight.shape[0]
+    y = torch.empty(batch, o, device=x.device, dtype=x.dtype)
+    with torch.cuda.device(x.device):
+        N.check(N.lib().ssm_decode_gemv(batch, o, k, _DTYPES[x.dtype], weight.data_ptr(),
+                                        x.data_ptr(), _ptr(norm_weight), float(eps), _ptr(bias),
+                                        _ptr(residual), y.data_ptr(), _stream(x.device)))
+    return y
+
+
+def in_proj_conv(weight: torch.Tensor, x: torch.Tensor, norm_weight: Optional[torch.Tensor],
+                 eps: float, bias: Optional[torch.Tensor], conv_weight: torch.Tensor,
+                 conv_bias: Optional[torch.Tensor], window: torch.Tensor):
+    """(xz (batch, 2*dim), xc (batch, dim)) of the in-projection and conv step;
+    the conv window advances in place."""
+    batch, k = x.shape
+    dim = weight.shape[0] // 2
+    width = conv_weight.shape[-1]
+    xz = torch.empty(batch, 2 * dim, device=x.device, dtype=x.dtype)
+    xc = torch.empty(batch, dim, device=x.device, dtype=x.dtype)
+    with torch.cuda.device(x.device):
+        N.check(N.lib().ssm_decode_in_proj_conv(batch, dim, k, width, _DTYPES[x.dtype],
+                                                weight.data_ptr(), x.data_ptr(), _ptr(norm_weight),
+                                                float(eps), _ptr(bias), conv_weight.data_ptr(),
+                                                _ptr(conv_bias), window.data_ptr(), xz.data_ptr(),
+                                                xc.data_ptr(), _stream(x.device)))
+    return xz, xc
+
+
+def ssm_step(params: torch.Tensor, rank: int, dt_proj_weight: torch.Tensor,
+             dt_bias: Optional[torch.Tensor], log_A: torch.Tensor, D: Optional[torch.Tensor],
+             xc: torch.Tensor, xz: torch.Tensor, state: torch.Tensor) -> torch.Tensor:
+    """y (batch, dim) of the state update + gate; state advances in place."""
+    batch, dim = xc.shape
+    nstate = state.shape[-1]
+    y = torch.empty_like(xc)
+    with torch.cuda.device(xc.device):
+        N.check(N.lib().ssm_decode_ssm_step(batch, dim, nstate, rank, _DTYPES[xc.dtype],
+                                            params.data_ptr(), dt_proj_weight.data_ptr(),
+                                            _ptr(dt_bias), log_A.data_ptr(), _ptr(D),
+                                            xc.data_ptr(), xz.data_ptr(), xz.stride(0),
+                                            state.data_ptr(), y.data_ptr(), _stream(xc.device)))
+    return y
+
+
+def gemv_supported(weight: torch.Tensor, x: torch.Tensor, *others) -> bool:
+    if not ENABLED or torch.is_grad_enabled():
+        return False
+    if not (x.is_cuda and x.dim() == 2 and x.dtype in _DTYPES and 1 <= x.shape[0] <= MAX_BATCH):
+        return False
+    e = _elems16(x.dtype)
+    k = x.shape[1]
+    if k % e or weight.dim() != 2 or weight.shape[1] != k:
+        return False
+    for t in (weight, x) + tuple(o for o in others if o is not None):
+        if t.dtype != x.dtype or not t.is_contiguous() or t.device != x.device:
+            return False
+    return _aligned(weight) and _aligned(x) and all(_aligned(o) for o in others if o is not None)
+
+
+def block_step_supported(ssm, x: torch.Tensor, norm_weight: Optional[torch.Tensor]) -> bool:
+    """Whether the fused kernels can run Mamba ``ssm`` on the token batch x."""
+    if torch.is_grad_enabled():
+        return False
+    ctx, state = ssm._conv_context, ssm._ssm_hiddens
+    if ctx is None or state is None:
+        return False
+    inner = ssm.inner_dim
+    batch = x.shape[0] if x.dim() == 2 else 0
+    e = _elems16(x.dtype) if x.dtype in _DTYPES else 0
+    if not e or not (2 <= ssm.conv_kernel <= 8) or ssm.state_dim not in _STATE_SIZES:
+        return False
+    if inner % e:
+        return False
+    params = [ssm.input_proj.weight, ssm.input_proj.bias, ssm.conv.weight, ssm.conv.bias,
+              ssm.ssm_param_proj.weight, ssm.delta_proj.weight, ssm.delta_proj.bias, ssm.log_A,
+              ssm.D, ssm.out_proj.weight, ssm.out_proj.bias, norm_weight]
+    if not gemv_supported(ssm.input_proj.weight, x, *params):
+        return False
+    if tuple(ctx.shape) != (batch, inner, ssm.conv_kernel - 1) or ctx.dtype != x.dtype \
+            or not ctx.is_contiguous():
+        return False
+    if tuple(state.shape) != (batch, inner, ssm.state_dim) or state.dtype != torch.float32 \
+            or not state.is_contiguous() or not _aligned(state):
+        return False
+    return True
+
+
+def block_step(ssm, x: torch.Tensor, norm_weight: Optional[torch.Tensor] = None,
+               eps: float = 1e-6, residual: bool = False) -> torch.Tensor:
+    """Mamba.step(norm(x)) (+ x when residual): the fused path of
+    ``Block.step`` (norm_weight and residual given) or ``Mamba.step``."""
+    xz, xc = in_proj_conv(ssm.input_proj.weight, x, norm_weight, eps, ssm.input_proj.bias,
+                          ssm.conv.weight, ssm.conv.bias, ssm._conv_context)
+    params = gemv(ssm.ssm_param_proj.weight, xc)                          # (batch, R + 2N)
+    y = ssm_step(params, ssm.delta_rank, ssm.delta_proj.weight, ssm.delta_proj.bias, ssm.log_A,
+                 ssm.D, xc, xz, ssm._ssm_hiddens)
+    return gemv(ssm.out_proj.weight, y, bias=ssm.out_proj.bias, residual=x if residual else None)

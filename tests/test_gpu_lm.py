@@ -182,3 +182,93 @@ def test_training_gradients_fp32(cuda):
         gr = sd[k].grad
         rms = float(gr.pow(2).mean().sqrt())
         _close(names[k].grad, gr, f"grad {k}", rtol=2e-3, atol=2e-4 * max(rms, 1e-3))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batch,kw", [
+    (1, dict(bias=True, conv_bias=True)),
+    (3, dict(bias=False, conv_bias=False)),
+    (8, dict(bias=True, conv_bias=False)),
+])
+def test_fused_decode_matches_eager_and_oracle(cuda, dtype, batch, kw):
+    """The four fused decode kernels per layer (and the fused LM head) against
+    the op-by-op step and the oracle's step chain."""
+    from ssm_mamba_amd import decode as DEC
+    m, cfg = make_lm(seed=20 + batch, vocab=67, model_dim=64, state_dim=16, layers=2, **kw)
+    m = m.to(cuda, dtype)
+    sd = lm_state64(m)
+    ids = _ids(batch, 19, cfg.vocab_size, seed=21)
+    lengths = (ids != cfg.pad_token_id).sum(dim=1)
+    toks = torch.randint(0, cfg.vocab_size, (5, batch), generator=torch.Generator().manual_seed(22))
+    outs = {}
+    for fused in (True, False):
+        DEC.ENABLED = fused
+        try:
+            with torch.no_grad():
+                m(ids.to(cuda), lengths.to(cuda), use_cache=True)
+                outs[fused] = [m.step(t.to(cuda)).float() for t in toks]
+                outs[(fused, "state")] = torch.stack([l.ssm._ssm_hiddens.clone() for l in m.layers])
+                outs[(fused, "ctx")] = torch.stack([l.ssm._conv_context.float() for l in m.layers])
+        finally:
+            DEC.ENABLED = True
+    _, caches = LR.lm_forward(sd, ids, lengths, use_cache=True)
+    if dtype == torch.float32:
+        tol = dict(rtol=1e-3, atol=1e-4)
+    else:
+        tol = dict(rtol=3e-2, atol=3e-2 * float(outs[False][0].abs().max()))
+    for i, t in enumerate(toks):
+        ref, caches = LR.lm_step(sd, t, caches)
+        _close(outs[True][i], ref, f"fused step {i}", **tol)
+        _close(outs[True][i], outs[False][i], f"fused vs eager step {i}", **tol)
+    _close(outs[(True, "state")], torch.stack([c[1] for c in caches]), "fused state", **tol)
+    _close(outs[(True, "ctx")], torch.stack([c[0] for c in caches]), "fused window",
+           rtol=tol["rtol"], atol=1e-6 if dtype == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batch", [1, 2, 5, 8])
+@pytest.mark.parametrize("out_dim,in_dim", [(1, 8), (37, 64), (300, 1032), (64, 4096)])
+def test_decode_gemv(cuda, dtype, batch, out_dim, in_dim):
+    from ssm_mamba_amd import decode as DEC
+    g = torch.Generator().manual_seed(out_dim + in_dim + batch)
+    W = torch.randn(out_dim, in_dim, generator=g).to(dtype)
+    x = torch.randn(batch, in_dim, generator=g).to(dtype)
+    nw = (0.3 * torch.randn(in_dim, generator=g)).to(dtype)
+    bias = torch.randn(out_dim, generator=g).to(dtype)
+    res = torch.randn(batch, out_dim, generator=g).to(dtype)
+    d = lambda t: t.to(cuda)
+    with torch.no_grad():
+        for use_norm in (False, True):
+            for use_extra in (False, True):
+                got = DEC.gemv(d(W), d(x), norm_weight=d(nw) if use_norm else None, eps=1e-6,
+                               bias=d(bias) if use_extra else None,
+                               residual=d(res) if use_extra else None)
+                v = x.double()
+                if use_norm:
+                    v = LR.rms_norm(v, nw.double())
+                ref = v @ W.double().t()
+                if use_extra:
+                    ref = ref + bias.double() + res.double()
+                scale = float(ref.abs().max())
+                if dtype == torch.float32:
+                    _close(got, ref, "gemv", rtol=1e-4, atol=1e-5 * max(1.0, scale))
+                else:
+                    _close(got, ref, "gemv", rtol=1e-2, atol=1e-2 * max(1.0, scale))
+
+
+def test_fused_decode_falls_back_outside_its_limits(cuda):
+    """Batch 9 exceeds the fused kernels' limit: the step takes the op-by-op
+    path and still matches the oracle."""
+    from ssm_mamba_amd import decode as DEC
+    m, cfg = make_lm(seed=30, vocab=29, model_dim=32, state_dim=16, layers=1)
+    m = m.to(cuda)
+    sd = lm_state64(m)
+    ids = _ids(9, 11, cfg.vocab_size, seed=31, pads=False)
+    with torch.no_grad():
+        m(ids.to(cuda), use_cache=True)
+        assert not DEC.block_step_supported(m.layers[0].ssm, torch.zeros(9, 32, device=cuda),
+                                            m.layers[0].norm.weight)
+        got = m.step(ids[:, 0].to(cuda))
+    _, caches = LR.lm_forward(sd, ids, use_cache=True)
+    ref, _ = LR.lm_step(sd, ids[:, 0], caches)
+    _close(got, ref, "batch-9 step", **F32)
