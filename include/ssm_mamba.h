@@ -160,11 +160,11 @@ int ssm_causal_conv1d_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t wi
  * modules/mamba.py:189-243) runs about twenty torch ops per layer and token;
  * these four calls do the same work:
  *
- *   ssm_decode_in_proj_conv   xz = W_in @ rmsnorm(x) [+ b_in]; conv step -> xc;
- *                             the conv window rolls
- *   ssm_decode_gemv           params = W_x @ xc                  (batch, rank + 2*nstate)
- *   ssm_decode_ssm_step       state update, y = (C.h + D xc) * silu(z)
- *   ssm_decode_gemv           x' = x + W_out @ y [+ b_out]       (residual set)
+ *   ssm_decode_in_proj_conv  xz = W_in @ rmsnorm(x) [+ b_in]; conv step -> xc;
+ *                            the conv window rolls
+ *   ssm_decode_gemv          params = W_x @ xc                 (batch, rank + 2*nstate)
+ *   ssm_decode_ssm_step      state update, y = (C.h + D xc) * silu(z)
+ *   ssm_decode_gemv          x' = x + W_out @ y [+ b_out]      (residual set)
  *
  * Every tensor except state has element type `dtype` (weights and the norm,
  * conv, dt and A/D parameters included); state (batch, dim, nstate) is fp32.
@@ -186,7 +186,7 @@ int ssm_decode_gemv(int64_t batch, int64_t out_dim, int64_t in_dim, int dtype, c
 /*
  * In-projection with the conv step (modules/mamba.py:199-214): xz (batch,
  * 2*dim) = in_proj_weight (2*dim, in_dim) @ v [+ in_proj_bias], v = x or its
- * RMSNorm (norm_weight non-NULL, as in ssm_decode_gemv); then for the x half
+ * RMSNorm (norm_weight non-NULL, as in ssm_decode_gemv); for the x half
  * xs = xz[:, :dim]: xc (batch, dim) = silu(sum_{j<width-1} conv_weight[c, j] *
  * conv_window[b, c, j] + conv_weight[c, width-1] * xs + conv_bias[c]) and the
  * window rolls: conv_window (batch, dim, width-1) <- [window[..., 1:], xs].
@@ -204,9 +204,9 @@ int ssm_decode_in_proj_conv(int64_t batch, int64_t dim, int64_t in_dim, int64_t 
  * params[:, :rank]; delta' = softplus(delta + dt_bias); A = -exp(log_A);
  * state = exp(delta' A) state + delta' xc B with B = params[:, rank:rank+nstate];
  * y = (sum_n C state + D xc) * silu(z), C = params[:, rank+nstate:],
- * z = xz[:, dim:2*dim] (row stride ld_xz).  state updated in place.
- * params (batch, rank + 2*nstate); dt_bias, D nullable; nstate in
- * {4, 8, 16, 32, 64}.
+ * z = xz[:, dim:2*dim] (row stride ld_xz).  params (batch, rank + 2*nstate);
+ * state (batch, dim, nstate) fp32 updated in place; y (batch, dim).  dt_bias,
+ * D nullable; nstate in {4, 8, 16, 32, 64}.
  */
 int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank, int dtype,
                         const void* params, const void* dt_proj_weight, const void* dt_bias,

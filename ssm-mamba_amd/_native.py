@@ -72,7 +72,8 @@ SIGNATURES = {
     "ssm_decode_in_proj_conv": (_i32, [
         _i64, _i64, _i64, _i64, _i32,          # batch, dim, in_dim, width, dtype
         _p, _p, _p, ctypes.c_float, _p,        # in_proj_weight, x, norm_weight, norm_eps, in_proj_bias
-        _p, _p, _p, _p, _p, _p,                # conv_weight, conv_bias, window, xz, xc, stream
+        _p, _p, _p,                            # conv_weight, conv_bias, window
+        _p, _p, _p,                            # xz, xc, stream
     ]),
     "ssm_decode_ssm_step": (_i32, [
         _i64, _i64, _i64, _i64, _i32,          # batch, dim, nstate, rank, dtype

@@ -392,8 +392,10 @@ int ssm_decode_in_proj_conv(int64_t batch, int64_t dim, int64_t in_dim, int64_t 
     return fail(SSM_ERR_INVALID,
                 "in_proj_weight, x, conv_weight, conv_window, xz and xc must be non-NULL");
   const int e = elems16(dtype);
-  if (in_dim < e || in_dim % e || dim < 1 || dim > INT_MAX / 4 || in_dim > INT_MAX / 2)
+  if (in_dim < e || in_dim % e || in_dim > INT_MAX / 2)
     return fail(SSM_ERR_UNSUPPORTED, "decode_in_proj_conv needs in_dim a positive multiple of %d", e);
+  if (dim < 1 || dim > INT_MAX / 4)
+    return fail(SSM_ERR_UNSUPPORTED, "decode_in_proj_conv needs 1 <= dim < 2^29");
   if (width < 2 || width > ssm::conv1d_max_width())
     return fail(SSM_ERR_UNSUPPORTED, "decode conv width must be in [2, %d] (got %lld)",
                 ssm::conv1d_max_width(), (long long)width);
@@ -417,10 +419,11 @@ int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank
   if (!(nstate == 4 || nstate == 8 || nstate == 16 || nstate == 32 || nstate == 64))
     return fail(SSM_ERR_UNSUPPORTED, "decode_ssm_step supports nstate in {4, 8, 16, 32, 64} (got %lld)",
                 (long long)nstate);
-  if (dim < 1 || dim > INT_MAX / 4 || rank < 1 || rank > 4096 || ld_xz < 2 * dim)
-    return fail(SSM_ERR_UNSUPPORTED, "decode_ssm_step needs dim >= 1, 1 <= rank <= 4096, ld_xz >= 2 * dim");
-  if (!aligned16(state)) return fail(SSM_ERR_UNSUPPORTED, "decode_ssm_step needs a 16-byte aligned state");
   const int64_t nout = rank + 2 * nstate;
+  if (dim < 1 || dim > INT_MAX / 4 || rank < 1 || nout > 16384 || ld_xz < 2 * dim)
+    return fail(SSM_ERR_UNSUPPORTED,
+                "decode_ssm_step needs dim >= 1, rank >= 1, rank + 2 * nstate <= 16384, ld_xz >= 2 * dim");
+  if (!aligned16(state)) return fail(SSM_ERR_UNSUPPORTED, "decode_ssm_step needs a 16-byte aligned state");
   const bool vecR = rank % elems16(dtype) == 0 && aligned16(dt_proj_weight);
   return hip_status(ssm::launch_decode_ssm_step(dtype == SSM_BF16, params, (int)nout, (int)rank,
                                                 dt_proj_weight, dt_bias, log_A, D, xc, xz, (int)ld_xz,

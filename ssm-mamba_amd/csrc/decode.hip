@@ -6,9 +6,9 @@
 //                                      xc = silu(window . w + xs w_last + b),
 //                                      window roll
 //   gemv_kernel                        p = W_x @ xc                    (B, R+2N)
-//   ssm_step_kernel                    delta = W_dt @ p[:R]; state update with
-//                                      B = p[R:R+N], C = p[R+N:];
-//                                      y = (C.h + D*xc) * silu(z)
+//   ssm_step_kernel                    delta = W_dt @ p[:R];
+//                                      state update with B = p[R:R+N],
+//                                      C = p[R+N:]; y = (C.h + D*xc) * silu(z)
 //   gemv_kernel (residual)             x' = x + W_out @ y
 //
 // and the LM head as gemv_kernel with the final norm.  Batch is small (one
@@ -63,6 +63,22 @@ __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
+}
+
+// Totals over the wave of NV per-lane values: afterwards out[g] of lane l is
+// the sum over all lanes of v[g * 16 + (l >> 2)] (zero past NV); the four
+// lanes of a quad agree.  permlane/DPP reduce-scatter, no LDS round trips.
+template <int NV>
+__device__ __forceinline__ void wave_totals(const float (&v)[NV], float (&out)[(NV + 15) / 16],
+                                            int lane) {
+#pragma unroll
+  for (int g = 0; g < (NV + 15) / 16; ++g) {
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] = g * 16 + i < NV ? v[g * 16 + i] : 0.0f;
+    wave_reduce16(t, lane);
+    out[g] = t[0];
+  }
 }
 
 // value rounded to T and back (the reference keeps these intermediates as T tensors)
@@ -126,6 +142,47 @@ __global__ __launch_bounds__(kDecThreads) void gemv_kernel(const GemvArgs a) {
     for (int r = 0; r < kRows; ++r) acc[r][b] = 0.0f;
   }
 
+  // epilogue operands (bias, residual, conv taps and window) of this lane's
+  // outputs, fetched before the weight stream so their latency overlaps it
+  constexpr int kNV = kRows * kMB;
+  constexpr int kNG = (kNV + 15) / 16;
+  constexpr int kMaxTaps = 8;
+  int e_row[kNG], e_b[kNG];
+  bool e_ok[kNG];
+  float e_bias[kNG], e_res[kNG], e_cb[kNG];
+  float e_cw[kNG][kMaxTaps], e_win[kNG][kMaxTaps - 1];
+#pragma unroll
+  for (int g = 0; g < kNG; ++g) {
+    const int i = g * 16 + (lane >> 2);
+    const int rl = i / kMB;
+    e_row[g] = row0 + rl;
+    e_b[g] = i - rl * kMB;
+    e_ok[g] = (lane & 3) == 0 && i < kNV && e_row[g] < O && e_b[g] < B;
+    const bool ok = e_ok[g];
+    e_bias[g] = ok && a.bias ? Elem<T>::load1(static_cast<const T*>(a.bias) + e_row[g]) : 0.0f;
+    e_res[g] = 0.0f;
+    e_cb[g] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxTaps; ++j) e_cw[g][j] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxTaps - 1; ++j) e_win[g][j] = 0.0f;
+    if constexpr (kEpi == kEpiPlain) {
+      if (ok && a.res)
+        e_res[g] = Elem<T>::load1(static_cast<const T*>(a.res) + (size_t)e_b[g] * O + e_row[g]);
+    } else {
+      if (ok && e_row[g] < a.dim) {
+        const int wd = a.width;
+        const T* __restrict__ cw = static_cast<const T*>(a.cw) + (size_t)e_row[g] * wd;
+        const T* __restrict__ win =
+            static_cast<const T*>(a.ctx) + ((size_t)e_b[g] * a.dim + e_row[g]) * (wd - 1);
+#pragma unroll
+        for (int j = 0; j < kMaxTaps; ++j) e_cw[g][j] = Elem<T>::load1(cw + min(j, wd - 1));
+#pragma unroll
+        for (int j = 0; j < kMaxTaps - 1; ++j) e_win[g][j] = Elem<T>::load1(win + min(j, wd - 2));
+        e_cb[g] = a.cb ? Elem<T>::load1(static_cast<const T*>(a.cb) + e_row[g]) : 0.0f;
+      }
+    }
+  }
   for (int kb = 0; kb < K; kb += PK) {
     Raw wr[kRows][kGemvPass];
 #pragma unroll
@@ -133,8 +190,12 @@ __global__ __launch_bounds__(kDecThreads) void gemv_kernel(const GemvArgs a) {
       const int row = min(row0 + r, O - 1);
 #pragma unroll
       for (int c = 0; c < kGemvPass; ++c) {
-        const int k0 = min(kb + c * span + lane * E, K - E);
-        wr[r][c] = ldchunk(W + (size_t)row * K + k0);
+        if (kb + c * span < K) {  // wave-uniform: whole chunks past K are not loaded
+          const int k0 = min(kb + c * span + lane * E, K - E);
+          wr[r][c] = ldchunk(W + (size_t)row * K + k0);
+        } else {
+          wr[r][c] = Chunk<T>::zero();
+        }
       }
     }
     // stage x[:, kb:kb+PK]: thread t owns chunk t of every batch row (PK / E == 256)
@@ -191,11 +252,9 @@ __global__ __launch_bounds__(kDecThreads) void gemv_kernel(const GemvArgs a) {
   }
 
   if constexpr (kNorm) {
-#pragma unroll
-    for (int b = 0; b < kMB; ++b) {
-      const float t = wave_sum(ssq[b]);
-      if (lane == 0) s_red[wave][b] = t;
-    }
+    float st[(kMB + 15) / 16];
+    wave_totals<kMB>(ssq, st, lane);
+    if ((lane & 3) == 0 && (lane >> 2) < kMB) s_red[wave][lane >> 2] = st[0];
     __syncthreads();
     if (threadIdx.x < kMB) {
       const int b = threadIdx.x;
@@ -204,54 +263,58 @@ __global__ __launch_bounds__(kDecThreads) void gemv_kernel(const GemvArgs a) {
     }
     __syncthreads();
   }
-  // every lane gets every total; lane r * kMB + b finishes output (row0 + r, b)
-  float tot[kRows][kMB];
+  // wave totals: lane 4i (+0..3) of group g finishes output i = g * 16 + (lane >> 2),
+  // i = r * kMB + b; its operands were fetched before the weight stream (below)
+  float tot[kNG];
+  {
+    float flat[kNV];
 #pragma unroll
-  for (int r = 0; r < kRows; ++r)
+    for (int r = 0; r < kRows; ++r)
 #pragma unroll
-    for (int b = 0; b < kMB; ++b) {
-      tot[r][b] = wave_sum(acc[r][b]);
-      if constexpr (kNorm) tot[r][b] *= s_scale[b];
-    }
-  if (lane >= kRows * kMB) return;
-  const int rl = lane / kMB;
-  const int bl = lane - rl * kMB;
-  float s = 0.0f;
-#pragma unroll
-  for (int r = 0; r < kRows; ++r)
-#pragma unroll
-    for (int b = 0; b < kMB; ++b)
-      if (r == rl && b == bl) s = tot[r][b];
-  const int row = row0 + rl;
-  if (row >= O || bl >= B) return;
-  if (a.bias) s += Elem<T>::load1(static_cast<const T*>(a.bias) + row);
+      for (int b = 0; b < kMB; ++b) flat[r * kMB + b] = acc[r][b];
+    wave_totals<kNV>(flat, tot, lane);
+  }
   T* __restrict__ y = static_cast<T*>(a.y);
-  if constexpr (kEpi == kEpiPlain) {
-    if (a.res) s += Elem<T>::load1(static_cast<const T*>(a.res) + (size_t)bl * O + row);
-    Elem<T>::store1(y + (size_t)bl * O + row, s);
-  } else {
-    Elem<T>::store1(y + (size_t)bl * O + row, s);
-    if (row < a.dim) {
-      const int wd = a.width;
-      const float xs = round_to<T>(s);
-      const T* __restrict__ cw = static_cast<const T*>(a.cw) + (size_t)row * wd;
-      T* __restrict__ win = static_cast<T*>(a.ctx) + ((size_t)bl * a.dim + row) * (wd - 1);
-      float cv = a.cb ? Elem<T>::load1(static_cast<const T*>(a.cb) + row) : 0.0f;
-      for (int j = 0; j < wd - 1; ++j) cv = fmaf(Elem<T>::load1(cw + j), Elem<T>::load1(win + j), cv);
-      cv = fmaf(Elem<T>::load1(cw + wd - 1), xs, cv);
-      Elem<T>::store1(static_cast<T*>(a.xc) + (size_t)bl * a.dim + row, silu_f(cv));
-      for (int j = 0; j + 1 < wd - 1; ++j) win[j] = win[j + 1];
-      Elem<T>::store1(win + wd - 2, xs);
+#pragma unroll
+  for (int g = 0; g < kNG; ++g) {
+    if (!e_ok[g]) continue;
+    const int row = e_row[g], bl = e_b[g];
+    float s = tot[g];
+    if constexpr (kNorm) s *= s_scale[bl];
+    s += e_bias[g];
+    if constexpr (kEpi == kEpiPlain) {
+      Elem<T>::store1(y + (size_t)bl * O + row, s + e_res[g]);
+    } else {
+      Elem<T>::store1(y + (size_t)bl * O + row, s);
+      if (row < a.dim) {
+        const int wd = a.width;
+        const float xs = round_to<T>(s);
+        float cv = e_cb[g];
+        float wlast = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMaxTaps; ++j) {
+          if (j < wd - 1) cv = fmaf(e_cw[g][j], e_win[g][j], cv);
+          if (j == wd - 1) wlast = e_cw[g][j];
+        }
+        cv = fmaf(wlast, xs, cv);
+        const float xcv = round_to<T>(silu_f(cv));
+        Elem<T>::store1(static_cast<T*>(a.xc) + (size_t)bl * a.dim + row, xcv);
+        T* __restrict__ win = static_cast<T*>(a.ctx) + ((size_t)bl * a.dim + row) * (wd - 1);
+#pragma unroll
+        for (int j = 0; j + 1 < kMaxTaps - 1; ++j)
+          if (j + 1 < wd - 1) Elem<T>::store1(win + j, e_win[g][j + 1]);
+        Elem<T>::store1(win + wd - 2, xs);
+      }
     }
   }
 }
 
-// One thread per (b, d): delta = W_dt[d, :R] . params[b, :R] (a T value, as the
-// reference's dt projection output), then the selective state update
-// (modules/mamba.py:223-240 with selective_update/kernel.cu:39-71:
-// delta' = softplus(delta + dt_bias), h' = exp(delta' A) h + delta' xc B,
-// y = (sum_n C h' + D xc) * silu(z)) with A = -exp(log_A), B = params[b, R:R+N],
-// C = params[b, R+N:R+2N].
+// Step-size projection, state update and gate, one thread per (b, d):
+//   delta = round_T(W_dt[d, :R] . p[b, :R]); delta' = softplus(delta + dt_bias[d])
+//   h' = exp(delta' A) h + delta' xc B,  A = -exp(log_A), B = p[b, R:R+N]
+//   y = (sum_n C h' + D xc) * silu(z),   C = p[b, R+N:R+2N], z = xz[b, dim + d]
+// (modules/mamba.py:216-240 with selective_update/kernel.cu:39-71; the T
+// roundings mirror the reference's intermediate T tensors).
 template <typename T, int kN, bool kVecR>
 __global__ __launch_bounds__(kDecThreads) void ssm_step_kernel(
     const T* __restrict__ p, int nout, int R, const T* __restrict__ Wdt,
@@ -262,12 +325,13 @@ __global__ __launch_bounds__(kDecThreads) void ssm_step_kernel(
   const int b = blockIdx.y;
   for (int i = threadIdx.x; i < nout; i += kDecThreads) s_p[i] = Elem<T>::load1(p + (size_t)b * nout + i);
   __syncthreads();
+
   const int d = blockIdx.x * kDecThreads + threadIdx.x;
   if (d >= dim) return;
+  constexpr int E = Chunk<T>::E;
   float dl = 0.0f;
   const T* __restrict__ wrow = Wdt + (size_t)d * R;
   if constexpr (kVecR) {
-    constexpr int E = Chunk<T>::E;
     for (int r0 = 0; r0 < R; r0 += E) {
       float w[E];
       Chunk<T>::cvt(ldchunk(wrow + r0), w);
@@ -367,7 +431,7 @@ hipError_t launch_ssm_step_t(const void* p, int nout, int R, const void* Wdt, co
   switch (nstate) {
 #define SSM_DEC_N(n)                                                                               \
   case n:                                                                                          \
-    return launch_ssm_step_n<T, n>(p, nout, R, Wdt, dtb, logA, D, xc, xz, ld, state, y, B, dim,   \
+    return launch_ssm_step_n<T, n>(p, nout, R, Wdt, dtb, logA, D, xc, xz, ld, state, y, B, dim,    \
                                    vecR, st);
     SSM_DEC_N(4)
     SSM_DEC_N(8)

@@ -118,7 +118,7 @@ def block_step_supported(ssm, x: torch.Tensor, norm_weight: Optional[torch.Tenso
     e = _elems16(x.dtype) if x.dtype in _DTYPES else 0
     if not e or not (2 <= ssm.conv_kernel <= 8) or ssm.state_dim not in _STATE_SIZES:
         return False
-    if inner % e:
+    if inner % e or ssm.delta_rank + 2 * ssm.state_dim > 16384:
         return False
     params = [ssm.input_proj.weight, ssm.input_proj.bias, ssm.conv.weight, ssm.conv.bias,
               ssm.ssm_param_proj.weight, ssm.delta_proj.weight, ssm.delta_proj.bias, ssm.log_A,
