@@ -424,7 +424,8 @@ int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank
     return fail(SSM_ERR_UNSUPPORTED,
                 "decode_ssm_step needs dim >= 1, rank >= 1, rank + 2 * nstate <= 16384, ld_xz >= 2 * dim");
   if (!aligned16(state)) return fail(SSM_ERR_UNSUPPORTED, "decode_ssm_step needs a 16-byte aligned state");
-  const bool vecR = rank % elems16(dtype) == 0 && aligned16(dt_proj_weight);
+  const bool vecR = rank % elems16(dtype) == 0 && rank <= 16 * elems16(dtype) &&
+                    aligned16(dt_proj_weight);
   return hip_status(ssm::launch_decode_ssm_step(dtype == SSM_BF16, params, (int)nout, (int)rank,
                                                 dt_proj_weight, dt_bias, log_A, D, xc, xz, (int)ld_xz,
                                                 state, y, (int)batch, (int)dim, (int)nstate, vecR,

@@ -321,48 +321,67 @@ __global__ __launch_bounds__(kDecThreads) void ssm_step_kernel(
     const T* __restrict__ dt_bias, const T* __restrict__ logA, const T* __restrict__ Dv,
     const T* __restrict__ xc, const T* __restrict__ xz, int ld_xz, float* __restrict__ state,
     T* __restrict__ y, int dim) {
+  constexpr int E = Chunk<T>::E;
+  constexpr int kMaxRC = 16;  // dt-projection chunks held in registers (R <= 16 E)
   extern __shared__ float s_p[];  // [nout]
   const int b = blockIdx.y;
+  const int d = blockIdx.x * kDecThreads + threadIdx.x;
+  const int dc = min(d, dim - 1);
+  // this thread's operands first (none depends on p), so their latency
+  // overlaps the staging of p and the barrier
+  typename Chunk<T>::Raw wv[kVecR ? kMaxRC : 1];
+  const T* __restrict__ wrow = Wdt + (size_t)dc * R;
+  if constexpr (kVecR) {
+#pragma unroll
+    for (int c = 0; c < kMaxRC; ++c) wv[c] = c * E < R ? ldchunk(wrow + c * E) : Chunk<T>::zero();
+  }
+  float* __restrict__ h = state + ((size_t)b * dim + dc) * kN;
+  float4 hv[kN / 4];
+#pragma unroll
+  for (int q = 0; q < kN / 4; ++q) hv[q] = *reinterpret_cast<const float4*>(h + 4 * q);
+  float la[kN];
+#pragma unroll
+  for (int n = 0; n < kN; ++n) la[n] = Elem<T>::load1(logA + (size_t)dc * kN + n);
+  const float bias = dt_bias ? Elem<T>::load1(dt_bias + dc) : 0.0f;
+  const float dv = Dv ? Elem<T>::load1(Dv + dc) : 0.0f;
+  const float u = Elem<T>::load1(xc + (size_t)b * dim + dc);
+  const float z = Elem<T>::load1(xz + (size_t)b * ld_xz + dim + dc);
+
   for (int i = threadIdx.x; i < nout; i += kDecThreads) s_p[i] = Elem<T>::load1(p + (size_t)b * nout + i);
   __syncthreads();
-
-  const int d = blockIdx.x * kDecThreads + threadIdx.x;
   if (d >= dim) return;
-  constexpr int E = Chunk<T>::E;
+
   float dl = 0.0f;
-  const T* __restrict__ wrow = Wdt + (size_t)d * R;
   if constexpr (kVecR) {
-    for (int r0 = 0; r0 < R; r0 += E) {
-      float w[E];
-      Chunk<T>::cvt(ldchunk(wrow + r0), w);
 #pragma unroll
-      for (int i = 0; i < E; ++i) dl = fmaf(w[i], s_p[r0 + i], dl);
+    for (int c = 0; c < kMaxRC; ++c) {
+      if (c * E < R) {
+        float w[E];
+        Chunk<T>::cvt(wv[c], w);
+#pragma unroll
+        for (int i = 0; i < E; ++i) dl = fmaf(w[i], s_p[c * E + i], dl);
+      }
     }
   } else {
     for (int r = 0; r < R; ++r) dl = fmaf(Elem<T>::load1(wrow + r), s_p[r], dl);
   }
   dl = round_to<T>(dl);
-  const float dt = softplus_t20(dl + (dt_bias ? Elem<T>::load1(dt_bias + d) : 0.0f));
-  const float u = Elem<T>::load1(xc + (size_t)b * dim + d);
+  const float dt = softplus_t20(dl + bias);
   const float du = dt * u;
-  float* __restrict__ h = state + ((size_t)b * dim + d) * kN;
   float out = 0.0f;
 #pragma unroll
-  for (int n0 = 0; n0 < kN; n0 += 4) {
-    const float4 hv = *reinterpret_cast<const float4*>(h + n0);
-    float hn[4] = {hv.x, hv.y, hv.z, hv.w};
+  for (int q = 0; q < kN / 4; ++q) {
+    float hn[4] = {hv[q].x, hv[q].y, hv[q].z, hv[q].w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = n0 + q;
-      const float A = -fast_exp2(Elem<T>::load1(logA + (size_t)d * kN + n) * kLog2e);
-      const float a = fast_exp2(dt * A * kLog2e);
-      hn[q] = fmaf(a, hn[q], du * s_p[R + n]);
-      out = fmaf(s_p[R + kN + n], hn[q], out);
+    for (int i = 0; i < 4; ++i) {
+      const int n = 4 * q + i;
+      const float a = fast_exp2(-dt * fast_exp2(la[n] * kLog2e) * kLog2e);  // exp(dt * A), A = -exp(log_A)
+      hn[i] = fmaf(a, hn[i], du * s_p[R + n]);
+      out = fmaf(s_p[R + kN + n], hn[i], out);
     }
-    *reinterpret_cast<float4*>(h + n0) = make_float4(hn[0], hn[1], hn[2], hn[3]);
+    *reinterpret_cast<float4*>(h + 4 * q) = make_float4(hn[0], hn[1], hn[2], hn[3]);
   }
-  if (Dv) out = fmaf(Elem<T>::load1(Dv + d), u, out);
-  const float z = Elem<T>::load1(xz + (size_t)b * ld_xz + dim + d);
+  out = fmaf(dv, u, out);
   Elem<T>::store1(y + (size_t)b * dim + d, out * silu_f(z));
 }
 
@@ -386,8 +405,10 @@ hipError_t launch_gemv_r(const GemvArgs& a, bool norm, bool conv, hipStream_t st
 
 template <typename T, int kMB>
 hipError_t launch_gemv_b(const GemvArgs& a, bool norm, bool conv, hipStream_t st) {
-  // four rows per wave for tall matrices (the LM head), two otherwise
+  // rows per wave: four for tall matrices (the LM head), one for short ones
+  // (more workgroups in flight), two otherwise
   if (a.O >= 16384) return launch_gemv_r<T, kMB, 4>(a, norm, conv, st);
+  if (a.O <= 2048 && !conv) return launch_gemv_r<T, kMB, 1>(a, norm, conv, st);
   return launch_gemv_r<T, kMB, 2>(a, norm, conv, st);
 }
 
