@@ -124,6 +124,16 @@ int ssm_selective_state_update(int64_t batch, int64_t dim, int64_t nstate, int d
                                int dt_softplus, void* out, void* stream);
 
 /*
+ * RMSNorm over the channel axis of channel-major x (batch, channels, seqlen):
+ * out[b, c, t] = x[b, c, t] * rsqrt(mean_c x[b, c, t]^2 + eps) * (1 + weight[c]),
+ * fp32 statistics, the result in `dtype` -- the reference's RMSNorm
+ * (modules/rms_norm.py:11-31) applied to the layout the scan streams.  x, out
+ * (batch, channels, seqlen) and weight (channels) have element type `dtype`.
+ */
+int ssm_rms_norm_cm(int64_t batch, int64_t channels, int64_t seqlen, int dtype, const void* x,
+                    const void* weight, float eps, void* out, void* stream);
+
+/*
  * Causal depthwise conv1d (+ SiLU) over channel-major rows: the prefill
  * convolution of the Mamba layer, nn.Conv1d(dim, dim, width, groups=dim,
  * padding=width-1)(x)[..., :seqlen] followed by F.silu

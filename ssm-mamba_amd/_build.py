@@ -16,7 +16,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_NAME = "libssm_mamba_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
-SOURCES = ["scan_fwd.hip", "scan_bwd.hip", "state_update.hip", "conv1d.hip", "decode.hip", "capi.hip"]
+SOURCES = ["scan_fwd.hip", "scan_bwd.hip", "state_update.hip", "conv1d.hip", "decode.hip", "norm.hip", "capi.hip"]
 
 ARCH = os.environ.get("SSM_MAMBA_ARCH", "gfx950")
 

@@ -81,6 +81,10 @@ SIGNATURES = {
         _p, _p, _i64,                          # xc, xz, ld_xz
         _p, _p, _p,                            # state, y, stream
     ]),
+    "ssm_rms_norm_cm": (_i32, [
+        _i64, _i64, _i64, _i32,                # batch, channels, seqlen, dtype
+        _p, _p, ctypes.c_float, _p, _p,        # x, weight, eps, out, stream
+    ]),
 }
 
 ABI_VERSION = 1

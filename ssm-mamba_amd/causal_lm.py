@@ -34,9 +34,12 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _native as _N
 from . import decode as _dec
 from .causal_conv1d import causal_conv1d_fn
 from .ops import selective_scan_fn, selective_state_update
+
+_DTYPES = {torch.float32: _N.SSM_F32, torch.bfloat16: _N.SSM_BF16}
 
 __all__ = ["RMSNorm", "Mamba", "Block", "CausalLMConfig", "CausalLM", "GreedyDecoder"]
 
@@ -51,6 +54,20 @@ def _proj_cm(weight: torch.Tensor, x: torch.Tensor, bias: Optional[torch.Tensor]
     if bias is None:
         return torch.bmm(w, x)
     return torch.baddbmm(bias[None, :, None].expand(x.shape[0], weight.shape[0], x.shape[2]), w, x)
+
+
+def rms_norm_cm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm over the channel axis of channel-major x (batch, channels, L) in
+    one HIP kernel (inference: no autograd)."""
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    batch, ch, seqlen = x.shape
+    with torch.cuda.device(x.device):
+        _N.check(_N.lib().ssm_rms_norm_cm(batch, ch, seqlen, _DTYPES[x.dtype], x.data_ptr(),
+                                          weight.contiguous().data_ptr(), float(eps),
+                                          out.data_ptr(),
+                                          torch.cuda.current_stream(x.device).cuda_stream))
+    return out
 
 
 def causal_conv_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]):
@@ -71,6 +88,9 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.zeros(dim))
 
     def forward(self, x: torch.Tensor, dim: int = -1) -> torch.Tensor:
+        if (dim % x.dim() == 1 and x.dim() == 3 and x.is_cuda and not torch.is_grad_enabled()
+                and x.dtype in (torch.float32, torch.bfloat16) and self.weight.dtype == x.dtype):
+            return rms_norm_cm(x, self.weight, self.eps)
         xf = x.float()
         d = dim % x.dim()
         scale = torch.rsqrt(xf.pow(2).mean(d, keepdim=True) + self.eps)
@@ -189,9 +209,11 @@ class Mamba(nn.Module):
         return y.transpose(1, 2).contiguous(), last
 
     def forward_cm(self, x: torch.Tensor, ssm_hiddens: Optional[torch.Tensor] = None,
-                   lengths: Optional[torch.Tensor] = None, use_cache: bool = False):
+                   lengths: Optional[torch.Tensor] = None, use_cache: bool = False,
+                   residual: Optional[torch.Tensor] = None, residual_inplace: bool = False):
         """Channel-major forward: x (batch, model_dim, L) -> (batch, model_dim, L)
-        and the last SSM state."""
+        (plus ``residual`` when given, added by the out-projection GEMM) and
+        the last SSM state."""
         inner, rank, nstate = self.inner_dim, self.delta_rank, self.state_dim
         w_in, b_in = self.input_proj.weight, self.input_proj.bias
         xs = _proj_cm(w_in[:inner], x, None if b_in is None else b_in[:inner])
@@ -211,7 +233,16 @@ class Mamba(nn.Module):
                                     h_init=ssm_hiddens, length=lengths, padding_side="left")
         if use_cache:
             self._ssm_hiddens = self._keep(self._ssm_hiddens, last.detach())
-        out = _proj_cm(self.out_proj.weight, y, self.out_proj.bias)
+        if residual is not None and self.out_proj.bias is None:
+            w = self.out_proj.weight.expand(y.shape[0], *self.out_proj.weight.shape)
+            if residual_inplace:
+                out = residual.baddbmm_(w, y)       # the stream is updated in place
+            else:
+                out = torch.baddbmm(residual, w, y)
+        else:
+            out = _proj_cm(self.out_proj.weight, y, self.out_proj.bias)
+            if residual is not None:
+                out = residual + out
         return out, last
 
     # ---- decode ----------------------------------------------------------
@@ -280,9 +311,18 @@ class Block(nn.Module):
         return y.transpose(1, 2).contiguous(), last
 
     def forward_cm(self, x: torch.Tensor, lengths: Optional[torch.Tensor] = None,
-                   ssm_hiddens: Optional[torch.Tensor] = None, use_cache: bool = False):
-        y, last = self.ssm.forward_cm(self.norm(x, dim=1), ssm_hiddens=ssm_hiddens,
-                                      lengths=lengths, use_cache=use_cache)
+                   ssm_hiddens: Optional[torch.Tensor] = None, use_cache: bool = False,
+                   inplace: bool = False):
+        """Channel-major block; with ``inplace`` (and no active dropout) the
+        residual stream x itself receives x + mixer(norm(x))."""
+        h = self.norm(x, dim=1)
+        if not self.training or self.dropout.p == 0.0:
+            # x + mixer(h) with the add in the out-projection GEMM (beta = 1)
+            return self.ssm.forward_cm(h, ssm_hiddens=ssm_hiddens, lengths=lengths,
+                                       use_cache=use_cache, residual=x,
+                                       residual_inplace=inplace and not torch.is_grad_enabled())
+        y, last = self.ssm.forward_cm(h, ssm_hiddens=ssm_hiddens, lengths=lengths,
+                                      use_cache=use_cache)
         return x + self.dropout(y), last
 
     def step(self, hidden_states: torch.Tensor) -> torch.Tensor:
@@ -359,8 +399,9 @@ class CausalLM(nn.Module):
         """input_ids (batch, seq_len) -> logits (batch, seq_len, vocab)."""
         x = self.embedding(input_ids).transpose(1, 2).contiguous()
         for layer in self.layers:
-            x, _ = layer.forward_cm(x, lengths=lengths, use_cache=use_cache)
-        x = self.norm(x.transpose(1, 2).contiguous())
+            # x is this method's own stream: layers may update it in place
+            x, _ = layer.forward_cm(x, lengths=lengths, use_cache=use_cache, inplace=True)
+        x = self.norm(x, dim=1).transpose(1, 2).contiguous()
         return self.lm_head(x)
 
     def step(self, input_ids: torch.Tensor) -> torch.Tensor:

@@ -32,6 +32,8 @@ hipError_t launch_decode_ssm_step(int bf16, const void* p, int nout, int R, cons
                                   const void* dtb, const void* logA, const void* D, const void* xc,
                                   const void* xz, int ld, float* state, void* y, int B, int dim,
                                   int nstate, bool vecR, hipStream_t st);
+hipError_t launch_rms_norm_cm(int bf16, const void* x, const void* w, float eps, void* out, int B,
+                              int C, int L, bool pair, hipStream_t st);
 hipError_t launch_causal_conv1d_fwd(int batch, int dim, int L, int K, int dtype_bf16,
                                     const void* x, const void* w, const void* bias, int silu,
                                     void* out, bool vec, hipStream_t st);
@@ -431,6 +433,23 @@ int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank
                                                 state, y, (int)batch, (int)dim, (int)nstate, vecR,
                                                 static_cast<hipStream_t>(stream)),
                     "decode_ssm_step launch");
+}
+
+int ssm_rms_norm_cm(int64_t batch, int64_t channels, int64_t seqlen, int dtype, const void* x,
+                    const void* weight, float eps, void* out, void* stream) {
+  if (dtype != SSM_F32 && dtype != SSM_BF16)
+    return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16 (got %d)", dtype);
+  if (batch < 1 || channels < 1 || seqlen < 1)
+    return fail(SSM_ERR_INVALID, "batch, channels and seqlen must be >= 1");
+  if (channels > INT_MAX / 2 || seqlen > INT_MAX / 2 || batch * ((seqlen + 127) / 128) > INT_MAX)
+    return fail(SSM_ERR_UNSUPPORTED, "rms_norm_cm sizes too large");
+  if (!x || !weight || !out) return fail(SSM_ERR_INVALID, "x, weight and out must be non-NULL");
+  const uintptr_t align = dtype == SSM_BF16 ? 4 : 8;
+  const bool pair = seqlen % 2 == 0 && ((uintptr_t)x % align) == 0 && ((uintptr_t)out % align) == 0;
+  return hip_status(ssm::launch_rms_norm_cm(dtype == SSM_BF16, x, weight, eps, out, (int)batch,
+                                            (int)channels, (int)seqlen, pair,
+                                            static_cast<hipStream_t>(stream)),
+                    "rms_norm_cm launch");
 }
 
 size_t ssm_causal_conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t width) {

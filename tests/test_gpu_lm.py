@@ -272,3 +272,27 @@ def test_fused_decode_falls_back_outside_its_limits(cuda):
     _, caches = LR.lm_forward(sd, ids, use_cache=True)
     ref, _ = LR.lm_step(sd, ids[:, 0], caches)
     _close(got, ref, "batch-9 step", **F32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batch,ch,seqlen", [(1, 8, 1), (2, 64, 37), (3, 1024, 256), (2, 100, 130)])
+def test_rms_norm_channel_major(cuda, dtype, batch, ch, seqlen):
+    """The channel-major RMSNorm kernel against the oracle's RMSNorm over the
+    channel axis, including odd lengths (element path) and an offset view."""
+    from ssm_mamba_amd.causal_lm import rms_norm_cm
+    g = torch.Generator().manual_seed(batch * ch + seqlen)
+    x = (torch.randn(batch, ch, seqlen + 1, generator=g) * 3).to(dtype)
+    w = (0.3 * torch.randn(ch, generator=g)).to(dtype)
+    for xs in (x[..., :seqlen], x[..., 1:]):
+        xs = xs.contiguous()
+        got = rms_norm_cm(xs.to(cuda), w.to(cuda), 1e-6)
+        ref = LR.rms_norm(xs.double().transpose(1, 2), w.double()).transpose(1, 2)
+        tol = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
+        _close(got, ref, "rms_norm_cm", **tol)
+    # an odd element offset exercises the unpaired path
+    flat = torch.randn(batch * ch * seqlen + 1, generator=g).to(dtype).to(cuda)
+    xo = flat[1:].view(batch, ch, seqlen)
+    got = rms_norm_cm(xo, w.to(cuda), 1e-6)
+    ref = LR.rms_norm(xo.cpu().double().transpose(1, 2), w.double()).transpose(1, 2)
+    tol = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
+    _close(got, ref, "rms_norm_cm offset", **tol)
