@@ -19,6 +19,8 @@ hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* 
 hipError_t launch_state_update(const UpdateParams& p, int dtype, bool vecN, hipStream_t st);
 size_t bc_prep_floats(int batch, int nstate, int seqlen);
 size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen);
+void fwd_segments(int batch, int nblk, int seqlen, int& nseg, int& seg_len);
+size_t fwd_seg_floats(int batch, int dim, int nstate, int seqlen);
 int conv1d_max_width();
 int decode_max_batch();
 hipError_t launch_decode_gemv(int bf16, const void* W, const void* x, const void* nw, float eps,
@@ -140,6 +142,8 @@ ssm::ScanParams make_scan_params(int64_t batch, int64_t dim, int64_t seqlen, int
   p.h_init = h_init;
   p.length = length;
   p.z = z;
+  p.seg_len = (int)seqlen;
+  p.nseg = 1;
   return p;
 }
 
@@ -236,9 +240,10 @@ int ssm_profile_end(char* buf, size_t buf_bytes) {
 int64_t ssm_scan_nchunks(int64_t seqlen) { return seqlen <= 0 ? 0 : (seqlen + SSM_CHUNK - 1) / SSM_CHUNK; }
 
 size_t ssm_scan_fwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate) {
-  (void)dim;
-  if (batch < 1 || seqlen < 1 || nstate < 1) return 0;
+  if (batch < 1 || dim < 1 || seqlen < 1 || nstate < 1) return 0;
   return round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float)) +
+         round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) *
+                  sizeof(float)) +
          ssm::kDummyBytes;
 }
 
@@ -269,9 +274,14 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   p.out = out;
   p.h_chunks = h_chunks;
   p.h_last = h_last;
-  // workspace: [prepped B/C][dummy]
-  p.dummy = static_cast<char*>(workspace) +
-            round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
+  // workspace: [prepped B/C][segment states and step sums][dummy]
+  char* ws = static_cast<char*>(workspace) +
+             round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
+  ssm::fwd_segments((int)batch, p.nblk, (int)seqlen, p.nseg, p.seg_len);
+  p.seg_h = reinterpret_cast<float*>(ws);
+  p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * batch * nstate * dim;
+  ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));
+  p.dummy = ws;
   const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out});
   return hip_status(ssm::launch_scan_fwd(p, dtype, aligned, static_cast<float*>(workspace),
                                          static_cast<hipStream_t>(stream)),

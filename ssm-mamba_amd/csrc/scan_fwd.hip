@@ -99,6 +99,11 @@ __device__ __forceinline__ void fwd_block(const float4 dl4, const float4 du4, co
 // Every pointer is its own __restrict__ argument: with that no-alias
 // information the compiler can prove the output stores never clobber the
 // prepped B/C block, which is what lets its wave-uniform reads be scalar loads.
+//
+// Sequence split (p.nseg > 1, blockIdx.z = segment s of p.seg_len steps):
+// segment s starts from h_init folded through the summaries of segments
+// 0..s-1 left by scan_fwd_segsum_kernel (h <- exp(A sum dt) h + h_seg, the
+// composition of the steps' affine maps).
 template <typename T, int kSG, bool kHasZ, bool kAligned>
 __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
@@ -106,7 +111,8 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
     const float* __restrict__ Dp, const float* __restrict__ biasp,
     const float* __restrict__ h_init, const int64_t* __restrict__ length,
     const T* __restrict__ zp, T* __restrict__ out, float* __restrict__ h_chunks,
-    float* __restrict__ h_last, void* __restrict__ dummy) {
+    float* __restrict__ h_last, void* __restrict__ dummy, const float* __restrict__ seg_h,
+    const float* __restrict__ seg_dt) {
   using R4 = typename Raw4<T>::type;
   constexpr int kT4 = kTileF / 4;        // 4-step columns per sub-tile
   constexpr int kSup = kSubF * kTileF;   // steps staged per super-tile
@@ -124,6 +130,10 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   const int b = blockIdx.y;
   const int d0 = blockIdx.x * kBlockCh;
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
+  // this workgroup's steps [Tbeg, Lend); rows are still addressed with L
+  const int seg = blockIdx.z;
+  const int Tbeg = seg * p.seg_len;
+  const int Lend = min(L, Tbeg + p.seg_len);
   const int ngroups = (N + 1) / 2;
   const int npair = bc_pairs(N);
   const int Lp = bc_row_len(L);
@@ -143,7 +153,14 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       const int n = (g * kWaves + w) * 2 + s;
       const bool ok = ch_ok && n < N;
       A2[g][s] = ok ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
-      h[g][s] = (ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
+      float hv = (ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
+      // carry in through the earlier segments' affine maps, in order
+      for (int sp = 0; ok && sp < seg; ++sp) {
+        const size_t sb = (size_t)sp * p.batch + b;
+        const float decay = fast_exp2(A2[g][s] * seg_dt[sb * Dm + ch]);
+        hv = fmaf(decay, hv, seg_h[(sb * N + n) * Dm + ch]);
+      }
+      h[g][s] = hv;
     }
 
   // ---- tile-phase mapping: thread = (channel row, 4 consecutive steps of
@@ -171,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   // the next phase A, so each register is carried exactly one iteration.
   // Past the end the last sub-tile is re-read (unconditional loads keep the
   // registers free of merges).
-  const int last_t0 = (L - 1) / kTileF * kTileF;
+  const int last_t0 = (Lend - 1) / kTileF * kTileF;
   R4 qu[kSubF], qd[kSubF], qz[kSubF];
   // B/C staging: thread -> (pair, step) of the super-tile, kBCPer float4 each
   constexpr int kBCItems = kSubF * kWaves * kTileF;
@@ -220,7 +237,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
 #pragma unroll
     for (int i = 0; i < kSubF; ++i) {
       const int t0 = T0 + i * kTileF;
-      if (kFull || t0 < L) {
+      if (kFull || t0 < Lend) {
         float uv[4], dv[4], de[4], du[4];
         decode4(qu[i], uv);
         decode4(qd[i], dv);
@@ -264,11 +281,11 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
 #pragma unroll
     for (int i = 0; i < kSubF; ++i) {
       const int t0 = T0 + i * kTileF;
-      if (!kFull && t0 >= L) break;
+      if (!kFull && t0 >= Lend) break;
       const float4* __restrict__ cDelta = sDelta[i * kT4];
       const float4* __restrict__ cDu = sDu[i * kT4];
       // ---- phase B over sub-tile i
-      const int nT4 = min(kT4, (L - t0 + 3) / 4);
+      const int nT4 = min(kT4, (Lend - t0 + 3) / 4);
       auto store_carry = [&](int t4) {
         if (save && (((t4 & 3) == 3) || t4 == nT4 - 1) && ch_ok) {
           // layout (batch, nchunks, nstate, dim): each state is one
@@ -412,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       // D*u and the gate
       {
         const int t = t0 + a_col;
-        if (kFull || (a_ok && t < L)) {
+        if (kFull || (a_ok && t < Lend)) {
           float y[4];
           float4 acc = sY[0][a_q][a_sw];
 #pragma unroll
@@ -433,30 +450,30 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
         }
       }
       // the next sub-tile's phase B rewrites the slices
-      if (i + 1 < kSubF && (kFull || t0 + kTileF < L)) __syncthreads();
+      if (i + 1 < kSubF && (kFull || t0 + kTileF < Lend)) __syncthreads();
     }
     // the next phase A rewrites only sDelta / sDu / sBC, last read by the
     // final phase B before the barrier that preceded the final phase C
   };
 
-  issue(0);
-  if (kSG == 1 && kSup <= L) phase_a(0, std::true_type{});
-  else phase_a(0, std::false_type{});
-  int T0 = 0;
+  issue(Tbeg);
+  if (kSG == 1 && Tbeg + kSup <= Lend) phase_a(Tbeg, std::true_type{});
+  else phase_a(Tbeg, std::false_type{});
+  int T0 = Tbeg;
   if constexpr (kSG == 1) {
-    for (; T0 + kSup <= L; T0 += kSup) {
+    for (; T0 + kSup <= Lend; T0 += kSup) {
       body(T0, std::true_type{});
       const int Tn = T0 + kSup;
-      if (Tn + kSup <= L) phase_a(Tn, std::true_type{});
-      else if (Tn < L) phase_a(Tn, std::false_type{});
+      if (Tn + kSup <= Lend) phase_a(Tn, std::true_type{});
+      else if (Tn < Lend) phase_a(Tn, std::false_type{});
     }
   }
-  for (; T0 < L; T0 += kSup) {
+  for (; T0 < Lend; T0 += kSup) {
     body(T0, std::false_type{});
-    if (T0 + kSup < L) phase_a(T0 + kSup, std::false_type{});
+    if (T0 + kSup < Lend) phase_a(T0 + kSup, std::false_type{});
   }
 
-  if (!save && h_last && ch_ok) {
+  if (!save && h_last && ch_ok && Lend == L) {
 #pragma unroll
     for (int g = 0; g < kSG; ++g)
 #pragma unroll
@@ -467,10 +484,206 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   }
 }
 
+// ---------------------------------------------------------------- segment summaries
+
+// For segment s = blockIdx.z (< nseg - 1) of batch row b and 64 channels: the
+// state the segment's steps produce from zero, h_seg = sum_t (prod_{t' > t}
+// a_t') delta_t u_t B_t, and the segment's summed step size sum_t delta_t
+// (padded steps count zero), the two numbers that let a later segment start
+// from the right state.  The same tiling as the forward (64 channels x 32
+// steps per tile, lane = channel, wave = state pair) without outputs: phase A
+// stages delta and delta*u in LDS (double-buffered by tile parity, so one
+// barrier per tile suffices), phase B runs the recurrence with B read as
+// wave-uniform values of the prepped layout.
+template <typename T, int kSG, bool kAligned>
+__global__ __launch_bounds__(kThreads) void scan_fwd_segsum_kernel(
+    const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
+    const float* __restrict__ Ap, const float* __restrict__ bc, const float* __restrict__ biasp,
+    const int64_t* __restrict__ length, float* __restrict__ seg_h, float* __restrict__ seg_dt) {
+  using R4 = typename Raw4<T>::type;
+  constexpr int kT4 = kTileF / 4;
+  static_assert(kBlockCh * kT4 == kThreads, "one 4-step row piece per thread");
+  __shared__ float4 sDelta[2][kT4][kBlockCh];
+  __shared__ float4 sDu[2][kT4][kBlockCh];
+  __shared__ float4 sB[2][kWaves][kTileF / 2];  // (B0, B1) of steps 2i, 2i+1 per pair
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = wave_id_uniform();
+  const int b = blockIdx.y;
+  const int d0 = blockIdx.x * kBlockCh;
+  const int seg = blockIdx.z;
+  const int L = p.seqlen, Dm = p.dim, N = p.nstate;
+  const int Tbeg = seg * p.seg_len;
+  const int Lend = min(L, Tbeg + p.seg_len);
+  const int npair = bc_pairs(N);
+  const int Lp = bc_row_len(L);
+  const size_t rb = (size_t)b * Dm;
+  int vlo, vhi;
+  valid_window(length, p.pad_right, b, L, vlo, vhi);
+
+  const int ch = d0 + lane;
+  const bool ch_ok = ch < Dm;
+  float h[kSG][2], A2[kSG][2];
+#pragma unroll
+  for (int g = 0; g < kSG; ++g)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int n = (g * kWaves + w) * 2 + s;
+      A2[g][s] = (ch_ok && n < N) ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
+      h[g][s] = 0.0f;
+    }
+
+  const int a_row = tid / kT4;
+  const int a_q = tid % kT4;
+  const int a_col = a_q * 4;
+  const int a_sw = a_row ^ col_swz(a_q);
+  const int a_ch = d0 + a_row;
+  const bool a_ok = a_ch < Dm;
+  const float Bias = (a_ok && biasp) ? biasp[a_ch] : 0.0f;
+  const int a_chc = min(a_ch, Dm - 1);
+  const T* __restrict__ u_row = u + (rb + a_chc) * L;
+  const T* __restrict__ d_row = dl + (rb + a_chc) * L;
+  const bool softplus = p.softplus != 0;
+  const int last_t0 = (Lend - 1) / kTileF * kTileF;
+  const float4* __restrict__ bc4 = reinterpret_cast<const float4*>(bc);
+  float dtsum = 0.0f;
+
+  // B staging (kSG == 1): thread tid < 256 owns (pair tid / 32, step tid % 32)
+  const int bc_G = (tid / kTileF) % kWaves;
+  const int bc_t = tid % kTileF;
+  auto load_b = [&](int T0) {
+    const int t = min(T0 + bc_t, Lp - 1);
+    return bc4[((size_t)b * npair + bc_G) * Lp + t];
+  };
+  R4 qu = load_raw4_nb<T, kAligned>(u_row, Tbeg + a_col, L, a_ok);
+  R4 qd = load_raw4_nb<T, kAligned>(d_row, Tbeg + a_col, L, a_ok);
+  float4 qb = kSG == 1 ? load_b(Tbeg) : make_float4(0.f, 0.f, 0.f, 0.f);
+  int buf = 0;
+  for (int T0 = Tbeg; T0 < Lend; T0 += kTileF) {
+    {
+      float uv[4], dv[4], de[4], du[4];
+      decode4(qu, uv);
+      decode4(qd, dv);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float x = dv[j] + Bias;
+        const float dt = softplus ? softplus_t20(x) : x;
+        const int tt = T0 + a_col + j;
+        const bool valid = a_ok && tt >= vlo && tt < vhi && tt < Lend;
+        de[j] = valid ? dt : 0.0f;
+        du[j] = de[j] * uv[j];
+        dtsum += de[j];
+      }
+      sDelta[buf][a_q][a_sw] = make_float4(de[0], de[1], de[2], de[3]);
+      sDu[buf][a_q][a_sw] = make_float4(du[0], du[1], du[2], du[3]);
+      if (kSG == 1 && tid < kWaves * kTileF) {
+        // (B0, B1) of this step into the pair's row: two steps per float4
+        float* row = reinterpret_cast<float*>(&sB[buf][bc_G][0]);
+        row[2 * bc_t] = qb.x;
+        row[2 * bc_t + 1] = qb.z;
+      }
+    }
+    // next tile's rows (the last tile re-reads itself)
+    const int Tn = min(T0 + kTileF, last_t0);
+    qu = load_raw4_nb<T, kAligned>(u_row, Tn + a_col, L, a_ok);
+    qd = load_raw4_nb<T, kAligned>(d_row, Tn + a_col, L, a_ok);
+    if constexpr (kSG == 1) qb = load_b(Tn);
+    __syncthreads();
+    const int nT4 = min(kT4, (Lend - T0 + 3) / 4);
+    if (kSG == 1 && nT4 == kT4) {
+      // full tile: 8 blocks unrolled, each block's LDS reads one block ahead
+      const float4* __restrict__ bro = sB[buf][w];
+      float4 dlb[2], dub[2], bb[2][2];
+      dlb[0] = sDelta[buf][0][lane ^ col_swz(0)];
+      dub[0] = sDu[buf][0][lane ^ col_swz(0)];
+      bb[0][0] = bro[0];
+      bb[0][1] = bro[1];
+#pragma unroll
+      for (int k = 0; k < kT4; ++k) {
+        const int c = k & 1;
+        if (k + 1 < kT4) {
+          dlb[c ^ 1] = sDelta[buf][k + 1][lane ^ col_swz(k + 1)];
+          dub[c ^ 1] = sDu[buf][k + 1][lane ^ col_swz(k + 1)];
+          bb[c ^ 1][0] = bro[2 * (k + 1)];
+          bb[c ^ 1][1] = bro[2 * (k + 1) + 1];
+        }
+        const float dlv[4] = {dlb[c].x, dlb[c].y, dlb[c].z, dlb[c].w};
+        const float duv[4] = {dub[c].x, dub[c].y, dub[c].z, dub[c].w};
+        const float b0[4] = {bb[c][0].x, bb[c][0].z, bb[c][1].x, bb[c][1].z};
+        const float b1[4] = {bb[c][0].y, bb[c][0].w, bb[c][1].y, bb[c][1].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          h[0][0] = fmaf(fast_exp2(dlv[j] * A2[0][0]), h[0][0], duv[j] * b0[j]);
+          h[0][1] = fmaf(fast_exp2(dlv[j] * A2[0][1]), h[0][1], duv[j] * b1[j]);
+        }
+      }
+      buf ^= 1;
+      continue;
+    }
+    for (int t4 = 0; t4 < nT4; ++t4) {
+      const float4 dl4 = sDelta[buf][t4][lane ^ col_swz(t4)];
+      const float4 du4 = sDu[buf][t4][lane ^ col_swz(t4)];
+      const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+      const float duv[4] = {du4.x, du4.y, du4.z, du4.w};
+      const int tb = T0 + 4 * t4;
+#pragma unroll
+      for (int g = 0; g < kSG; ++g) {
+        const int G = g * kWaves + w;
+        if (G < npair) {
+          const float4* __restrict__ q = bc4 + ((size_t)b * npair + G) * Lp + tb;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float4 v = q[j];  // (B0, C0, B1, C1), wave-uniform
+            h[g][0] = fmaf(fast_exp2(dlv[j] * A2[g][0]), h[g][0], duv[j] * v.x);
+            h[g][1] = fmaf(fast_exp2(dlv[j] * A2[g][1]), h[g][1], duv[j] * v.z);
+          }
+        }
+      }
+    }
+    buf ^= 1;
+  }
+
+  const size_t sb = (size_t)seg * p.batch + b;
+  if (ch_ok) {
+#pragma unroll
+    for (int g = 0; g < kSG; ++g)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int n = (g * kWaves + w) * 2 + s;
+        if (n < N) seg_h[(sb * N + n) * Dm + ch] = h[g][s];
+      }
+  }
+  // the 8 threads of a channel row are 8 consecutive lanes
+#pragma unroll
+  for (int m = 1; m < kT4; m <<= 1) dtsum += __shfl_xor(dtsum, m, 64);
+  if (a_q == 0 && a_ok) seg_dt[sb * Dm + a_ch] = dtsum;
+}
+
 // ---------------------------------------------------------------- launch
 
 size_t bc_prep_floats(int batch, int nstate, int seqlen) {
   return (size_t)batch * bc_pairs(nstate) * bc_row_len(seqlen) * 4;
+}
+
+// Segments of the forward sequence split: enough for about one workgroup per
+// compute unit of the 256-CU gfx950 (every workgroup holds a CU's worth of
+// LDS), each a whole number of super-tiles; 1 when the batch and channel
+// blocks already fill the device.
+void fwd_segments(int batch, int nblk, int seqlen, int& nseg, int& seg_len) {
+  constexpr int kSup = kSubF * kTileF;
+  constexpr int kTargetWG = 256, kMaxSeg = 16;
+  const int rows = batch * nblk;
+  int s = rows >= kTargetWG ? 1 : kTargetWG / rows;
+  s = std::max(1, std::min({s, kMaxSeg, (seqlen + kSup - 1) / kSup}));
+  seg_len = ((seqlen + s - 1) / s + kSup - 1) / kSup * kSup;
+  nseg = (seqlen + seg_len - 1) / seg_len;
+}
+
+size_t fwd_seg_floats(int batch, int dim, int nstate, int seqlen) {
+  int nseg, seg_len;
+  fwd_segments(batch, (dim + kBlockCh - 1) / kBlockCh, seqlen, nseg, seg_len);
+  return (size_t)(nseg - 1) * batch * dim * (nstate + 1);
 }
 
 hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t st) {
@@ -491,12 +704,20 @@ hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t
 
 template <typename T, int kSG, bool kHasZ, bool kAligned>
 static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t st) {
-  dim3 grid(p.nblk, p.batch);
+  if (p.nseg > 1) {
+    ProfScope prof("scan_fwd_segsum", st);
+    hipLaunchKernelGGL((scan_fwd_segsum_kernel<T, kSG, kAligned>),
+                       dim3(p.nblk, p.batch, p.nseg - 1), dim3(kThreads), 0, st, dims_of(p),
+                       (const T*)p.u, (const T*)p.delta, p.A, bc, p.bias, p.length, p.seg_h,
+                       p.seg_dt);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   ProfScope prof("scan_fwd", st);
-  hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(kThreads), 0, st,
-                     dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias,
-                     p.h_init, p.length, (const T*)p.z, (T*)p.out, p.h_chunks, p.h_last,
-                     p.dummy);
+  hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kHasZ, kAligned>),
+                     dim3(p.nblk, p.batch, p.nseg), dim3(kThreads), 0, st, dims_of(p),
+                     (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias, p.h_init, p.length,
+                     (const T*)p.z, (T*)p.out, p.h_chunks, p.h_last, p.dummy, p.seg_h, p.seg_dt);
   return hipGetLastError();
 }
 

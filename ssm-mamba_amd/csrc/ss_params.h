@@ -28,6 +28,8 @@ struct ScanDims {
   int batch, dim, seqlen, nstate, nchunks, nblk;
   int pad_right;
   int softplus;
+  int seg_len;  // steps per sequence segment (a multiple of the forward super-tile)
+  int nseg;     // segments (1: the whole row in one workgroup)
 };
 
 struct ScanParams {
@@ -72,6 +74,13 @@ struct ScanParams {
   // 256 bytes of workspace that masked-off lanes store to (never read), so
   // the kernels' steady-state stores need no branches
   void* dummy;
+
+  // sequence split of the forward (nseg > 1): per segment s < nseg - 1 the
+  // state its steps produce from zero, (nseg - 1, batch, nstate, dim), and the
+  // sum of its step sizes, (nseg - 1, batch, dim)
+  int seg_len, nseg;
+  float* seg_h;
+  float* seg_dt;
 };
 
 constexpr size_t kDummyBytes = 256;
@@ -92,7 +101,8 @@ struct UpdateParams {
 };
 
 inline ScanDims dims_of(const ScanParams& p) {
-  return ScanDims{p.batch, p.dim, p.seqlen, p.nstate, p.nchunks, p.nblk, p.pad_right, p.softplus};
+  return ScanDims{p.batch, p.dim,       p.seqlen,  p.nstate, p.nchunks,
+                  p.nblk,  p.pad_right, p.softplus, p.seg_len, p.nseg};
 }
 
 }  // namespace ssm
