@@ -250,10 +250,16 @@ size_t ssm_scan_fwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, 
 size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate) {
   if (batch < 1 || dim < 1 || seqlen < 1 || nstate < 1) return 0;
   const size_t nblk = (dim + ssm::kBlockCh - 1) / ssm::kBlockCh;
+  int nseg, seg_len;
+  ssm::fwd_segments((int)batch, (int)nblk, (int)seqlen, nseg, seg_len);
+  const size_t rows = (size_t)batch * nseg;  // (segment, batch row) partial rows
   return round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float)) +
          round256(2 * nblk * batch * nstate * seqlen * sizeof(float)) +
-         round256((size_t)batch * dim * nstate * sizeof(float)) +
-         2 * round256((size_t)batch * dim * sizeof(float)) + ssm::kDummyBytes;
+         round256(rows * dim * nstate * sizeof(float)) +
+         2 * round256(rows * dim * sizeof(float)) +
+         round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) *
+                  sizeof(float)) +
+         ssm::kDummyBytes;
 }
 
 int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
@@ -321,18 +327,25 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   p.dC = dC;
   p.dD = dD;
   p.dbias = ddelta_bias;
-  // workspace: [prepped B/C][dB/dC partials][dA partials][dD partials][dbias partials][dummy]
+  // workspace: [prepped B/C][dB/dC partials][dA partials][dD partials][dbias partials]
+  // [segment carries and step sums][dummy]; the dA/dD/dbias partials have one
+  // row per (segment, batch row)
+  ssm::fwd_segments((int)batch, p.nblk, (int)seqlen, p.nseg, p.seg_len);
+  const size_t rows = (size_t)batch * p.nseg;
   char* ws = static_cast<char*>(workspace);
   float* bc = reinterpret_cast<float*>(ws);
   ws += round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
   p.ws_bc = reinterpret_cast<float*>(ws);
   ws += round256(2 * (size_t)p.nblk * batch * nstate * seqlen * sizeof(float));
   p.ws_A = reinterpret_cast<float*>(ws);
-  ws += round256((size_t)batch * dim * nstate * sizeof(float));
+  ws += round256(rows * dim * nstate * sizeof(float));
   p.ws_D = reinterpret_cast<float*>(ws);
-  ws += round256((size_t)batch * dim * sizeof(float));
+  ws += round256(rows * dim * sizeof(float));
   p.ws_bias = reinterpret_cast<float*>(ws);
-  ws += round256((size_t)batch * dim * sizeof(float));
+  ws += round256(rows * dim * sizeof(float));
+  p.seg_h = reinterpret_cast<float*>(ws);
+  p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * batch * nstate * dim;
+  ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));
   p.dummy = ws;
   const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, dout, du, ddelta, dz});
   return hip_status(ssm::launch_scan_bwd(p, dtype, aligned, bc, static_cast<hipStream_t>(stream)),

@@ -130,7 +130,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const float* __restrict__ dh_last, T* __restrict__ dup, T* __restrict__ ddp,
     T* __restrict__ dzp, float* __restrict__ dh_init, float* __restrict__ ws_bc,
     float* __restrict__ ws_A, float* __restrict__ ws_D, float* __restrict__ ws_bias,
-    void* __restrict__ dummy) {
+    void* __restrict__ dummy, const float* __restrict__ seg_g, const float* __restrict__ seg_dt) {
   using R4 = typename Raw4<T>::type;
   constexpr int kT4 = kTileB / 4;         // 4-step columns per tile (4)
   constexpr int kItems = kBlockCh * kT4;  // (row, column) items per tile (256)
@@ -160,6 +160,12 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   const int blk = blockIdx.x;
   const int d0 = blk * kBlockCh;
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
+  // sequence split: this workgroup's tiles [tile_beg, tile_end) of segment seg
+  const int seg = blockIdx.z;
+  const int ntiles = (L + kTileB - 1) / kTileB;
+  const int tile_beg = seg * (p.seg_len / kTileB);
+  const int tile_end = min(ntiles, tile_beg + p.seg_len / kTileB);
+  const size_t srow = (size_t)seg * p.batch + b;  // (segment, batch row) of the partials
   const int ngroups = (N + 1) / 2;
   const int npair = bc_pairs(N);
   const int Lp = bc_row_len(L);
@@ -181,10 +187,17 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     for (int s = 0; s < 2; ++s) {
       const int n = (g * kWaves + w) * 2 + s;
       const bool ok = ch_ok && n < N;
-      gam[g][s] = (ok && dh_last) ? dh_last[(rb + ch) * N + n] : 0.0f;
       dA[g][s] = 0.0f;
       Av[g][s] = ok ? Ap[(size_t)ch * N + n] : 0.0f;
       A2[g][s] = Av[g][s] * kLog2e;
+      // carry in from the later segments, last first:
+      // gamma <- gamma_seg + exp(A sum dt) gamma (their summaries, zero carry-in)
+      float q = (ok && dh_last) ? dh_last[(rb + ch) * N + n] : 0.0f;
+      for (int sp = p.nseg - 1; ok && sp > seg; --sp) {
+        const size_t sb = (size_t)(sp - 1) * p.batch + b;
+        q = fmaf(fast_exp2(A2[g][s] * seg_dt[sb * Dm + ch]), q, seg_g[(sb * N + n) * Dm + ch]);
+      }
+      gam[g][s] = q;
     }
 
   // ---- tile-phase mapping.  Group 0 (waves 0-3) owns the u / delta side
@@ -419,16 +432,15 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   // Rotated loop: a tile's phase A (which waits for its prefetched inputs)
   // runs at the end of the previous iteration, in the same iteration as the
   // loads and the stores issued after them, so the waits count exactly.
-  const int ntiles = (L + kTileB - 1) / kTileB;
-  issue(ntiles - 1);
-  phase_a(ntiles - 1);
-  for (int tile = ntiles - 1; tile >= 0; --tile) {
+  issue(tile_end - 1);
+  phase_a(tile_end - 1);
+  for (int tile = tile_end - 1; tile >= tile_beg; --tile) {
     __syncthreads();
-    issue(max(tile - 1, 0));  // at tile 0 the tile itself is re-read, unused
+    issue(max(tile - 1, tile_beg));  // at the first tile the tile itself is re-read, unused
     phase_b(tile);
     __syncthreads();
     phase_c(tile);
-    if (tile > 0) phase_a(tile - 1);
+    if (tile > tile_beg) phase_a(tile - 1);
     // the next phase B overwrites the slices only after the barrier at the
     // top of the next iteration
   }
@@ -440,8 +452,8 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     for (int s = 0; s < 2; ++s) {
       const int n = (g * kWaves + w) * 2 + s;
       if (ch_ok && n < N) {
-        ws_A[(rb + ch) * N + n] = dA[g][s];
-        if (dh_init) dh_init[(rb + ch) * N + n] = gam[g][s];
+        ws_A[(srow * Dm + ch) * N + n] = dA[g][s];
+        if (dh_init && seg == 0) dh_init[(rb + ch) * N + n] = gam[g][s];
       }
     }
   // the 4 items of a channel row are 4 consecutive lanes of group 0
@@ -449,16 +461,189 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const float sd = group_sum<kT4>(accD);
     const float sb = group_sum<kT4>(accB);
     if (a_ok && a_q == 0) {
-      ws_D[rb + a_ch] = sd;
-      ws_bias[rb + a_ch] = sb;
+      ws_D[srow * Dm + a_ch] = sd;
+      ws_bias[srow * Dm + a_ch] = sb;
     }
   }
 }
 
-// Adds the partial sums: dB/dC over channel blocks, dA/dD/dbias over batch rows.
+// ---------------------------------------------------------------- segment summaries
+
+// For segment s = blockIdx.z + 1 (segments 1 .. nseg-1) of batch row b and 64
+// channels: the adjoint carry the segment hands to the one before it when its
+// own carry-in is zero, gamma_seg (the reverse recurrence G_t = gamma_t +
+// dout_t C_t, gamma_{t-1} = a_t G_t run from the segment's last step down to
+// its first), and the segment's summed step size.  With a carry-in q the
+// segment hands on gamma_seg + exp(A sum dt) q, which the main backward folds
+// from the last segment down.  dout is masked and gated exactly as in the main
+// kernel.  Tiles of 32 steps walked backwards; phase A stages delta and the
+// effective dout (double-buffered by tile parity: one barrier per tile) and
+// the tile's (C0, C1) per state pair.
+template <typename T, int kSG, bool kHasZ, bool kAligned>
+__global__ __launch_bounds__(kThreads) void scan_bwd_segsum_kernel(
+    const ScanDims p, const T* __restrict__ dl, const T* __restrict__ dyp,
+    const T* __restrict__ zp, const float* __restrict__ Ap, const float* __restrict__ bc,
+    const float* __restrict__ biasp, const int64_t* __restrict__ length,
+    float* __restrict__ seg_g, float* __restrict__ seg_dt) {
+  using R4 = typename Raw4<T>::type;
+  constexpr int kTS = 32;  // steps per tile
+  constexpr int kT4 = kTS / 4;
+  static_assert(kBlockCh * kT4 == kThreads, "one 4-step row piece per thread");
+  __shared__ float4 sDelta[2][kT4][kBlockCh];
+  __shared__ float4 sDo[2][kT4][kBlockCh];
+  __shared__ float4 sC[2][kWaves][kTS / 2];  // (C0, C1) of steps 2i, 2i+1 per pair
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = wave_id_uniform();
+  const int b = blockIdx.y;
+  const int d0 = blockIdx.x * kBlockCh;
+  const int seg = blockIdx.z + 1;
+  const int L = p.seqlen, Dm = p.dim, N = p.nstate;
+  const int Tbeg = seg * p.seg_len;
+  const int Lend = min(L, Tbeg + p.seg_len);
+  const int npair = bc_pairs(N);
+  const int Lp = bc_row_len(L);
+  const size_t rb = (size_t)b * Dm;
+  int vlo, vhi;
+  valid_window(length, p.pad_right, b, L, vlo, vhi);
+
+  const int ch = d0 + lane;
+  const bool ch_ok = ch < Dm;
+  float gam[kSG][2], A2[kSG][2];
+#pragma unroll
+  for (int g = 0; g < kSG; ++g)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int n = (g * kWaves + w) * 2 + s;
+      A2[g][s] = (ch_ok && n < N) ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
+      gam[g][s] = 0.0f;
+    }
+
+  const int a_row = tid / kT4;
+  const int a_q = tid % kT4;
+  const int a_col = a_q * 4;
+  // the forward's column swizzle (8 columns of 4 steps)
+  const int a_sw = a_row ^ (a_q | ((a_q & 1) << 3));
+  const int a_ch = d0 + a_row;
+  const bool a_ok = a_ch < Dm;
+  const float Bias = (a_ok && biasp) ? biasp[a_ch] : 0.0f;
+  const int a_chc = min(a_ch, Dm - 1);
+  const T* __restrict__ d_row = dl + (rb + a_chc) * L;
+  const T* __restrict__ y_row = dyp + (rb + a_chc) * L;
+  const T* __restrict__ z_row = kHasZ ? zp + (rb + a_chc) * L : y_row;
+  const bool softplus = p.softplus != 0;
+  const float4* __restrict__ bc4 = reinterpret_cast<const float4*>(bc);
+  const int c_G = (tid / kTS) % kWaves;
+  const int c_t = tid % kTS;
+  auto load_c = [&](int T0) {
+    const int t = min(T0 + c_t, Lp - 1);
+    return bc4[((size_t)b * npair + c_G) * Lp + t];
+  };
+  const int Tlast = Tbeg + (Lend - 1 - Tbeg) / kTS * kTS;
+  float dtsum = 0.0f;
+
+  R4 qd = load_raw4_nb<T, kAligned>(d_row, Tlast + a_col, L, a_ok);
+  R4 qy = load_raw4_nb<T, kAligned>(y_row, Tlast + a_col, L, a_ok);
+  R4 qz = kHasZ ? load_raw4_nb<T, kAligned>(z_row, Tlast + a_col, L, a_ok) : R4{};
+  float4 qc = kSG == 1 ? load_c(Tlast) : make_float4(0.f, 0.f, 0.f, 0.f);
+  int buf = 0;
+  for (int T0 = Tlast; T0 >= Tbeg; T0 -= kTS) {
+    {
+      float dv[4], yv[4], zv[4], de[4], dov[4];
+      decode4(qd, dv);
+      decode4(qy, yv);
+      if constexpr (kHasZ) decode4(qz, zv);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tt = T0 + a_col + j;
+        const bool valid = a_ok && tt >= vlo && tt < vhi && tt < Lend;
+        const float x = dv[j] + Bias;
+        const float dt = softplus ? softplus_t20(x) : x;
+        de[j] = valid ? dt : 0.0f;
+        const float dym = valid ? yv[j] : 0.0f;
+        if constexpr (kHasZ) dov[j] = dym * (zv[j] * sigmoidf_fast(zv[j]));
+        else dov[j] = dym;
+        dtsum += de[j];
+      }
+      sDelta[buf][a_q][a_sw] = make_float4(de[0], de[1], de[2], de[3]);
+      sDo[buf][a_q][a_sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
+      if (kSG == 1 && tid < kWaves * kTS) {
+        float* row = reinterpret_cast<float*>(&sC[buf][c_G][0]);
+        row[2 * c_t] = qc.y;
+        row[2 * c_t + 1] = qc.w;
+      }
+    }
+    // the previous tile in time (the first tile re-reads itself)
+    const int Tn = max(T0 - kTS, Tbeg);
+    qd = load_raw4_nb<T, kAligned>(d_row, Tn + a_col, L, a_ok);
+    qy = load_raw4_nb<T, kAligned>(y_row, Tn + a_col, L, a_ok);
+    if constexpr (kHasZ) qz = load_raw4_nb<T, kAligned>(z_row, Tn + a_col, L, a_ok);
+    if constexpr (kSG == 1) qc = load_c(Tn);
+    __syncthreads();
+    // steps past Lend hold zeros (identity steps), so whole tiles are walked
+    if constexpr (kSG == 1) {
+      const float4* __restrict__ cro = sC[buf][w];
+#pragma unroll
+      for (int k = kT4 - 1; k >= 0; --k) {
+        const float4 dl4 = sDelta[buf][k][lane ^ (k | ((k & 1) << 3))];
+        const float4 do4 = sDo[buf][k][lane ^ (k | ((k & 1) << 3))];
+        const float4 c01 = cro[2 * k], c23 = cro[2 * k + 1];
+        const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+        const float dov[4] = {do4.x, do4.y, do4.z, do4.w};
+        const float c0[4] = {c01.x, c01.z, c23.x, c23.z};
+        const float c1[4] = {c01.y, c01.w, c23.y, c23.w};
+#pragma unroll
+        for (int j = 3; j >= 0; --j) {
+          gam[0][0] = fast_exp2(dlv[j] * A2[0][0]) * fmaf(dov[j], c0[j], gam[0][0]);
+          gam[0][1] = fast_exp2(dlv[j] * A2[0][1]) * fmaf(dov[j], c1[j], gam[0][1]);
+        }
+      }
+    } else {
+      for (int k = kT4 - 1; k >= 0; --k) {
+        const float4 dl4 = sDelta[buf][k][lane ^ (k | ((k & 1) << 3))];
+        const float4 do4 = sDo[buf][k][lane ^ (k | ((k & 1) << 3))];
+        const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+        const float dov[4] = {do4.x, do4.y, do4.z, do4.w};
+        const int tb = min(T0 + 4 * k, Lp - 4);
+#pragma unroll
+        for (int g = 0; g < kSG; ++g) {
+          const int G = g * kWaves + w;
+          if (G < npair) {
+            const float4* __restrict__ q = bc4 + ((size_t)b * npair + G) * Lp + tb;
+#pragma unroll
+            for (int j = 3; j >= 0; --j) {
+              const float4 v = q[j];  // (B0, C0, B1, C1), wave-uniform
+              gam[g][0] = fast_exp2(dlv[j] * A2[g][0]) * fmaf(dov[j], v.y, gam[g][0]);
+              gam[g][1] = fast_exp2(dlv[j] * A2[g][1]) * fmaf(dov[j], v.w, gam[g][1]);
+            }
+          }
+        }
+      }
+    }
+    buf ^= 1;
+  }
+
+  const size_t sb = (size_t)(seg - 1) * p.batch + b;
+  if (ch_ok) {
+#pragma unroll
+    for (int g = 0; g < kSG; ++g)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int n = (g * kWaves + w) * 2 + s;
+        if (n < N) seg_g[(sb * N + n) * Dm + ch] = gam[g][s];
+      }
+  }
+#pragma unroll
+  for (int m = 1; m < kT4; m <<= 1) dtsum += __shfl_xor(dtsum, m, 64);
+  if (a_q == 0 && a_ok) seg_dt[sb * Dm + a_ch] = dtsum;
+}
+
+// Adds the partial sums: dB/dC over channel blocks, dA/dD/dbias over the
+// (segment, batch row) rows, each in a fixed order.
 template <typename T>
 __global__ __launch_bounds__(256) void scan_bwd_reduce_kernel(
-    const int batch, const int dim, const int N, const int L, const int nblk,
+    const int batch, const int rows, const int dim, const int N, const int L, const int nblk,
     const float* __restrict__ ws_bc, const float* __restrict__ ws_A,
     const float* __restrict__ ws_D, const float* __restrict__ ws_bias, T* __restrict__ dB,
     T* __restrict__ dC, float* __restrict__ dA, float* __restrict__ dD,
@@ -477,12 +662,12 @@ __global__ __launch_bounds__(256) void scan_bwd_reduce_kernel(
     } else if (i < 2 * nBC + nA) {
       const size_t r = i - 2 * nBC;
       float s = 0.0f;
-      for (int bb = 0; bb < batch; ++bb) s += ws_A[(size_t)bb * nA + r];
+      for (int bb = 0; bb < rows; ++bb) s += ws_A[(size_t)bb * nA + r];
       dA[r] = s;
     } else {
       const size_t d = i - 2 * nBC - nA;
       float sd = 0.0f, sb = 0.0f;
-      for (int bb = 0; bb < batch; ++bb) {
+      for (int bb = 0; bb < rows; ++bb) {
         sd += ws_D[(size_t)bb * dim + d];
         sb += ws_bias[(size_t)bb * dim + d];
       }
@@ -499,13 +684,22 @@ hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t
 
 template <typename T, int kSG, bool kHasZ, bool kAligned>
 static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t st) {
-  dim3 grid(p.nblk, p.batch);
+  if (p.nseg > 1) {
+    ProfScope prof("scan_bwd_segsum", st);
+    hipLaunchKernelGGL((scan_bwd_segsum_kernel<T, kSG, kHasZ, kAligned>),
+                       dim3(p.nblk, p.batch, p.nseg - 1), dim3(kThreads), 0, st, dims_of(p),
+                       (const T*)p.delta, (const T*)p.dout, (const T*)p.z, p.A, bc, p.bias,
+                       p.length, p.seg_h, p.seg_dt);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  dim3 grid(p.nblk, p.batch, p.nseg);
   ProfScope prof("scan_bwd", st);
   hipLaunchKernelGGL((scan_bwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(kThreads), 0, st,
                      dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias,
                      p.h_init, p.length, (const T*)p.z, p.h_chunks_in, (const T*)p.dout,
                      p.dh_last, (T*)p.du, (T*)p.ddelta, (T*)p.dz, p.dh_init, p.ws_bc, p.ws_A,
-                     p.ws_D, p.ws_bias, p.dummy);
+                     p.ws_D, p.ws_bias, p.dummy, p.seg_h, p.seg_dt);
   return hipGetLastError();
 }
 
@@ -528,8 +722,9 @@ static hipError_t launch_bwd2(const ScanParams& p, const float* bc, bool aligned
   const size_t total = 2 * (size_t)p.batch * p.nstate * p.seqlen + (size_t)p.dim * p.nstate + p.dim;
   const int blocks = (int)std::min<size_t>((total + 255) / 256, 16384);
   ProfScope prof("scan_bwd_reduce", st);
-  hipLaunchKernelGGL(scan_bwd_reduce_kernel<T>, dim3(blocks), dim3(256), 0, st, p.batch, p.dim,
-                     p.nstate, p.seqlen, p.nblk, p.ws_bc, p.ws_A, p.ws_D, p.ws_bias, (T*)p.dB,
+  hipLaunchKernelGGL(scan_bwd_reduce_kernel<T>, dim3(blocks), dim3(256), 0, st, p.batch,
+                     p.batch * p.nseg, p.dim, p.nstate, p.seqlen, p.nblk, p.ws_bc, p.ws_A, p.ws_D,
+                     p.ws_bias, (T*)p.dB,
                      (T*)p.dC, p.dA, p.dD, p.dbias);
   return hipGetLastError();
 }
