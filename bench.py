@@ -174,11 +174,13 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
     `decode_steps` greedy steps (48 layers + norm + LM head + pick each), the
     step captured once in a HIP graph and replayed.  Returns tokens/s for both
     and the share of time in the scan / state-update kernels: for the prefill
-    from the library's per-kernel HIP events, for the decode from a graph of
-    the step's 48 state updates alone on the same buffers."""
+    from the library's per-kernel HIP events (forward scan, its segment
+    summaries and the B/C prep), for the decode from a graph of the step's 48
+    state-update kernels alone on the same buffers."""
     import torch
 
     from ssm_mamba_amd import _native as N
+    from ssm_mamba_amd import decode as DEC
     from ssm_mamba_amd import selective_update as su
     from ssm_mamba_amd.causal_lm import CausalLM, CausalLMConfig
 
@@ -210,7 +212,7 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
         N.profile_begin()
         model(ids, lengths, use_cache=True)
         prof = N.profile_end()
-        scan_ms = sum(v[1] for k, v in prof.items() if k in ("scan_fwd", "bc_prep"))
+        scan_ms = sum(v[1] for k, v in prof.items() if k in ("scan_fwd", "scan_fwd_segsum", "bc_prep"))
 
         dec.prefill(ids, lengths)
         torch.cuda.synchronize()
@@ -222,19 +224,27 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
         dec_ms = e0.elapsed_time(e1)
         new_tokens = dec.tokens[:, :decode_steps + 1].clone()
 
-        # the step's 48 state updates alone, on the model's own buffers
+        # the step's 48 state-update kernels alone (the fused decode kernel that
+        # also applies the dt projection and the gate), on the model's buffers
         inner, nstate = 2 * cfg.model_dim, cfg.state_dim
-        x = torch.randn(batch, inner, device=dev).bfloat16()
-        Bv = torch.randn(batch, nstate, device=dev).bfloat16()
         layers = [l.ssm for l in model.layers]
-        A = [-torch.exp(m.log_A.float()) for m in layers]
-        Ds = [m.D.float() for m in layers]
-        bs = [m.delta_proj.bias.float() for m in layers]
-        out = torch.empty(batch, inner, device=dev, dtype=torch.bfloat16)
+        rank = layers[0].delta_rank
+        params = torch.randn(batch, rank + 2 * nstate, device=dev).bfloat16()
+        xc = torch.randn(batch, inner, device=dev).bfloat16()
+        xz = torch.randn(batch, 2 * inner, device=dev).bfloat16()
+        fused = DEC.block_step_supported(layers[0], torch.zeros(batch, cfg.model_dim, device=dev,
+                                                                dtype=torch.bfloat16),
+                                         model.layers[0].norm.weight)
 
         def updates():
-            for m, a, d, b in zip(layers, A, Ds, bs):
-                su.apply_ext(x, a, Bv, Bv, d, x, b, m._ssm_hiddens, z=x, inplace=True, out=out)
+            for m in layers:
+                if fused:
+                    DEC.ssm_step(params, rank, m.delta_proj.weight, m.delta_proj.bias, m.log_A, m.D,
+                                 xc, xz, m._ssm_hiddens)
+                else:
+                    su.apply_ext(xc, -torch.exp(m.log_A.float()), params[:, :nstate].contiguous(),
+                                 params[:, :nstate].contiguous(), m.D.float(), xc,
+                                 m.delta_proj.bias.float(), m._ssm_hiddens, z=xc, inplace=True)
 
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
@@ -267,6 +277,7 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
         "decode_tokens_per_s": round(batch * decode_steps / (dec_ms * 1e-3), 1),
         "decode_update_share": round(upd_ms / dec_ms, 4),
         "decode_update_us_per_step": round(1e3 * upd_ms / decode_steps, 2),
+        "decode_fused_kernels": bool(fused),
         "first_new_tokens": new_tokens[0, :8].tolist(),
     }
     del model, dec
