@@ -345,6 +345,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-extra", action="store_true", help="only the config-1 step")
+    ap.add_argument("--no-e2e", action="store_true", help="skip config 4 (end to end)")
     ap.add_argument("--e2e", action="store_true",
                     help="only config 4 end to end (causal LM prefill + 128 decode steps); "
                          "prints its own JSON line")
@@ -440,7 +441,8 @@ def main():
                                   "kernels_ms": {k: round(v, 4) for k, v in k3.items()}}
         del x3
         try:
-            res["e2e"] = time_e2e(dev)
+            if not args.no_e2e:
+                res["e2e"] = time_e2e(dev)
         except Exception as exc:  # reported, not fatal to the headline line
             res["e2e"] = {"error": f"{type(exc).__name__}: {exc}"}
     if not args.no_cpu:
