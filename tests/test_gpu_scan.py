@@ -88,6 +88,28 @@ def test_lengths(cuda, padding_side, dtype):
              h_init=True, dlast=True)
 
 
+@pytest.mark.parametrize("padding_side,lengths", [("right", [300, 777]), ("left", [1, 650]),
+                                                   ("right", [0, 129])])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sequence_split_many_segments(cuda, padding_side, lengths, dtype):
+    """Batch 2 x 2 channel blocks fills 4 workgroups, so the scan splits L = 777
+    into 7 segments (6 of 128 steps and a ragged tail); lengths start and end
+    inside segments; h_init, dh_last and z carry across every boundary."""
+    run_case(cuda, 2, 80, 777, 16, dtype, seed=11, length=torch.tensor(lengths),
+             padding_side=padding_side, h_init=True, dlast=True)
+
+
+@pytest.mark.parametrize("nstate", [32, 64])
+def test_sequence_split_state_groups(cuda, nstate):
+    """More than 16 states take the summaries' multi-group path."""
+    run_case(cuda, 1, 64, 500, nstate, torch.float32, seed=nstate + 3, h_init=True, dlast=True,
+             length=torch.tensor([431]), padding_side="left")
+
+
+def test_sequence_split_forward_large_state(cuda):
+    run_case(cuda, 1, 64, 300, 200, torch.float32, seed=5, h_init=True, bwd=False)
+
+
 def test_no_softplus_no_z_no_D(cuda):
     run_case(cuda, 2, 64, 96, 16, torch.float32, seed=8, with_z=False, softplus=False,
              with_D=False, with_bias=False, positive_delta=True)
