@@ -275,7 +275,8 @@ def test_fused_decode_falls_back_outside_its_limits(cuda):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("batch,ch,seqlen", [(1, 8, 1), (2, 64, 37), (3, 1024, 256), (2, 100, 130)])
+@pytest.mark.parametrize("batch,ch,seqlen", [(1, 8, 1), (2, 64, 37), (3, 1024, 256), (2, 100, 130),
+                                              (1, 2048, 77), (4, 1024, 2048)])
 def test_rms_norm_channel_major(cuda, dtype, batch, ch, seqlen):
     """The channel-major RMSNorm kernel against the oracle's RMSNorm over the
     channel axis, including odd lengths (element path) and an offset view."""
