@@ -75,11 +75,13 @@ def time_scan(ss, N, x, steps, warmup, fwd_only=False):
     import torch
 
     def step():
+        # training step: the forward also keeps the ungated output for dz
+        y = None if fwd_only else torch.empty_like(x["u"])
         out, h = ss.forward(x["u"], x["A"], x["B"], x["C"], x["D"], x["delta"], x["bias"],
-                            None, None, None, z=x["z"], save_chunks=not fwd_only)
+                            None, None, None, z=x["z"], save_chunks=not fwd_only, out_ungated=y)
         if not fwd_only:
             ss.backward(x["u"], x["A"], x["B"], x["C"], x["D"], x["delta"], x["bias"], h, None,
-                        x["dout"], None, z=x["z"])
+                        x["dout"], None, z=x["z"], out_ungated=y)
 
     for _ in range(warmup):
         step()
@@ -340,8 +342,10 @@ def _cpu_model() -> str:
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # the GPU clocks take about 50 steps (40 ms) to settle after the first
+    # launches; the timed steps then measure the steady state
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-extra", action="store_true", help="only the config-1 step")

@@ -70,6 +70,10 @@ size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, 
  *              (no softplus when delta_softplus == 0)
  *   h_chunks = states after each SSM_CHUNK steps, or NULL (inference); then
  *              h_last (nullable) receives the final state.
+ *   out_ungated (nullable, requires z) = D*u + sum_n C*h, the output before
+ *              the gate: the backward needs it for dz.  The reference gates
+ *              outside the kernel (modules/mamba.py:182), where autograd
+ *              saves the same tensor.
  * D, delta_bias, h_init, length, z are nullable.  padding_right: 1 = valid
  * positions are t < length[b], 0 = t >= seqlen - length[b] (lengths are
  * clamped to [0, seqlen]); padded steps leave the state unchanged.
@@ -79,8 +83,9 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                            const void* u, const void* delta, const float* A, const void* B,
                            const void* C, const float* D, const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
-                           const void* z, int delta_softplus, void* out, float* h_chunks,
-                           float* h_last, void* workspace, size_t workspace_bytes, void* stream);
+                           const void* z, int delta_softplus, void* out, void* out_ungated,
+                           float* h_chunks, float* h_last, void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 /*
  * Selective-scan backward.  Replaces selective_scan_backward
@@ -91,7 +96,9 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
  * Inputs as for the forward plus h_chunks (from the forward), dout (the
  * upstream gradient of out; ignored at padded positions) and dh_last
  * (nullable = zero).  Writes du, ddelta, dA, dB, dC (all overwritten), and
- * when non-NULL dD, ddelta_bias, dh_init (requires h_init) and dz (requires z).
+ * when non-NULL dD, ddelta_bias and dh_init (requires h_init).  With z,
+ * out_ungated (the forward's ungated output) and dz are required; without z
+ * both must be NULL.
  * nstate <= 64.  workspace: ssm_scan_bwd_workspace_bytes() bytes.  The result
  * is deterministic (fixed-order reductions, no atomics on global memory).
  */
@@ -99,11 +106,11 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                            const void* u, const void* delta, const float* A, const void* B,
                            const void* C, const float* D, const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
-                           const void* z, int delta_softplus, const float* h_chunks,
-                           const void* dout, const float* dh_last, void* du, void* ddelta,
-                           float* dA, void* dB, void* dC, float* dD, float* ddelta_bias,
-                           float* dh_init, void* dz, void* workspace, size_t workspace_bytes,
-                           void* stream);
+                           const void* z, const void* out_ungated, int delta_softplus,
+                           const float* h_chunks, const void* dout, const float* dh_last,
+                           void* du, void* ddelta, float* dA, void* dB, void* dC, float* dD,
+                           float* ddelta_bias, float* dh_init, void* dz, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /*
  * One decode step.  Replaces selective_update

@@ -37,13 +37,13 @@ SIGNATURES = {
         _i64, _i64, _i64, _i64, _i32,          # batch, dim, seqlen, nstate, dtype
         _p, _p, _p, _p, _p, _p, _p, _p, _p,    # u, delta, A, B, C, D, delta_bias, h_init, length
         _i32, _p, _i32,                        # padding_right, z, delta_softplus
-        _p, _p, _p,                            # out, h_chunks, h_last
+        _p, _p, _p, _p,                        # out, out_ungated, h_chunks, h_last
         _p, _sz, _p,                           # workspace, bytes, stream
     ]),
     "ssm_selective_scan_bwd": (_i32, [
         _i64, _i64, _i64, _i64, _i32,
         _p, _p, _p, _p, _p, _p, _p, _p, _p,    # u, delta, A, B, C, D, delta_bias, h_init, length
-        _i32, _p, _i32,                        # padding_right, z, delta_softplus
+        _i32, _p, _p, _i32,                    # padding_right, z, out_ungated, delta_softplus
         _p, _p, _p,                            # h_chunks, dout, dh_last
         _p, _p, _p, _p, _p, _p, _p, _p, _p,    # du, ddelta, dA, dB, dC, dD, ddelta_bias, dh_init, dz
         _p, _sz, _p,                           # workspace, bytes, stream
@@ -87,7 +87,7 @@ SIGNATURES = {
     ]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def lib() -> ctypes.CDLL:

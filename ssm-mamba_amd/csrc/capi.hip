@@ -187,7 +187,7 @@ extern "C" {
 
 const char* ssm_last_error(void) { return g_err.c_str(); }
 
-int ssm_abi_version(void) { return 1; }
+int ssm_abi_version(void) { return 2; }
 
 int ssm_profile_begin(void) {
   g_err.clear();
@@ -266,18 +266,21 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                            const void* u, const void* delta, const float* A, const void* B,
                            const void* C, const float* D, const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
-                           const void* z, int delta_softplus, void* out, float* h_chunks,
-                           float* h_last, void* workspace, size_t workspace_bytes, void* stream) {
+                           const void* z, int delta_softplus, void* out, void* out_ungated,
+                           float* h_chunks, float* h_last, void* workspace, size_t workspace_bytes,
+                           void* stream) {
   g_err.clear();
   if (int e = check_common(batch, dim, seqlen, nstate, dtype, 256)) return e;
   if (!u || !delta || !A || !B || !C || !out)
     return fail(SSM_ERR_INVALID, "u, delta, A, B, C and out must be non-NULL");
+  if (out_ungated && !z) return fail(SSM_ERR_INVALID, "out_ungated requires z");
   const size_t need = ssm_scan_fwd_workspace_bytes(batch, dim, seqlen, nstate);
   if (!workspace || workspace_bytes < need)
     return fail(SSM_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
   ssm::ScanParams p = make_scan_params(batch, dim, seqlen, nstate, u, delta, A, B, C, D, delta_bias,
                                        h_init, length, padding_right, z, delta_softplus);
   p.out = out;
+  p.out_ungated = out_ungated;
   p.h_chunks = h_chunks;
   p.h_last = h_last;
   // workspace: [prepped B/C][segment states and step sums][dummy]
@@ -288,7 +291,7 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * batch * nstate * dim;
   ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));
   p.dummy = ws;
-  const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out});
+  const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out, out_ungated});
   return hip_status(ssm::launch_scan_fwd(p, dtype, aligned, static_cast<float*>(workspace),
                                          static_cast<hipStream_t>(stream)),
                     "selective_scan forward launch");
@@ -298,8 +301,9 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                            const void* u, const void* delta, const float* A, const void* B,
                            const void* C, const float* D, const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
-                           const void* z, int delta_softplus, const float* h_chunks,
-                           const void* dout, const float* dh_last, void* du, void* ddelta,
+                           const void* z, const void* out_ungated, int delta_softplus,
+                           const float* h_chunks, const void* dout, const float* dh_last,
+                           void* du, void* ddelta,
                            float* dA, void* dB, void* dC, float* dD, float* ddelta_bias,
                            float* dh_init, void* dz, void* workspace, size_t workspace_bytes,
                            void* stream) {
@@ -309,7 +313,9 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
     return fail(SSM_ERR_INVALID,
                 "u, delta, A, B, C, h_chunks, dout, du, ddelta, dA, dB and dC must be non-NULL");
   if (dh_init && !h_init) return fail(SSM_ERR_INVALID, "dh_init requires h_init");
-  if (dz && !z) return fail(SSM_ERR_INVALID, "dz requires z");
+  if ((dz || out_ungated) && !z) return fail(SSM_ERR_INVALID, "dz and out_ungated require z");
+  if (z && (!dz || !out_ungated))
+    return fail(SSM_ERR_INVALID, "z requires dz and out_ungated (the forward's ungated output)");
   const size_t need = ssm_scan_bwd_workspace_bytes(batch, dim, seqlen, nstate);
   if (!workspace || workspace_bytes < need)
     return fail(SSM_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
@@ -321,6 +327,7 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   p.du = du;
   p.ddelta = ddelta;
   p.dz = dz;
+  p.out_ungated = const_cast<void*>(out_ungated);
   p.dh_init = dh_init;
   p.dA = dA;
   p.dB = dB;
@@ -347,7 +354,7 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * batch * nstate * dim;
   ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));
   p.dummy = ws;
-  const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, dout, du, ddelta, dz});
+  const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out_ungated, dout, du, ddelta, dz});
   return hip_status(ssm::launch_scan_bwd(p, dtype, aligned, bc, static_cast<hipStream_t>(stream)),
                     "selective_scan backward launch");
 }

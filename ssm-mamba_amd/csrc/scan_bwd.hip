@@ -11,7 +11,8 @@
 //   dD       = sum dout * u,  dbias = sum ddelta,  dh_init = gamma_{-1}
 // dout is the upstream gradient masked to zero at padded positions (the loss
 // does not see them), times silu(z) when the z gate is fused; then
-// dz = dy * out * silu'(z) with out recomputed from the states.
+// dz = dy * y * silu'(z) with y the forward's ungated output (saved by the
+// forward, so the backward does not recompute sum_n C h).
 //
 // Work decomposition mirrors the forward (workgroup = batch row b x 64
 // channels, 8 waves, lane = channel, wave w = state pairs G = g*8 + w).  Tiles
@@ -21,7 +22,7 @@
 // reverse recurrence.  The tile's B/C block (prepped fp32 layout) is staged in
 // LDS together with the per-step values and read with broadcast LDS loads, so
 // the loop has no scalar-memory traffic and no scalar-register pressure.  Per-position
-// sums over states (sum G B, sum A G a h, sum C h) leave each wave in its own
+// sums over states (sum G B, sum A G a h) leave each wave in its own
 // LDS slice and are added in a fixed order; the per-position sums over
 // channels (dB, dC) are reduced across the 64 lanes with a permlane/DPP
 // reduce-scatter and written as one partial per (channel block, b, n, t),
@@ -126,7 +127,8 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const float* __restrict__ Ap, const float* __restrict__ bc,
     const float* __restrict__ Dp, const float* __restrict__ biasp,
     const float* __restrict__ h_init, const int64_t* __restrict__ length,
-    const T* __restrict__ zp, const float* __restrict__ h_chunks, const T* __restrict__ dyp,
+    const T* __restrict__ zp, const T* __restrict__ yup, const float* __restrict__ h_chunks,
+    const T* __restrict__ dyp,
     const float* __restrict__ dh_last, T* __restrict__ dup, T* __restrict__ ddp,
     T* __restrict__ dzp, float* __restrict__ dh_init, float* __restrict__ ws_bc,
     float* __restrict__ ws_A, float* __restrict__ ws_D, float* __restrict__ ws_bias,
@@ -151,7 +153,6 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   // added in a fixed order in phase C (deterministic result)
   __shared__ float4 sGB[kWaves][kT4][kBlockCh];  // sum_n G B
   __shared__ float4 sDD[kWaves][kT4][kBlockCh];  // sum_n A G a h_{t-1}
-  __shared__ float4 sY[kHasZ ? kWaves : 1][kT4][kBlockCh];  // sum_n C h
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -202,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
 
   // ---- tile-phase mapping.  Group 0 (waves 0-3) owns the u / delta side
   // (softplus, staging, then du, ddelta, dD, dbias); group 1 (waves 4-7) the
-  // dout / z side (the gate, staging dout, then dz).  Item = (channel row, 4
+  // dout / z side (the gate, staging dout, dz).  Item = (channel row, 4
   // consecutive steps) in both groups.
   const bool grp1 = w >= kWaves / 2;
   const int item = tid % kItems;
@@ -218,6 +219,9 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   const bool load2 = !grp1 || kHasZ;
   const T* __restrict__ row1 = (grp1 ? dyp : u) + (rb + a_chc) * L;
   const T* __restrict__ row2 = load2 ? (grp1 ? zp : dl) + (rb + a_chc) * L : row1;
+  // group 1: the ungated forward output (group 0 re-reads its u row, so both
+  // groups issue the same memory operations)
+  const T* __restrict__ row3 = (kHasZ && grp1) ? yup + (rb + a_chc) * L : row1;
   const bool softplus = p.softplus != 0;
   float accD = 0.0f, accB = 0.0f;
 
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   // clamped, valid address (masks are applied where the values are used):
   // a branch around a load, or a select on a value right after it, makes the
   // compiler wait for outstanding memory operations there.
-  R4 n1, n2;            // raw row pieces (group 0: u, delta; group 1: dout, z)
+  R4 n1, n2, n3;        // raw row pieces (group 0: u, delta; group 1: dout, z, y)
   float hcn[kSG][2];    // states saved by the forward before the tile
   float bcn[kSG][kT4];  // the tile's B/C blocks of the wave's pairs (block registers)
   const int chc = min(ch, Dm - 1);
@@ -233,6 +237,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const int t = tile * kTileB + a_col;
     n1 = load_raw4_nb<T, kAligned>(row1, t, L, a_ok);
     n2 = load_raw4_nb<T, kAligned>(row2, t, L, a_ok);
+    if constexpr (kHasZ) n3 = load_raw4_nb<T, kAligned>(row3, t, L, a_ok);
 #pragma unroll
     for (int g = 0; g < kSG; ++g) {
       const int Gc = min(g * kWaves + w, npair - 1);
@@ -254,7 +259,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
 
   float hc[kSG][2];
   float bcc[kSG][kT4];
-  float dzf[4];  // group 1: dy_masked * silu'(z), times out in phase C
+  float dzo[4];  // group 1: dz of the tile, stored in phase C
   // ---- phase A: stage a tile's per-position quantities in LDS and take its
   // saved states and B/C blocks
   auto phase_a = [&](const int tile) {
@@ -280,8 +285,9 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       sDu[a_q][a_sw] = make_float4(du[0], du[1], du[2], du[3]);
       sU[par][a_q][a_sw] = make_float4(v1[0], v1[1], v1[2], v1[3]);
       sSg[a_q][a_sw] = make_float4(sg[0], sg[1], sg[2], sg[3]);
-    } else {  // dy = v1, z = v2
-      float dov[4];
+    } else {  // dy = v1, z = v2, y = v3
+      float dov[4], v3[4];
+      if constexpr (kHasZ) decode4(n3, v3);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int tt = t0 + a_col + j;
@@ -290,10 +296,10 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         if constexpr (kHasZ) {
           const float sz = sigmoidf_fast(v2[j]);
           dov[j] = dym * (v2[j] * sz);
-          dzf[j] = dym * (sz * fmaf(v2[j], 1.0f - sz, 1.0f));
+          dzo[j] = dym * v3[j] * (sz * fmaf(v2[j], 1.0f - sz, 1.0f));
         } else {
           dov[j] = dym;
-          dzf[j] = 0.0f;
+          dzo[j] = 0.0f;
         }
       }
       sDout[par][a_q][a_sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
@@ -334,9 +340,8 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         }
       };
       auto fwd = [&](int jq, const StepVals& sv) {
-        float y[4];
+        float y[4];  // unused here (the forward saved the output)
         bwd_recompute_block(jq, sv, bcc[g][jq], A2[g], hc[g], a, H, y);
-        if constexpr (kHasZ) put4(sY[w], jq, y);
       };
       // the value of lane l after the reduction: index l >> 2 of the block's
       // 16 (kind = dB/dC, state, step); quads hold the same value
@@ -410,20 +415,6 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       store4_nb<T, kAligned>(dup + (rb + a_ch) * L, t, L, a_ok, dummy, duo);
       store4_nb<T, kAligned>(ddp + (rb + a_ch) * L, t, L, a_ok, dummy, ddo);
     } else {
-      float dzo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if constexpr (kHasZ) {
-        float4 ys = sY[0][a_q][a_sw];
-#pragma unroll
-        for (int ww = 1; ww < kWaves; ++ww) {
-          const float4 q3 = sY[ww][a_q][a_sw];
-          ys.x += q3.x; ys.y += q3.y; ys.z += q3.z; ys.w += q3.w;
-        }
-        const float ysv[4] = {ys.x, ys.y, ys.z, ys.w};
-        float uu[4];
-        f4_to(sU[par][a_q][a_sw], uu);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dzo[j] = dzf[j] * fmaf(Dv, uu[j], ysv[j]);
-      }
       store4_nb<T, kAligned>(dzp + (rb + a_ch) * L, t, L, kHasZ && a_ok, dummy, dzo);
       store4_nb<T, kAligned>(dzp, t, L, false, dummy, dzo);
     }
@@ -697,7 +688,8 @@ static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t 
   ProfScope prof("scan_bwd", st);
   hipLaunchKernelGGL((scan_bwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(kThreads), 0, st,
                      dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias,
-                     p.h_init, p.length, (const T*)p.z, p.h_chunks_in, (const T*)p.dout,
+                     p.h_init, p.length, (const T*)p.z, (const T*)p.out_ungated, p.h_chunks_in,
+                     (const T*)p.dout,
                      p.dh_last, (T*)p.du, (T*)p.ddelta, (T*)p.dz, p.dh_init, p.ws_bc, p.ws_A,
                      p.ws_D, p.ws_bias, p.dummy, p.seg_h, p.seg_dt);
   return hipGetLastError();

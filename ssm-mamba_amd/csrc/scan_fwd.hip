@@ -104,16 +104,21 @@ __device__ __forceinline__ void fwd_block(const float4 dl4, const float4 du4, co
 // segment s starts from h_init folded through the summaries of segments
 // 0..s-1 left by scan_fwd_segsum_kernel (h <- exp(A sum dt) h + h_seg, the
 // composition of the steps' affine maps).
-template <typename T, int kSG, bool kHasZ, bool kAligned>
+//
+// kZ: 0 no gate; 1 out = y * silu(z); 2 the same and the ungated y also
+// written to yu (the value the backward needs for dz).
+template <typename T, int kSG, int kZ, bool kAligned>
 __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
     const float* __restrict__ Ap, const float* __restrict__ bc,
     const float* __restrict__ Dp, const float* __restrict__ biasp,
     const float* __restrict__ h_init, const int64_t* __restrict__ length,
-    const T* __restrict__ zp, T* __restrict__ out, float* __restrict__ h_chunks,
-    float* __restrict__ h_last, void* __restrict__ dummy, const float* __restrict__ seg_h,
-    const float* __restrict__ seg_dt) {
+    const T* __restrict__ zp, T* __restrict__ out, T* __restrict__ yu,
+    float* __restrict__ h_chunks, float* __restrict__ h_last, void* __restrict__ dummy,
+    const float* __restrict__ seg_h, const float* __restrict__ seg_dt) {
   using R4 = typename Raw4<T>::type;
+  constexpr bool kHasZ = kZ != 0;
+  constexpr bool kSaveY = kZ == 2;
   constexpr int kT4 = kTileF / 4;        // 4-step columns per sub-tile
   constexpr int kSup = kSubF * kTileF;   // steps staged per super-tile
   static_assert(kBlockCh * kT4 == kThreads, "one 4-step row piece per thread");
@@ -441,6 +446,10 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
           y[1] = skip[i][1] + acc.y;
           y[2] = skip[i][2] + acc.z;
           y[3] = skip[i][3] + acc.w;
+          if constexpr (kSaveY) {
+            if constexpr (kFull) store4_nb<T, kAligned>(yu + (rb + a_ch) * L, t, L, a_ok, dummy, y);
+            else store4<T, kAligned>(yu + (rb + a_ch) * L, t, L, y);
+          }
           if constexpr (kHasZ) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) y[j] *= gate[i][j];
@@ -702,7 +711,7 @@ hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t
   return hipGetLastError();
 }
 
-template <typename T, int kSG, bool kHasZ, bool kAligned>
+template <typename T, int kSG, int kZ, bool kAligned>
 static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t st) {
   if (p.nseg > 1) {
     ProfScope prof("scan_fwd_segsum", st);
@@ -714,21 +723,24 @@ static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t 
     if (e != hipSuccess) return e;
   }
   ProfScope prof("scan_fwd", st);
-  hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kHasZ, kAligned>),
+  hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kZ, kAligned>),
                      dim3(p.nblk, p.batch, p.nseg), dim3(kThreads), 0, st, dims_of(p),
                      (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias, p.h_init, p.length,
-                     (const T*)p.z, (T*)p.out, p.h_chunks, p.h_last, p.dummy, p.seg_h, p.seg_dt);
+                     (const T*)p.z, (T*)p.out, (T*)p.out_ungated, p.h_chunks, p.h_last, p.dummy,
+                     p.seg_h, p.seg_dt);
   return hipGetLastError();
 }
 
 template <typename T, int kSG>
 static hipError_t launch_fwd3(const ScanParams& p, const float* bc, bool aligned, hipStream_t st) {
-  const bool z = p.z != nullptr;
-  if (z)
-    return aligned ? launch_fwd4<T, kSG, true, true>(p, bc, st)
-                   : launch_fwd4<T, kSG, true, false>(p, bc, st);
-  return aligned ? launch_fwd4<T, kSG, false, true>(p, bc, st)
-                 : launch_fwd4<T, kSG, false, false>(p, bc, st);
+  if (p.z && p.out_ungated)
+    return aligned ? launch_fwd4<T, kSG, 2, true>(p, bc, st)
+                   : launch_fwd4<T, kSG, 2, false>(p, bc, st);
+  if (p.z)
+    return aligned ? launch_fwd4<T, kSG, 1, true>(p, bc, st)
+                   : launch_fwd4<T, kSG, 1, false>(p, bc, st);
+  return aligned ? launch_fwd4<T, kSG, 0, true>(p, bc, st)
+                 : launch_fwd4<T, kSG, 0, false>(p, bc, st);
 }
 
 template <typename T>

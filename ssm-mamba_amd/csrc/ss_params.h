@@ -47,6 +47,9 @@ struct ScanParams {
   const float* h_init; // nullable
   const int64_t* length;  // nullable
   const void* z;       // nullable
+  // ungated output D*u + sum_n C*h (with z): written by the forward when
+  // non-null, read by the backward for dz
+  void* out_ungated;
 
   // forward outputs
   void* out;
@@ -97,6 +100,9 @@ struct UpdateParams {
   const float* D;      // nullable
   const float* bias;   // nullable
   const void* z;       // nullable
+  // ungated output D*u + sum_n C*h (with z): written by the forward when
+  // non-null, read by the backward for dz
+  void* out_ungated;
   void* out;
 };
 

@@ -76,10 +76,14 @@ class _SelectiveScanExtFn(torch.autograd.Function):
                                 for t in (A, D, delta_bias, h_init))
         length = ensure_contiguous(length)
         need_grad = any(ctx.needs_input_grad)
+        # with the gate, the backward needs the ungated output (what autograd
+        # saves for the reference's out * silu(z) outside the kernel)
+        y = torch.empty_like(u) if (need_grad and z is not None) else None
         out, h = selective_scan.forward(u, A32, B, C, D32, delta, bias32, h0, length, padding_side,
-                                        z=z, delta_softplus=delta_softplus, save_chunks=need_grad)
+                                        z=z, delta_softplus=delta_softplus, save_chunks=need_grad,
+                                        out_ungated=y)
         if need_grad:
-            ctx.save_for_backward(u, delta, A32, B, C, D32, z, bias32, h, h0, length)
+            ctx.save_for_backward(u, delta, A32, B, C, D32, z, y, bias32, h, h0, length)
             ctx.delta_softplus = delta_softplus
             ctx.padding_side = padding_side
             return out, selective_scan.last_state(h)
@@ -87,11 +91,12 @@ class _SelectiveScanExtFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, dh_last):
-        u, delta, A, B, C, D, z, bias, h, h0, length = ctx.saved_tensors
+        u, delta, A, B, C, D, z, y, bias, h, h0, length = ctx.saved_tensors
         dout = ensure_contiguous(dout.to(u.dtype))
         dh_last = None if dh_last is None else ensure_contiguous(dh_last.float())
         res = selective_scan.backward(u, A, B, C, D, delta, bias, h, h0, dout, dh_last, length,
-                                      ctx.padding_side, z=z, delta_softplus=ctx.delta_softplus)
+                                      ctx.padding_side, z=z, delta_softplus=ctx.delta_softplus,
+                                      out_ungated=y)
         du, dA, dB, dC, dD, ddelta, dbias, dh0 = res[:8]
         dz = res[8] if z is not None else None
         return du, ddelta, dA, dB, dC, dD, dz, dbias, dh0, None, None, None

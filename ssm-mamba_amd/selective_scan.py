@@ -19,6 +19,11 @@ Differences, all deliberate:
 * Keyword extensions: ``z`` (fused output gate out * silu(z)),
   ``delta_softplus`` and, for ``forward``, ``save_chunks=False`` (inference:
   only the final state is produced).
+* With z, ``forward(..., out_ungated=y)`` also writes the ungated output
+  D*u + sum_n C*h into y, and ``backward`` takes it back
+  (``out_ungated=y``, required with z) for dz = dy * y * silu'(z); the
+  reference applies the gate outside the kernel, where autograd saves the
+  same tensor.
 """
 from __future__ import annotations
 
@@ -115,12 +120,19 @@ def forward(u: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
             D: Optional[torch.Tensor], delta: torch.Tensor, delta_bias: Optional[torch.Tensor],
             h_init: Optional[torch.Tensor] = None, length: Optional[torch.Tensor] = None,
             padding_side: Optional[str] = None, *, z: Optional[torch.Tensor] = None,
-            delta_softplus: bool = True, save_chunks: bool = True) -> List[torch.Tensor]:
+            delta_softplus: bool = True, save_chunks: bool = True,
+            out_ungated: Optional[torch.Tensor] = None) -> List[torch.Tensor]:
     """Returns [out, h]: out (batch, dim, seqlen) in u's dtype (gated by silu(z)
     when z is given) and h, the chunk-state carrier (batch, nchunks,
     state_dim, dim) float32 -- or, with save_chunks=False, the final state
-    (batch, dim, state_dim)."""
+    (batch, dim, state_dim).  out_ungated (with z): a (batch, dim, seqlen)
+    tensor of u's dtype that receives the output before the gate."""
     batch, dim, seqlen, nstate = _validate(u, A, B, C, D, delta, delta_bias, h_init, length, z)
+    if out_ungated is not None:
+        if z is None:
+            raise RuntimeError("out_ungated requires z")
+        _check(out_ungated, "out_ungated", (batch, dim, seqlen), "batch_size, num_channels, seq_len",
+               (u.dtype,), str(u.dtype).replace("torch.", "") + " (the dtype of u)")
     L = N.lib()
     dev = u.device
     out = torch.empty_like(u)
@@ -138,8 +150,8 @@ def forward(u: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
             batch, dim, seqlen, nstate, _STREAM_DTYPES[u.dtype],
             u.data_ptr(), delta.data_ptr(), A.data_ptr(), B.data_ptr(), C.data_ptr(),
             _ptr(D), _ptr(delta_bias), _ptr(h_init), _ptr(length), padding_right, _ptr(z),
-            1 if delta_softplus else 0, out.data_ptr(), _ptr(h_chunks), _ptr(h_last),
-            ws.data_ptr(), wsb, _stream(dev)))
+            1 if delta_softplus else 0, out.data_ptr(), _ptr(out_ungated), _ptr(h_chunks),
+            _ptr(h_last), ws.data_ptr(), wsb, _stream(dev)))
     return [out, h]
 
 
@@ -148,12 +160,19 @@ def backward(u: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
              h: torch.Tensor, h_init: Optional[torch.Tensor], dout: torch.Tensor,
              dh_last: Optional[torch.Tensor], length: Optional[torch.Tensor] = None,
              padding_side: Optional[str] = None, *, z: Optional[torch.Tensor] = None,
-             delta_softplus: bool = True) -> List[Optional[torch.Tensor]]:
+             delta_softplus: bool = True,
+             out_ungated: Optional[torch.Tensor] = None) -> List[Optional[torch.Tensor]]:
     """Returns [du, dA, dB, dC, dD, ddelta, ddelta_bias, dh_init] (+ [dz] when z
     is given), the reference's order (``selective_scan.cpp:376``).  dD /
     ddelta_bias are None when D / delta_bias are None; dh_init is None without
-    h_init."""
+    h_init.  With z, out_ungated is the forward's ungated output."""
     batch, dim, seqlen, nstate = _validate(u, A, B, C, D, delta, delta_bias, h_init, length, z)
+    if (z is None) != (out_ungated is None):
+        raise RuntimeError("backward with z requires out_ungated (the forward's ungated output)"
+                           if z is not None else "out_ungated requires z")
+    if out_ungated is not None:
+        _check(out_ungated, "out_ungated", (batch, dim, seqlen), "batch_size, num_channels, seq_len",
+               (u.dtype,), str(u.dtype).replace("torch.", "") + " (the dtype of u)")
     if nstate > 64:
         raise RuntimeError("selective_scan backward only supports state_dim <= 64")
     _check_dim(h, 4, "h")
@@ -184,7 +203,8 @@ def backward(u: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
             batch, dim, seqlen, nstate, _STREAM_DTYPES[u.dtype],
             u.data_ptr(), delta.data_ptr(), A.data_ptr(), B.data_ptr(), C.data_ptr(),
             _ptr(D), _ptr(delta_bias), _ptr(h_init), _ptr(length), padding_right, _ptr(z),
-            1 if delta_softplus else 0, h.data_ptr(), dout.data_ptr(), _ptr(dh_last),
+            _ptr(out_ungated), 1 if delta_softplus else 0, h.data_ptr(), dout.data_ptr(),
+            _ptr(dh_last),
             du.data_ptr(), ddelta.data_ptr(), dA.data_ptr(), dB.data_ptr(), dC.data_ptr(),
             _ptr(dD), _ptr(dbias), _ptr(dh_init), _ptr(dz), ws.data_ptr(), wsb, _stream(dev)))
     res = [du, dA, dB, dC, dD, ddelta, dbias, dh_init]

@@ -21,10 +21,11 @@ def test_scan_golden(cuda, path):
     pad = "right" if bool(g["padding_right"]) else "left"
     sp = bool(g["softplus"])
     args = (d["u"], d["A"], d["B"], d["C"], d.get("D"), d["delta"], d.get("delta_bias"))
+    y = None if d.get("z") is None else torch.empty_like(d["u"])
     out, h = ss.forward(*args, d.get("h_init"), d.get("length"), pad, z=d.get("z"),
-                        delta_softplus=sp)
+                        delta_softplus=sp, out_ungated=y)
     res = ss.backward(*args, h, d.get("h_init"), d["dy"], d.get("dh_last"), d.get("length"), pad,
-                      z=d.get("z"), delta_softplus=sp)
+                      z=d.get("z"), delta_softplus=sp, out_ungated=y)
     torch.cuda.synchronize()
     ref = lambda k: torch.from_numpy(g["out_" + k])
     f32 = torch.float32

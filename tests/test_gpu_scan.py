@@ -29,12 +29,16 @@ def run_case(cuda, batch, dim, seqlen, nstate, dtype, *, seed=0, with_z=True, h_
     d = to_dev(c, cuda)
     ln_dev = None if length is None else length.to(cuda)
     pr = (padding_side or "right") == "right"
+    y = None if d["z"] is None else torch.empty_like(d["u"])
     out, h = ss.forward(d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"],
-                        d["h_init"], ln_dev, padding_side, z=d["z"], delta_softplus=softplus)
+                        d["h_init"], ln_dev, padding_side, z=d["z"], delta_softplus=softplus,
+                        out_ungated=y)
     ref = R.scan_fwd(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["delta_bias"],
                      c["h_init"], length, pr, c["z"], softplus)
     torch.cuda.synchronize()
     assert_close(out, ref["y"], dtype, "out")
+    if y is not None:
+        assert_close(y, ref["out"], dtype, "out_ungated")
     assert_close(h.permute(0, 3, 1, 2), ref["h_chunks"],
                  torch.float32 if dtype == torch.float32 else dtype, "h_chunks", scale_atol=True)
     if not bwd:
@@ -44,7 +48,7 @@ def run_case(cuda, batch, dim, seqlen, nstate, dtype, *, seed=0, with_z=True, h_
     dl = torch.randn(batch, dim, nstate, generator=g) if dlast else None
     res = ss.backward(d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"], h,
                       d["h_init"], dy.to(cuda), None if dl is None else dl.to(cuda), ln_dev,
-                      padding_side, z=d["z"], delta_softplus=softplus)
+                      padding_side, z=d["z"], delta_softplus=softplus, out_ungated=y)
     rb = R.scan_bwd(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["delta_bias"],
                     c["h_init"], length, pr, c["z"], softplus, dy=dy, dh_last=dl)
     torch.cuda.synchronize()
@@ -137,8 +141,9 @@ def test_config1_full_size_properties(cuda):
     batch, dim, seqlen, nstate = 8, 2048, 2048, 16
     c = make_case(batch, dim, seqlen, nstate, torch.bfloat16, seed=1)
     d = to_dev(c, cuda)
+    y = torch.empty_like(d["u"])
     out, h = ss.forward(d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"],
-                        None, None, None, z=d["z"])
+                        None, None, None, z=d["z"], out_ungated=y)
     sub = slice(0, 2048, 97)  # 22 channels spread over the channel blocks
     cs = {k: (v[:, sub] if k in ("u", "delta", "z") else v) for k, v in c.items()}
     cs["A"], cs["D"], cs["delta_bias"] = c["A"][sub], c["D"][sub], c["delta_bias"][sub]
@@ -150,8 +155,8 @@ def test_config1_full_size_properties(cuda):
     g = torch.Generator().manual_seed(5)
     dy = torch.randn(batch, dim, seqlen, generator=g).to(torch.bfloat16).to(cuda)
     args = (d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"], h, None, dy, None)
-    r1 = ss.backward(*args, z=d["z"])
-    r2 = ss.backward(*args, z=d["z"])
+    r1 = ss.backward(*args, z=d["z"], out_ungated=y)
+    r2 = ss.backward(*args, z=d["z"], out_ungated=y)
     for a, b_ in zip(r1, r2):
         if a is not None:
             assert torch.equal(a, b_), "backward is not deterministic"
@@ -161,11 +166,12 @@ def test_config1_full_size_properties(cuda):
         dh = {k: (v[:, lo:hi].contiguous() if k in ("u", "delta", "z") else v) for k, v in d.items()}
         dh["A"], dh["D"], dh["delta_bias"] = d["A"][lo:hi].contiguous(), d["D"][lo:hi].contiguous(), \
             d["delta_bias"][lo:hi].contiguous()
+        yh = torch.empty_like(dh["u"])
         _, hh = ss.forward(dh["u"], dh["A"], dh["B"], dh["C"], dh["D"], dh["delta"],
-                           dh["delta_bias"], None, None, None, z=dh["z"])
+                           dh["delta_bias"], None, None, None, z=dh["z"], out_ungated=yh)
         halves.append(ss.backward(dh["u"], dh["A"], dh["B"], dh["C"], dh["D"], dh["delta"],
                                   dh["delta_bias"], hh, None, dy[:, lo:hi].contiguous(), None,
-                                  z=dh["z"]))
+                                  z=dh["z"], out_ungated=yh))
     for idx, nm in ((2, "dB"), (3, "dC")):
         # each of the three results is rounded to bf16 once (relative error
         # <= 2^-9); the fp32 partial sums agree to ~1e-6

@@ -44,22 +44,44 @@ def test_invalid_arguments_return_errors():
     from ssm_mamba_amd import _native as N
     lib = N.lib()
     rc = lib.ssm_selective_scan_fwd(1, 1, 1, 300, 0, *([None] * 9), 1, None, 1, None, None, None,
-                                    None, 0, None)
+                                    None, None, 0, None)
     assert rc == 2 and b"state_dim <= 256" in lib.ssm_last_error()
     rc = lib.ssm_selective_scan_fwd(1, 1, 0, 16, 0, *([None] * 9), 1, None, 1, None, None, None,
-                                    None, 0, None)
+                                    None, None, 0, None)
     assert rc == 1 and b">= 1" in lib.ssm_last_error()
     rc = lib.ssm_selective_scan_fwd(1, 1, 1, 16, 7, *([None] * 9), 1, None, 1, None, None, None,
-                                    None, 0, None)
+                                    None, None, 0, None)
     assert rc == 1 and b"dtype" in lib.ssm_last_error()
     rc = lib.ssm_selective_scan_fwd(1, 1, 1, 16, 0, *([None] * 9), 1, None, 1, None, None, None,
-                                    None, 0, None)
+                                    None, None, 0, None)
     assert rc == 1 and b"non-NULL" in lib.ssm_last_error()
-    rc = lib.ssm_selective_scan_bwd(1, 1, 1, 65, 0, *([None] * 9), 1, None, 1, None, None, None,
-                                    *([None] * 9), None, 0, None)
+    rc = lib.ssm_selective_scan_bwd(1, 1, 1, 65, 0, *([None] * 9), 1, None, None, 1, None, None,
+                                    None, *([None] * 9), None, 0, None)
     assert rc == 2 and b"state_dim <= 64" in lib.ssm_last_error()
     rc = lib.ssm_selective_state_update(1, 1, 16, 0, *([None] * 10), 1, None, None)
     assert rc == 1 and b"non-NULL" in lib.ssm_last_error()
+
+
+def test_gate_arguments_are_checked():
+    """With z the backward needs the forward's ungated output and dz; without z
+    neither may be given.  The checks return before any pointer is used, so
+    placeholder addresses stand in for the device buffers (no GPU needed)."""
+    from ssm_mamba_amd import _native as N
+    lib = N.lib()
+    P = 4096  # never dereferenced: every call below fails its argument checks
+
+    def bwd(z, y, dz):
+        return lib.ssm_selective_scan_bwd(1, 64, 16, 16, 0, P, P, P, P, P, None, None, None, None,
+                                          1, z, y, 1, P, P, None, P, P, P, P, P, None, None, None,
+                                          dz, P, 1 << 30, None)
+
+    for z, y, dz in ((P, None, P), (P, P, None), (P, None, None)):
+        assert bwd(z, y, dz) == 1 and b"requires dz and out_ungated" in lib.ssm_last_error()
+    for y, dz in ((P, None), (None, P), (P, P)):
+        assert bwd(None, y, dz) == 1 and b"require z" in lib.ssm_last_error()
+    rc = lib.ssm_selective_scan_fwd(1, 64, 16, 16, 0, P, P, P, P, P, None, None, None, None, 1,
+                                    None, 1, P, P, P, None, P, 1 << 30, None)
+    assert rc == 1 and b"out_ungated requires z" in lib.ssm_last_error()
 
 
 def _scan_args(batch=2, dim=4, seqlen=8, nstate=3):
