@@ -631,32 +631,55 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_segsum_kernel(
 }
 
 // Adds the partial sums: dB/dC over channel blocks, dA/dD/dbias over the
-// (segment, batch row) rows, each in a fixed order.
-template <typename T>
+// (segment, batch row) rows, each in a fixed order.  kVec: dB/dC four
+// consecutive elements per thread (128-bit partial loads, 4-element stores;
+// batch * nstate * seqlen a multiple of 4 and dB/dC aligned), so a thread
+// keeps nblk 16-byte loads in flight.
+template <typename T, bool kVec>
 __global__ __launch_bounds__(256) void scan_bwd_reduce_kernel(
     const int batch, const int rows, const int dim, const int N, const int L, const int nblk,
     const float* __restrict__ ws_bc, const float* __restrict__ ws_A,
     const float* __restrict__ ws_D, const float* __restrict__ ws_bias, T* __restrict__ dB,
     T* __restrict__ dC, float* __restrict__ dA, float* __restrict__ dD,
     float* __restrict__ dbias) {
+  constexpr int kW = kVec ? 4 : 1;  // dB/dC elements per work item
   const size_t nBC = (size_t)batch * N * L;
   const size_t nA = (size_t)dim * N;
-  const size_t total = 2 * nBC + nA + dim;
+  const size_t nbc_items = 2 * nBC / kW;
+  const size_t total = nbc_items + nA + dim;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
-    if (i < 2 * nBC) {
-      const size_t kind = i / nBC, r = i % nBC;
+    if (i < nbc_items) {
+      const size_t e = i * kW;
+      const size_t kind = e / nBC, r = e % nBC;
       const float* src = ws_bc + kind * nblk * nBC + r;
-      float s = 0.0f;
-      for (int k = 0; k < nblk; ++k) s += src[(size_t)k * nBC];
-      Elem<T>::store1((kind ? dC : dB) + r, s);
-    } else if (i < 2 * nBC + nA) {
-      const size_t r = i - 2 * nBC;
-      float s = 0.0f;
-      for (int bb = 0; bb < rows; ++bb) s += ws_A[(size_t)bb * nA + r];
-      dA[r] = s;
+      T* dst = (kind ? dC : dB) + r;
+      if constexpr (kVec) {
+        float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+        for (int k = 0; k < nblk; ++k) {
+          const float4 v = *reinterpret_cast<const float4*>(src + (size_t)k * nBC);
+          s4.x += v.x; s4.y += v.y; s4.z += v.z; s4.w += v.w;
+        }
+        const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+        if constexpr (sizeof(T) == 4) {
+          *reinterpret_cast<float4*>(dst) = s4;
+        } else {
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2(pack_bf16x2(sv[0], sv[1]), pack_bf16x2(sv[2], sv[3]));
+        }
+      } else {
+        float acc = 0.0f;
+        for (int k = 0; k < nblk; ++k) acc += src[(size_t)k * nBC];
+        Elem<T>::store1(dst, acc);
+      }
+    } else if (i < nbc_items + nA) {
+      const size_t r = i - nbc_items;
+      float acc = 0.0f;
+      for (int bb = 0; bb < rows; ++bb) acc += ws_A[(size_t)bb * nA + r];
+      dA[r] = acc;
     } else {
-      const size_t d = i - 2 * nBC - nA;
+      const size_t d = i - nbc_items - nA;
       float sd = 0.0f, sb = 0.0f;
       for (int bb = 0; bb < rows; ++bb) {
         sd += ws_D[(size_t)bb * dim + d];
@@ -711,13 +734,21 @@ static hipError_t launch_bwd2(const ScanParams& p, const float* bc, bool aligned
   else if (p.nstate <= 32) e = launch_bwd3<T, 2>(p, bc, aligned, st);
   else e = launch_bwd3<T, 4>(p, bc, aligned, st);
   if (e != hipSuccess) return e;
-  const size_t total = 2 * (size_t)p.batch * p.nstate * p.seqlen + (size_t)p.dim * p.nstate + p.dim;
+  const size_t nBC = (size_t)p.batch * p.nstate * p.seqlen;
+  const uintptr_t vec_align = 4 * sizeof(T);
+  const bool vec = nBC % 4 == 0 && (uintptr_t)p.dB % vec_align == 0 &&
+                   (uintptr_t)p.dC % vec_align == 0;
+  const size_t total = 2 * nBC / (vec ? 4 : 1) + (size_t)p.dim * p.nstate + p.dim;
   const int blocks = (int)std::min<size_t>((total + 255) / 256, 16384);
   ProfScope prof("scan_bwd_reduce", st);
-  hipLaunchKernelGGL(scan_bwd_reduce_kernel<T>, dim3(blocks), dim3(256), 0, st, p.batch,
-                     p.batch * p.nseg, p.dim, p.nstate, p.seqlen, p.nblk, p.ws_bc, p.ws_A, p.ws_D,
-                     p.ws_bias, (T*)p.dB,
-                     (T*)p.dC, p.dA, p.dD, p.dbias);
+  if (vec)
+    hipLaunchKernelGGL((scan_bwd_reduce_kernel<T, true>), dim3(blocks), dim3(256), 0, st, p.batch,
+                       p.batch * p.nseg, p.dim, p.nstate, p.seqlen, p.nblk, p.ws_bc, p.ws_A,
+                       p.ws_D, p.ws_bias, (T*)p.dB, (T*)p.dC, p.dA, p.dD, p.dbias);
+  else
+    hipLaunchKernelGGL((scan_bwd_reduce_kernel<T, false>), dim3(blocks), dim3(256), 0, st, p.batch,
+                       p.batch * p.nseg, p.dim, p.nstate, p.seqlen, p.nblk, p.ws_bc, p.ws_A,
+                       p.ws_D, p.ws_bias, (T*)p.dB, (T*)p.dC, p.dA, p.dD, p.dbias);
   return hipGetLastError();
 }
 

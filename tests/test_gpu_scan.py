@@ -79,6 +79,14 @@ def test_state_dims(cuda, nstate):
     run_case(cuda, 2, 64, 80, nstate, torch.float32, seed=nstate, h_init=True, dlast=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("nstate", [1, 3])
+def test_odd_partial_count(cuda, dtype, nstate):
+    """batch * nstate * seqlen not a multiple of 4: the dB/dC partial sums
+    take the element-wise reduction path."""
+    run_case(cuda, 1, 64, 37, nstate, dtype, seed=40 + nstate, h_init=True, dlast=True)
+
+
 @pytest.mark.parametrize("nstate", [128, 200, 256])
 def test_state_dims_forward_large(cuda, nstate):
     run_case(cuda, 1, 64, 48, nstate, torch.float32, seed=nstate, bwd=False)
