@@ -149,13 +149,17 @@ int ssm_rms_norm_cm(int64_t batch, int64_t channels, int64_t seqlen, int dtype, 
  *   out[b,c,t] = act(bias[c] + sum_{j<width} weight[c,j] * x[b,c,t-(width-1)+j]),
  *   x = 0 before t = 0; act = silu when silu != 0, else the identity.
  * x, out (batch, dim, seqlen); weight (dim, width) (the (dim, 1, width) conv
- * weight); bias (dim) nullable.  All of x, out, weight, bias (and the
+ * weight); bias (dim) nullable.  All of x, out, weight, bias, window (and the
  * gradients below) have element type `dtype`; arithmetic is fp32.
  * width <= 8.
+ * window (nullable): (batch, dim, width-1) receives the decode cache a
+ * prefill leaves (modules/mamba.py:113-135): the width-1 inputs x[b,c,t] for
+ * t = len-(width-1) .. len-1, zero for t < 0, with len = lengths[b] clamped to
+ * [0, seqlen] (lengths nullable: len = seqlen; lengths requires window).
  */
 int ssm_causal_conv1d_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t width, int dtype,
                           const void* x, const void* weight, const void* bias, int silu, void* out,
-                          void* stream);
+                          const int64_t* lengths, void* window, void* stream);
 
 /* Device workspace (bytes) for ssm_causal_conv1d_bwd. */
 size_t ssm_causal_conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t width);

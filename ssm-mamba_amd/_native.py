@@ -55,7 +55,8 @@ SIGNATURES = {
     ]),
     "ssm_causal_conv1d_fwd": (_i32, [
         _i64, _i64, _i64, _i64, _i32,          # batch, dim, seqlen, width, dtype
-        _p, _p, _p, _i32, _p, _p,              # x, weight, bias, silu, out, stream
+        _p, _p, _p, _i32, _p,                  # x, weight, bias, silu, out
+        _p, _p, _p,                            # lengths, window, stream
     ]),
     "ssm_causal_conv1d_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "ssm_causal_conv1d_bwd": (_i32, [

@@ -34,7 +34,8 @@ def _check_x(x: torch.Tensor) -> None:
 class CausalConv1dFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
-                silu: bool) -> torch.Tensor:
+                silu: bool, lengths: Optional[torch.Tensor] = None,
+                window: Optional[torch.Tensor] = None) -> torch.Tensor:
         _check_x(x)
         x = x.contiguous()
         batch, dim, seqlen = x.shape
@@ -46,12 +47,27 @@ class CausalConv1dFn(torch.autograd.Function):
         if b is not None and b.numel() != dim:
             raise RuntimeError("bias must have shape (channels,)")
         out = torch.empty_like(x)
+        if window is not None:
+            if (tuple(window.shape) != (batch, dim, width - 1) or window.dtype != x.dtype
+                    or not window.is_contiguous() or window.device != x.device):
+                raise RuntimeError("window must be a contiguous (batch, channels, width - 1) "
+                                   "tensor of x's dtype on x's device")
+        if lengths is not None:
+            if window is None:
+                raise RuntimeError("lengths requires window")
+            if (lengths.dtype != torch.int64 or tuple(lengths.shape) != (batch,)
+                    or lengths.device != x.device):
+                raise RuntimeError("lengths must be an int64 (batch,) tensor on x's device")
+            lengths = lengths.contiguous()
         L = N.lib()
         with torch.cuda.device(x.device):
             N.check(L.ssm_causal_conv1d_fwd(batch, dim, seqlen, width, _DTYPES[x.dtype],
                                             x.data_ptr(), w.data_ptr(),
                                             None if b is None else b.data_ptr(), int(silu),
-                                            out.data_ptr(), _stream(x.device)))
+                                            out.data_ptr(),
+                                            None if lengths is None else lengths.data_ptr(),
+                                            None if window is None else window.data_ptr(),
+                                            _stream(x.device)))
         ctx.save_for_backward(x, w, b)
         ctx.silu = silu
         ctx.weight_shape = weight.shape
@@ -81,14 +97,19 @@ class CausalConv1dFn(torch.autograd.Function):
         dw = dw.reshape(ctx.weight_shape).to(ctx.weight_dtype)
         if db is not None:
             db = db.to(ctx.bias_dtype)
-        return dx, dw, db, None
+        return dx, dw, db, None, None, None
 
 
 def causal_conv1d_fn(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
-                     activation: Optional[str] = "silu") -> torch.Tensor:
+                     activation: Optional[str] = "silu", *,
+                     window: Optional[torch.Tensor] = None,
+                     lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
     """act(causal depthwise conv1d(x)) for x (batch, channels, seq_len) with
     weight (channels, 1, width) or (channels, width), width <= 8, optional bias
-    (channels,); ``activation`` is "silu" or None."""
+    (channels,); ``activation`` is "silu" or None.  ``window`` (batch,
+    channels, width - 1), if given, receives the decode cache of a prefill:
+    the width - 1 inputs ending at position lengths[b] - 1 (seq_len - 1
+    without lengths), zero before the row start (``modules/mamba.py:113-135``)."""
     if activation not in (None, "silu"):
         raise RuntimeError("activation must be 'silu' or None")
-    return CausalConv1dFn.apply(x, weight, bias, activation == "silu")
+    return CausalConv1dFn.apply(x, weight, bias, activation == "silu", lengths, window)

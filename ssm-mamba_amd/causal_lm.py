@@ -70,11 +70,13 @@ def rms_norm_cm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tens
     return out
 
 
-def causal_conv_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]):
+def causal_conv_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+                     window: Optional[torch.Tensor] = None,
+                     lengths: Optional[torch.Tensor] = None):
     """silu(causal depthwise conv1d(x)) over channel-major x (batch, channels, L)
     in one HIP kernel: ``modules/mamba.py:138-139`` (left zero padding of k-1,
-    keep the first L)."""
-    return causal_conv1d_fn(x, weight, bias, activation="silu")
+    keep the first L); ``window`` receives the decode conv cache."""
+    return causal_conv1d_fn(x, weight, bias, activation="silu", window=window, lengths=lengths)
 
 
 class RMSNorm(nn.Module):
@@ -158,6 +160,23 @@ class Mamba(nn.Module):
 
         self._ssm_hiddens: Optional[torch.Tensor] = None   # (batch, inner, N) float32
         self._conv_context: Optional[torch.Tensor] = None  # (batch, inner, k-1)
+        self._param_cache = None
+
+    def _scan_params(self):
+        """(A, D, delta_bias) for the scan: A = -exp(log_A) (``modules/mamba.py:166``)
+        and D / delta_bias in float32.  Without autograd they are kept and
+        recomputed only when a parameter changes (its version counter, storage,
+        dtype or device), so an inference prefill runs no conversion kernels."""
+        bias = self.delta_proj.bias
+        if torch.is_grad_enabled():
+            return -torch.exp(self.log_A.float()), self.D, bias
+        key = tuple(None if t is None else (t._version, t.data_ptr(), t.dtype, t.device)
+                    for t in (self.log_A, self.D, bias))
+        if self._param_cache is None or self._param_cache[0] != key:
+            self._param_cache = (key, -torch.exp(self.log_A.detach().float()),
+                                 self.D.detach().float(),
+                                 None if bias is None else bias.detach().float())
+        return self._param_cache[1:]
 
     # ---- caches ---------------------------------------------------------
     def allocate_cache(self, batch: int, device=None, dtype=None) -> None:
@@ -186,17 +205,16 @@ class Mamba(nn.Module):
             return old
         return new.clone(memory_format=torch.contiguous_format)
 
-    def _store_conv_context(self, xs: torch.Tensor, lengths: Optional[torch.Tensor]) -> None:
-        """The k-1 pre-conv inputs ending at position lengths-1, zero where the
-        window starts before the sequence (``modules/mamba.py:113-135``)."""
-        batch, inner, seqlen = xs.shape
-        k1 = self.conv_kernel - 1
-        if lengths is None:
-            lengths = torch.full((batch,), seqlen, device=xs.device, dtype=torch.long)
-        idx = lengths[:, None] - k1 + torch.arange(k1, device=xs.device)
-        ctx = xs.gather(2, idx.clamp(min=0)[:, None, :].expand(batch, inner, k1))
-        ctx = ctx * (idx >= 0)[:, None, :].to(ctx.dtype)
-        self._conv_context = self._keep(self._conv_context, ctx.detach())
+    def _conv_window(self, xs: torch.Tensor) -> torch.Tensor:
+        """The buffer a prefill's conv kernel fills with the decode conv cache:
+        the existing cache when it fits (its address stays fixed for a captured
+        decode graph), else a new one."""
+        shape = (xs.shape[0], xs.shape[1], self.conv_kernel - 1)
+        ctx = self._conv_context
+        if (ctx is not None and tuple(ctx.shape) == shape and ctx.dtype == xs.dtype
+                and ctx.device == xs.device and ctx.is_contiguous()):
+            return ctx
+        return torch.empty(shape, device=xs.device, dtype=xs.dtype)
 
     # ---- prefill / training ----------------------------------------------
     def forward(self, hidden_states: torch.Tensor, ssm_hiddens: Optional[torch.Tensor] = None,
@@ -218,19 +236,24 @@ class Mamba(nn.Module):
         w_in, b_in = self.input_proj.weight, self.input_proj.bias
         xs = _proj_cm(w_in[:inner], x, None if b_in is None else b_in[:inner])
         z = _proj_cm(w_in[inner:], x, None if b_in is None else b_in[inner:])
+        # with use_cache the conv kernel also leaves the k-1 pre-conv inputs
+        # ending at position lengths-1 (zero before the row start), the
+        # reference's conv cache (modules/mamba.py:113-135)
+        window = self._conv_window(xs) if use_cache else None
+        xc = causal_conv_silu(xs, self.conv.weight, self.conv.bias, window=window,
+                              lengths=lengths if use_cache else None)
         if use_cache:
-            self._store_conv_context(xs, lengths)
-        xc = causal_conv_silu(xs, self.conv.weight, self.conv.bias)
+            self._conv_context = window
         params = _proj_cm(self.ssm_param_proj.weight, xc)           # (batch, R + 2N, L)
         delta = _proj_cm(self.delta_proj.weight, params[:, :rank])
         Bm = params[:, rank:rank + nstate].contiguous()
         Cm = params[:, rank + nstate:].contiguous()
-        A = -torch.exp(self.log_A.float())
+        A, D, dt_bias = self._scan_params()
         # padding_side "left" is the reference's default at this call
         # (modules/mamba.py:170-175 passes no padding argument)
-        y, last = selective_scan_fn(xc, delta, A, Bm, Cm, self.D, z=z,
-                                    delta_bias=self.delta_proj.bias, return_last_state=True,
-                                    h_init=ssm_hiddens, length=lengths, padding_side="left")
+        y, last = selective_scan_fn(xc, delta, A, Bm, Cm, D, z=z, delta_bias=dt_bias,
+                                    return_last_state=True, h_init=ssm_hiddens, length=lengths,
+                                    padding_side="left")
         if use_cache:
             self._ssm_hiddens = self._keep(self._ssm_hiddens, last.detach())
         if residual is not None and self.out_proj.bias is None:

@@ -21,6 +21,7 @@ size_t bc_prep_floats(int batch, int nstate, int seqlen);
 size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen);
 void fwd_segments(int batch, int nblk, int seqlen, int& nseg, int& seg_len);
 size_t fwd_seg_floats(int batch, int dim, int nstate, int seqlen);
+int fwd_summary_split(int batch, int nblk, int nseg);
 int conv1d_max_width();
 int decode_max_batch();
 hipError_t launch_decode_gemv(int bf16, const void* W, const void* x, const void* nw, float eps,
@@ -38,7 +39,8 @@ hipError_t launch_rms_norm_cm(int bf16, const void* x, const void* w, float eps,
                               int C, int L, bool pair, hipStream_t st);
 hipError_t launch_causal_conv1d_fwd(int batch, int dim, int L, int K, int dtype_bf16,
                                     const void* x, const void* w, const void* bias, int silu,
-                                    void* out, bool vec, hipStream_t st);
+                                    void* out, const int64_t* lengths, void* window, bool vec,
+                                    hipStream_t st);
 hipError_t launch_causal_conv1d_bwd(int batch, int dim, int L, int K, int dtype_bf16,
                                     const void* x, const void* w, const void* bias,
                                     const void* dout, int silu, void* dx, void* dw, void* dbias,
@@ -144,6 +146,7 @@ ssm::ScanParams make_scan_params(int64_t batch, int64_t dim, int64_t seqlen, int
   p.z = z;
   p.seg_len = (int)seqlen;
   p.nseg = 1;
+  p.sub_k = 1;
   return p;
 }
 
@@ -287,8 +290,9 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   char* ws = static_cast<char*>(workspace) +
              round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
   ssm::fwd_segments((int)batch, p.nblk, (int)seqlen, p.nseg, p.seg_len);
+  p.sub_k = ssm::fwd_summary_split((int)batch, p.nblk, p.nseg);
   p.seg_h = reinterpret_cast<float*>(ws);
-  p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * batch * nstate * dim;
+  p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * p.sub_k * batch * nstate * dim;
   ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));
   p.dummy = ws;
   const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out, out_ungated});
@@ -489,14 +493,16 @@ size_t ssm_causal_conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t
 
 int ssm_causal_conv1d_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t width, int dtype,
                           const void* x, const void* weight, const void* bias, int silu, void* out,
-                          void* stream) {
+                          const int64_t* lengths, void* window, void* stream) {
   int rc = check_conv(batch, dim, seqlen, width, dtype);
   if (rc != SSM_OK) return rc;
   if (!x || !weight || !out) return fail(SSM_ERR_INVALID, "x, weight and out must be non-NULL");
+  if (lengths && !window) return fail(SSM_ERR_INVALID, "lengths requires window");
   const bool vec = seqlen % 8 == 0 && aligned16(x) && aligned16(out);
   return hip_status(ssm::launch_causal_conv1d_fwd((int)batch, (int)dim, (int)seqlen, (int)width,
                                                   dtype == SSM_BF16, x, weight, bias, silu ? 1 : 0,
-                                                  out, vec, static_cast<hipStream_t>(stream)),
+                                                  out, lengths, window, vec,
+                                                  static_cast<hipStream_t>(stream)),
                     "causal_conv1d_fwd launch");
 }
 

@@ -95,14 +95,25 @@ __device__ __forceinline__ void block_sum(float (&v)[K + 1], float* red) {
   }
 }
 
+// window (nullable): the decode cache of the row, the K-1 inputs ending at
+// position len-1 (len = lengths[b] clamped to [0, L], or L), zero where the
+// window starts before the row (the conv context the reference keeps after a
+// prefill, modules/mamba.py:113-135).
 template <typename T, int K, bool kVec>
 __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
-    T* __restrict__ out, int dim, int L, int silu) {
+    T* __restrict__ out, int dim, int L, int silu, const int64_t* __restrict__ lengths,
+    T* __restrict__ window) {
   const size_t row = blockIdx.x;
   const int c = (int)(row % (size_t)dim);
   const T* __restrict__ xr = x + row * (size_t)L;
   T* __restrict__ orow = out + row * (size_t)L;
+  if (K > 1 && window && threadIdx.x < K - 1) {
+    const int b = (int)(row / (size_t)dim);
+    const int len = lengths ? (int)min<int64_t>(max<int64_t>(lengths[b], 0), L) : L;
+    const int idx = len - (K - 1) + (int)threadIdx.x;
+    Elem<T>::store1(window + row * (K - 1) + threadIdx.x, idx >= 0 ? Elem<T>::load1(xr + idx) : 0.0f);
+  }
   float wk[K], bs;
   load_taps<K>(w, bias, c, wk, bs);
   if constexpr (kVec) {
@@ -259,19 +270,21 @@ __global__ __launch_bounds__(256) void causal_conv1d_wgrad_kernel(const float* _
 
 template <typename T, int K>
 hipError_t launch_fwd_k(int batch, int dim, int L, const void* x, const void* w, const void* bias,
-                        int silu, void* out, bool vec, hipStream_t st) {
+                        int silu, void* out, const int64_t* lengths, void* window, bool vec,
+                        hipStream_t st) {
   ProfScope prof("causal_conv1d_fwd", st);
   const dim3 grid((unsigned)((size_t)batch * dim));
   auto* xp = static_cast<const T*>(x);
   auto* wp = static_cast<const T*>(w);
   auto* bp = static_cast<const T*>(bias);
   auto* op = static_cast<T*>(out);
+  auto* wo = static_cast<T*>(window);
   if (vec)
     hipLaunchKernelGGL((causal_conv1d_fwd_kernel<T, K, true>), grid, dim3(kConvThreads), 0, st, xp,
-                       wp, bp, op, dim, L, silu);
+                       wp, bp, op, dim, L, silu, lengths, wo);
   else
     hipLaunchKernelGGL((causal_conv1d_fwd_kernel<T, K, false>), grid, dim3(kConvThreads), 0, st, xp,
-                       wp, bp, op, dim, L, silu);
+                       wp, bp, op, dim, L, silu, lengths, wo);
   return hipGetLastError();
 }
 
@@ -305,16 +318,17 @@ hipError_t launch_bwd_k(int batch, int dim, int L, const void* x, const void* w,
 
 template <typename T>
 hipError_t dispatch_fwd(int batch, int dim, int L, int K, const void* x, const void* w,
-                        const void* bias, int silu, void* out, bool vec, hipStream_t st) {
+                        const void* bias, int silu, void* out, const int64_t* lengths,
+                        void* window, bool vec, hipStream_t st) {
   switch (K) {
-    case 1: return launch_fwd_k<T, 1>(batch, dim, L, x, w, bias, silu, out, vec, st);
-    case 2: return launch_fwd_k<T, 2>(batch, dim, L, x, w, bias, silu, out, vec, st);
-    case 3: return launch_fwd_k<T, 3>(batch, dim, L, x, w, bias, silu, out, vec, st);
-    case 4: return launch_fwd_k<T, 4>(batch, dim, L, x, w, bias, silu, out, vec, st);
-    case 5: return launch_fwd_k<T, 5>(batch, dim, L, x, w, bias, silu, out, vec, st);
-    case 6: return launch_fwd_k<T, 6>(batch, dim, L, x, w, bias, silu, out, vec, st);
-    case 7: return launch_fwd_k<T, 7>(batch, dim, L, x, w, bias, silu, out, vec, st);
-    case 8: return launch_fwd_k<T, 8>(batch, dim, L, x, w, bias, silu, out, vec, st);
+    case 1: return launch_fwd_k<T, 1>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
+    case 2: return launch_fwd_k<T, 2>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
+    case 3: return launch_fwd_k<T, 3>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
+    case 4: return launch_fwd_k<T, 4>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
+    case 5: return launch_fwd_k<T, 5>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
+    case 6: return launch_fwd_k<T, 6>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
+    case 7: return launch_fwd_k<T, 7>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
+    case 8: return launch_fwd_k<T, 8>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -347,9 +361,12 @@ int conv1d_max_width() { return kMaxWidth; }
 
 hipError_t launch_causal_conv1d_fwd(int batch, int dim, int L, int K, int dtype_bf16,
                                     const void* x, const void* w, const void* bias, int silu,
-                                    void* out, bool vec, hipStream_t st) {
-  return dtype_bf16 ? dispatch_fwd<__hip_bfloat16>(batch, dim, L, K, x, w, bias, silu, out, vec, st)
-                    : dispatch_fwd<float>(batch, dim, L, K, x, w, bias, silu, out, vec, st);
+                                    void* out, const int64_t* lengths, void* window, bool vec,
+                                    hipStream_t st) {
+  return dtype_bf16 ? dispatch_fwd<__hip_bfloat16>(batch, dim, L, K, x, w, bias, silu, out, lengths,
+                                                   window, vec, st)
+                    : dispatch_fwd<float>(batch, dim, L, K, x, w, bias, silu, out, lengths, window,
+                                          vec, st);
 }
 
 hipError_t launch_causal_conv1d_bwd(int batch, int dim, int L, int K, int dtype_bf16,

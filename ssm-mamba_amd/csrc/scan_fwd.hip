@@ -159,8 +159,8 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       const bool ok = ch_ok && n < N;
       A2[g][s] = ok ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
       float hv = (ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
-      // carry in through the earlier segments' affine maps, in order
-      for (int sp = 0; ok && sp < seg; ++sp) {
+      // carry in through the earlier sub-segments' affine maps, in order
+      for (int sp = 0; ok && sp < seg * p.sub_k; ++sp) {
         const size_t sb = (size_t)sp * p.batch + b;
         const float decay = fast_exp2(A2[g][s] * seg_dt[sb * Dm + ch]);
         hv = fmaf(decay, hv, seg_h[(sb * N + n) * Dm + ch]);
@@ -495,11 +495,13 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
 
 // ---------------------------------------------------------------- segment summaries
 
-// For segment s = blockIdx.z (< nseg - 1) of batch row b and 64 channels: the
-// state the segment's steps produce from zero, h_seg = sum_t (prod_{t' > t}
-// a_t') delta_t u_t B_t, and the segment's summed step size sum_t delta_t
-// (padded steps count zero), the two numbers that let a later segment start
-// from the right state.  The same tiling as the forward (64 channels x 32
+// For sub-segment j = blockIdx.z (seg_len / sub_k steps; the sub-segments
+// cover segments 0 .. nseg - 2) of batch row b and 64 channels: the state the
+// sub-segment's steps produce from zero, h_seg = sum_t (prod_{t' > t} a_t')
+// delta_t u_t B_t, and its summed step size sum_t delta_t (padded steps count
+// zero), the two numbers that let a later segment start from the right state.
+// Finer sub-segments than segments keep the device full when the segments
+// alone would leave CUs idle (few batch rows x channel blocks).  The same tiling as the forward (64 channels x 32
 // steps per tile, lane = channel, wave = state pair) without outputs: phase A
 // stages delta and delta*u in LDS (double-buffered by tile parity, so one
 // barrier per tile suffices), phase B runs the recurrence with B read as
@@ -521,10 +523,11 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_segsum_kernel(
   const int w = wave_id_uniform();
   const int b = blockIdx.y;
   const int d0 = blockIdx.x * kBlockCh;
-  const int seg = blockIdx.z;
+  const int seg = blockIdx.z;  // sub-segment index
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
-  const int Tbeg = seg * p.seg_len;
-  const int Lend = min(L, Tbeg + p.seg_len);
+  const int sub_len = p.seg_len / p.sub_k;
+  const int Tbeg = seg * sub_len;
+  const int Lend = min(L, Tbeg + sub_len);
   const int npair = bc_pairs(N);
   const int Lp = bc_row_len(L);
   const size_t rb = (size_t)b * Dm;
@@ -689,10 +692,25 @@ void fwd_segments(int batch, int nblk, int seqlen, int& nseg, int& seg_len) {
   nseg = (seqlen + seg_len - 1) / seg_len;
 }
 
+// Forward summaries per segment: the summary kernel covers segments
+// 0 .. nseg - 2 only, so with few segments it may leave CUs idle; splitting
+// each segment's summary into 2 or 4 sub-segments (of a whole number of
+// 32-step tiles) restores about one workgroup per CU.
+int fwd_summary_split(int batch, int nblk, int nseg) {
+  constexpr int kTargetWG = 256;
+  if (nseg <= 1) return 1;
+  const long wg = (long)(nseg - 1) * batch * nblk;
+  int k = 1;
+  while (k < 4 && wg * 2 * k <= kTargetWG) k *= 2;
+  return k;
+}
+
 size_t fwd_seg_floats(int batch, int dim, int nstate, int seqlen) {
   int nseg, seg_len;
-  fwd_segments(batch, (dim + kBlockCh - 1) / kBlockCh, seqlen, nseg, seg_len);
-  return (size_t)(nseg - 1) * batch * dim * (nstate + 1);
+  const int nblk = (dim + kBlockCh - 1) / kBlockCh;
+  fwd_segments(batch, nblk, seqlen, nseg, seg_len);
+  const int k = fwd_summary_split(batch, nblk, nseg);
+  return (size_t)(nseg - 1) * k * batch * dim * (nstate + 1);
 }
 
 hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t st) {
@@ -716,7 +734,8 @@ static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t 
   if (p.nseg > 1) {
     ProfScope prof("scan_fwd_segsum", st);
     hipLaunchKernelGGL((scan_fwd_segsum_kernel<T, kSG, kAligned>),
-                       dim3(p.nblk, p.batch, p.nseg - 1), dim3(kThreads), 0, st, dims_of(p),
+                       dim3(p.nblk, p.batch, (p.nseg - 1) * p.sub_k), dim3(kThreads), 0, st,
+                       dims_of(p),
                        (const T*)p.u, (const T*)p.delta, p.A, bc, p.bias, p.length, p.seg_h,
                        p.seg_dt);
     hipError_t e = hipGetLastError();

@@ -30,6 +30,7 @@ struct ScanDims {
   int softplus;
   int seg_len;  // steps per sequence segment (a multiple of the forward super-tile)
   int nseg;     // segments (1: the whole row in one workgroup)
+  int sub_k;    // forward summaries per segment (sub-segments of seg_len / sub_k steps)
 };
 
 struct ScanParams {
@@ -78,10 +79,12 @@ struct ScanParams {
   // the kernels' steady-state stores need no branches
   void* dummy;
 
-  // sequence split of the forward (nseg > 1): per segment s < nseg - 1 the
-  // state its steps produce from zero, (nseg - 1, batch, nstate, dim), and the
-  // sum of its step sizes, (nseg - 1, batch, dim)
-  int seg_len, nseg;
+  // sequence split (nseg > 1).  Forward: per sub-segment j (seg_len / sub_k
+  // steps) of segments 0 .. nseg - 2, the state its steps produce from zero,
+  // ((nseg - 1) * sub_k, batch, nstate, dim), and the sum of its step sizes,
+  // ((nseg - 1) * sub_k, batch, dim).  Backward (sub_k = 1): the per-segment
+  // adjoint carries and step sums of segments 1 .. nseg - 1.
+  int seg_len, nseg, sub_k;
   float* seg_h;
   float* seg_dt;
 };
@@ -100,15 +103,12 @@ struct UpdateParams {
   const float* D;      // nullable
   const float* bias;   // nullable
   const void* z;       // nullable
-  // ungated output D*u + sum_n C*h (with z): written by the forward when
-  // non-null, read by the backward for dz
-  void* out_ungated;
   void* out;
 };
 
 inline ScanDims dims_of(const ScanParams& p) {
-  return ScanDims{p.batch, p.dim,       p.seqlen,  p.nstate, p.nchunks,
-                  p.nblk,  p.pad_right, p.softplus, p.seg_len, p.nseg};
+  return ScanDims{p.batch,    p.dim,     p.seqlen,  p.nstate, p.nchunks, p.nblk,
+                  p.pad_right, p.softplus, p.seg_len, p.nseg,   p.sub_k};
 }
 
 }  // namespace ssm

@@ -40,6 +40,33 @@ def test_forward(cuda, dtype, seqlen, width):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("width", [2, 4, 8])
+@pytest.mark.parametrize("seqlen", [3, 64, 2051])
+def test_forward_window(cuda, dtype, width, seqlen):
+    """The decode conv cache written by the forward: the width-1 inputs ending
+    at position lengths[b]-1, zero before the row start, lengths clamped to
+    [0, seqlen]; without lengths the row's last width-1 inputs.  The output
+    is unchanged by the extra write."""
+    from ssm_mamba_amd.causal_conv1d import causal_conv1d_fn
+    x, w, b = _case(4, 6, seqlen, width, seed=seqlen + width)
+    x, w, b = x.to(dtype), w.to(dtype), b.to(dtype)
+    lens = torch.tensor([seqlen, 0, 1, seqlen + 5], dtype=torch.long)
+    for lengths in (lens, None):
+        win = torch.full((4, 6, width - 1), 7.0, dtype=dtype, device=cuda)
+        got = causal_conv1d_fn(x.to(cuda), w.to(cuda), b.to(cuda), window=win,
+                               lengths=None if lengths is None else lengths.to(cuda))
+        assert_close(got, _ref(x.double(), w.double(), b.double(), True), dtype, "out")
+        ref = torch.zeros(4, 6, width - 1, dtype=dtype)
+        for bb in range(4):
+            n = seqlen if lengths is None else min(max(int(lengths[bb]), 0), seqlen)
+            for j in range(width - 1):
+                t = n - (width - 1) + j
+                if t >= 0:
+                    ref[bb, :, j] = x[bb, :, t]
+        assert torch.equal(win.cpu(), ref), f"window lengths={lengths}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("seqlen", [5, 40, 2048, 4099])
 @pytest.mark.parametrize("width", [1, 3, 4, 8])
 def test_backward(cuda, dtype, seqlen, width):
