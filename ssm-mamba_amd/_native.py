@@ -88,7 +88,7 @@ SIGNATURES = {
     ]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def lib() -> ctypes.CDLL:

@@ -190,7 +190,7 @@ extern "C" {
 
 const char* ssm_last_error(void) { return g_err.c_str(); }
 
-int ssm_abi_version(void) { return 2; }
+int ssm_abi_version(void) { return 3; }
 
 int ssm_profile_begin(void) {
   g_err.clear();
