@@ -19,9 +19,10 @@
 // of 16 steps (one saved-state chunk) are walked from the end.  For each tile
 // a wave reloads the state the forward saved at the tile start, recomputes the
 // 16 states and decay factors of its two states into registers, then runs the
-// reverse recurrence.  The tile's B/C block (prepped fp32 layout) is staged in
-// LDS together with the per-step values and read with broadcast LDS loads, so
-// the loop has no scalar-memory traffic and no scalar-register pressure.  Per-position
+// reverse recurrence.  The tile's B and C are read straight from B and C (one
+// element per thread, coalesced along the steps, a tile ahead), parked in LDS
+// in block-register order, and each wave takes its 4-step blocks from there
+// as block registers read through DPP row broadcasts.  Per-position
 // sums over states (sum G B, sum A G a h) leave each wave in its own
 // LDS slice and are added in a fixed order; the per-position sums over
 // channels (dB, dC) are reduced across the 64 lanes with a permlane/DPP
@@ -124,7 +125,7 @@ __device__ __forceinline__ constexpr int bcol_swz(int q) { return 4 * q + 2 * (q
 template <typename T, int kSG, bool kHasZ, bool kAligned>
 __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
-    const float* __restrict__ Ap, const float* __restrict__ bc,
+    const float* __restrict__ Ap, const T* __restrict__ Bp, const T* __restrict__ Cp,
     const float* __restrict__ Dp, const float* __restrict__ biasp,
     const float* __restrict__ h_init, const int64_t* __restrict__ length,
     const T* __restrict__ zp, const T* __restrict__ yup, const float* __restrict__ h_chunks,
@@ -168,10 +169,10 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   const int tile_end = min(ntiles, tile_beg + p.seg_len / kTileB);
   const size_t srow = (size_t)seg * p.batch + b;  // (segment, batch row) of the partials
   const int ngroups = (N + 1) / 2;
-  const int npair = bc_pairs(N);
-  const int Lp = bc_row_len(L);
   const size_t rb = (size_t)b * Dm;
   const size_t nBC = (size_t)p.batch * N * L;
+  const T* __restrict__ Braw = Bp + (size_t)b * N * L;
+  const T* __restrict__ Craw = Cp + (size_t)b * N * L;
   float* const dummyf = static_cast<float*>(dummy);
 
   int vlo, vhi;
@@ -231,7 +232,14 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   // compiler wait for outstanding memory operations there.
   R4 n1, n2, n3;        // raw row pieces (group 0: u, delta; group 1: dout, z, y)
   float hcn[kSG][2];    // states saved by the forward before the tile
-  float bcn[kSG][kT4];  // the tile's B/C blocks of the wave's pairs (block registers)
+  // B and C of the next tile: thread i reads element i (and i + 512, ...)
+  // of the tile's (B|C, state, step) set, coalesced along the steps;
+  // phase A parks it in LDS in block-register order and phase B takes the
+  // wave's 4-step blocks from there
+  constexpr int kBCStates = 2 * kWaves * kSG;  // states covered by the dispatch bucket
+  static_assert(2 * kBCStates * kTileB == kSG * kThreads, "kSG B/C elements per thread");
+  __shared__ float sBlk[kWaves * kSG][kT4][16];  // [pair][block][(step, state, B|C)]
+  float bcn[kSG];
   const int chc = min(ch, Dm - 1);
   auto issue = [&](int tile) {
     const int t = tile * kTileB + a_col;
@@ -240,10 +248,12 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     if constexpr (kHasZ) n3 = load_raw4_nb<T, kAligned>(row3, t, L, a_ok);
 #pragma unroll
     for (int g = 0; g < kSG; ++g) {
-      const int Gc = min(g * kWaves + w, npair - 1);
-#pragma unroll
-      for (int jq = 0; jq < kT4; ++jq)
-        bcn[g][jq] = bc[bc_offset(b, Gc, npair, Lp, tile * kTileB + 4 * jq) + (lane & 15)];
+      // element e = (B|C, state, step) of the tile, clamped into the rows
+      // (states past N are zeroed in phase A, steps past L meet delta = 0)
+      const int e = g * kThreads + tid;
+      const int n = min((e / kTileB) % kBCStates, N - 1);
+      const int t = min(tile * kTileB + e % kTileB, L - 1);
+      bcn[g] = Elem<T>::load1((e / (kTileB * kBCStates) ? Craw : Braw) + (size_t)n * L + t);
     }
 #pragma unroll
     for (int g = 0; g < kSG; ++g)
@@ -258,7 +268,6 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   };
 
   float hc[kSG][2];
-  float bcc[kSG][kT4];
   float dzo[4];  // group 1: dz of the tile, stored in phase C
   // ---- phase A: stage a tile's per-position quantities in LDS and take its
   // saved states and B/C blocks
@@ -305,9 +314,11 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       sDout[par][a_q][a_sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
     }
 #pragma unroll
-    for (int g = 0; g < kSG; ++g)
-#pragma unroll
-      for (int jq = 0; jq < kT4; ++jq) bcc[g][jq] = bcn[g][jq];
+    for (int g = 0; g < kSG; ++g) {
+      const int e = g * kThreads + tid;
+      const int j = e % kTileB, n = (e / kTileB) % kBCStates, kind = e / (kTileB * kBCStates);
+      sBlk[n >> 1][j >> 2][(j & 3) * 4 + (n & 1) * 2 + kind] = n < N ? bcn[g] : 0.0f;
+    }
 #pragma unroll
     for (int g = 0; g < kSG; ++g)
 #pragma unroll
@@ -329,6 +340,9 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       }
       float a[2][kChunk], H[2][kChunk];
       StepVals X, Y;
+      float bcg[kT4];  // block registers of the wave's pair G: lane l holds value l & 15
+#pragma unroll
+      for (int jq = 0; jq < kT4; ++jq) bcg[jq] = sBlk[G][jq][lane & 15];
       // slice update: the first group writes, later groups add
       auto put4 = [&](float4 (&slice)[kT4][kBlockCh], int q, const float (&v)[4]) {
         float4& dst = slice[q][lane ^ bcol_swz(q)];
@@ -341,7 +355,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       };
       auto fwd = [&](int jq, const StepVals& sv) {
         float y[4];  // unused here (the forward saved the output)
-        bwd_recompute_block(jq, sv, bcc[g][jq], A2[g], hc[g], a, H, y);
+        bwd_recompute_block(jq, sv, bcg[jq], A2[g], hc[g], a, H, y);
       };
       // the value of lane l after the reduction: index l >> 2 of the block's
       // 16 (kind = dB/dC, state, step); quads hold the same value
@@ -351,7 +365,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       float* const wsb = ws_bc + ((size_t)rkind * p.nblk + blk) * nBC + ((size_t)b * N + rn) * L;
       auto rev = [&](int jq, const StepVals& sv) {
         float gB[4], gD[4], vals[16];
-        bwd_reverse_block(jq, sv, bcc[g][jq], Av[g], A2[g], hc[g], a, H, gam[g], dA[g], vals, gB,
+        bwd_reverse_block(jq, sv, bcg[jq], Av[g], A2[g], hc[g], a, H, gam[g], dA[g], vals, gB,
                           gD);
         put4(sGB[w], jq, gB);
         put4(sDD[w], jq, gD);
@@ -710,7 +724,8 @@ static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t 
   dim3 grid(p.nblk, p.batch, p.nseg);
   ProfScope prof("scan_bwd", st);
   hipLaunchKernelGGL((scan_bwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(kThreads), 0, st,
-                     dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias,
+                     dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, (const T*)p.B,
+                     (const T*)p.C, p.D, p.bias,
                      p.h_init, p.length, (const T*)p.z, (const T*)p.out_ungated, p.h_chunks_in,
                      (const T*)p.dout,
                      p.dh_last, (T*)p.du, (T*)p.ddelta, (T*)p.dz, p.dh_init, p.ws_bc, p.ws_A,
@@ -756,8 +771,10 @@ static hipError_t launch_bwd2(const ScanParams& p, const float* bc, bool aligned
 // nstate <= 64.
 hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* bc,
                            hipStream_t st) {
-  hipError_t e = launch_bc_prep(p, dtype, bc, st);
-  if (e != hipSuccess) return e;
+  if (p.nseg > 1) {  // only the segment summaries read the prepped layout
+    hipError_t e = launch_bc_prep(p, dtype, bc, st);
+    if (e != hipSuccess) return e;
+  }
   if (dtype == 1) return launch_bwd2<__hip_bfloat16>(p, bc, aligned, st);
   return launch_bwd2<float>(p, bc, aligned, st);
 }

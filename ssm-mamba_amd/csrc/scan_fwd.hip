@@ -15,11 +15,13 @@
 //            are loaded during the previous tile's phase B;
 //   phase B  lane = channel, wave w = state pairs G = g*8 + w: a sequential
 //            recurrence over the tile held in registers.  B and C are
-//            wave-uniform (same b, n, t across the wave) and come from the
-//            prepped fp32 block layout through scalar loads, double-buffered so
-//            each 4-step block's scalar and LDS loads are issued one block
-//            ahead.  Each wave leaves its partial sum over its states of C*h in
-//            its own LDS slice;
+//            wave-uniform (same b, n, t across the wave).  With N <= 16 phase A
+//            reads them straight from B and C (coalesced along the steps) and
+//            stages the super-tile's (B0, C0, B1, C1) per pair and step in LDS,
+//            read back with broadcast loads; larger N read the prepped fp32
+//            block layout through scalar loads.  Each 4-step block's loads are
+//            issued one block ahead.  Each wave leaves its partial sum over its
+//            states of C*h in its own LDS slice;
 //   phase C  the phase-A threads add the eight slices in a fixed order, D*u
 //            and the z gate, and store the tile.
 // The state after every kChunk steps is saved for the backward (h_chunks,
@@ -110,8 +112,8 @@ __device__ __forceinline__ void fwd_block(const float4 dl4, const float4 du4, co
 template <typename T, int kSG, int kZ, bool kAligned>
 __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
-    const float* __restrict__ Ap, const float* __restrict__ bc,
-    const float* __restrict__ Dp, const float* __restrict__ biasp,
+    const float* __restrict__ Ap, const float* __restrict__ bc, const T* __restrict__ Bp,
+    const T* __restrict__ Cp, const float* __restrict__ Dp, const float* __restrict__ biasp,
     const float* __restrict__ h_init, const int64_t* __restrict__ length,
     const T* __restrict__ zp, T* __restrict__ out, T* __restrict__ yu,
     float* __restrict__ h_chunks, float* __restrict__ h_last, void* __restrict__ dummy,
@@ -195,12 +197,16 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   // registers free of merges).
   const int last_t0 = (Lend - 1) / kTileF * kTileF;
   R4 qu[kSubF], qd[kSubF], qz[kSubF];
-  // B/C staging: thread -> (pair, step) of the super-tile, kBCPer float4 each
+  // B/C staging (kSG == 1): thread -> (pair, step) of the super-tile,
+  // kBCPer items of (B0, C0, B1, C1) read straight from B and C (the states
+  // 2G, 2G+1 of the pair; masked to zero at staging for states past N, so
+  // those waves run the common path and add nothing)
   constexpr int kBCItems = kSubF * kWaves * kTileF;
   constexpr int kBCPer = kBCItems / kThreads;
   static_assert(kBCItems % kThreads == 0, "whole B/C items per thread");
-  const float4* __restrict__ bc4 = reinterpret_cast<const float4*>(bc);
-  float4 qbc[kBCPer];
+  const T* __restrict__ Braw = static_cast<const T*>(Bp) + (size_t)b * N * L;
+  const T* __restrict__ Craw = static_cast<const T*>(Cp) + (size_t)b * N * L;
+  float qbc[kBCPer][4];
   auto issue = [&](int T0) {
 #pragma unroll
     for (int i = 0; i < kSubF; ++i) {
@@ -217,10 +223,15 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
         const int step = item % kTileF;
         const int G = (item / kTileF) % kWaves;
         const int sub = item / (kTileF * kWaves);
-        // clamped into the pair's prepped row (rows are padded to 16 steps;
-        // steps past it are never read by phase B)
-        const int t = min(min(T0, last_t0) + sub * kTileF + step, Lp - 1);
-        qbc[r] = bc4[((size_t)b * npair + G) * Lp + t];
+        // clamped into the rows (steps past L only meet delta = 0 and are
+        // never stored; states past N are zeroed at staging)
+        const int t = min(min(T0, last_t0) + sub * kTileF + step, L - 1);
+        const size_t o0 = (size_t)min(2 * G, N - 1) * L + t;
+        const size_t o1 = (size_t)min(2 * G + 1, N - 1) * L + t;
+        qbc[r][0] = Elem<T>::load1(Braw + o0);
+        qbc[r][1] = Elem<T>::load1(Craw + o0);
+        qbc[r][2] = Elem<T>::load1(Braw + o1);
+        qbc[r][3] = Elem<T>::load1(Craw + o1);
       }
     }
   };
@@ -267,12 +278,14 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       }
     }
     if constexpr (kSG == 1) {
-      // pairs past the last one have zero B and C (prepped layout), so their
-      // waves run the common path and contribute nothing
 #pragma unroll
       for (int r = 0; r < kBCPer; ++r) {
         const int item = r * kThreads + tid;
-        sBC[item / (kTileF * kWaves)][(item / kTileF) % kWaves][item % kTileF] = qbc[r];
+        const int G = (item / kTileF) % kWaves;
+        const bool ok0 = 2 * G < N, ok1 = 2 * G + 1 < N;
+        sBC[item / (kTileF * kWaves)][G][item % kTileF] =
+            make_float4(ok0 ? qbc[r][0] : 0.0f, ok0 ? qbc[r][1] : 0.0f, ok1 ? qbc[r][2] : 0.0f,
+                        ok1 ? qbc[r][3] : 0.0f);
       }
     }
   };
@@ -744,9 +757,9 @@ static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t 
   ProfScope prof("scan_fwd", st);
   hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kZ, kAligned>),
                      dim3(p.nblk, p.batch, p.nseg), dim3(kThreads), 0, st, dims_of(p),
-                     (const T*)p.u, (const T*)p.delta, p.A, bc, p.D, p.bias, p.h_init, p.length,
-                     (const T*)p.z, (T*)p.out, (T*)p.out_ungated, p.h_chunks, p.h_last, p.dummy,
-                     p.seg_h, p.seg_dt);
+                     (const T*)p.u, (const T*)p.delta, p.A, bc, (const T*)p.B, (const T*)p.C, p.D,
+                     p.bias, p.h_init, p.length, (const T*)p.z, (T*)p.out, (T*)p.out_ungated,
+                     p.h_chunks, p.h_last, p.dummy, p.seg_h, p.seg_dt);
   return hipGetLastError();
 }
 
@@ -770,11 +783,18 @@ static hipError_t launch_fwd2(const ScanParams& p, const float* bc, bool aligned
   return launch_fwd3<T, 16>(p, bc, aligned, st);
 }
 
-// bc must hold bc_prep_floats() floats; it is filled here before the scan.
+// The prepped B/C layout serves the segment summaries and state counts past
+// 16; the main kernel reads B and C directly otherwise.
+bool fwd_needs_bc_prep(const ScanParams& p) { return p.nseg > 1 || p.nstate > 16; }
+
+// bc must hold bc_prep_floats() floats; it is filled here before the scan
+// when a kernel reads the prepped layout.
 hipError_t launch_scan_fwd(const ScanParams& p, int dtype, bool aligned, float* bc,
                            hipStream_t st) {
-  hipError_t e = launch_bc_prep(p, dtype, bc, st);
-  if (e != hipSuccess) return e;
+  if (fwd_needs_bc_prep(p)) {
+    hipError_t e = launch_bc_prep(p, dtype, bc, st);
+    if (e != hipSuccess) return e;
+  }
   if (dtype == 1) return launch_fwd2<__hip_bfloat16>(p, bc, aligned, st);
   return launch_fwd2<float>(p, bc, aligned, st);
 }
