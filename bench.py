@@ -232,6 +232,10 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
         layers = [l.ssm for l in model.layers]
         rank = layers[0].delta_rank
         params = torch.randn(batch, rank + 2 * nstate, device=dev).bfloat16()
+        nparts = DEC.xproj_blocks(inner, rank + 2 * nstate) if DEC.FOLD_XPROJ else 0
+        # with the x-projection folded, the kernel also adds its partials
+        parts = (torch.randn(nparts, batch, (rank + 2 * nstate + 3) // 4 * 4, device=dev) / nparts
+                 if nparts else None)
         xc = torch.randn(batch, inner, device=dev).bfloat16()
         xz = torch.randn(batch, 2 * inner, device=dev).bfloat16()
         fused = DEC.block_step_supported(layers[0], torch.zeros(batch, cfg.model_dim, device=dev,
@@ -241,8 +245,8 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
         def updates():
             for m in layers:
                 if fused:
-                    DEC.ssm_step(params, rank, m.delta_proj.weight, m.delta_proj.bias, m.log_A, m.D,
-                                 xc, xz, m._ssm_hiddens)
+                    DEC.ssm_step(params if parts is None else parts, rank, m.delta_proj.weight,
+                                 m.delta_proj.bias, m.log_A, m.D, xc, xz, m._ssm_hiddens)
                 else:
                     su.apply_ext(xc, -torch.exp(m.log_A.float()), params[:, :nstate].contiguous(),
                                  params[:, :nstate].contiguous(), m.D.float(), xc,

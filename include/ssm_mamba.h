@@ -187,6 +187,10 @@ int ssm_causal_conv1d_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t wi
  *   ssm_decode_ssm_step      state update, y = (C.h + D xc) * silu(z)
  *   ssm_decode_gemv          x' = x + W_out @ y [+ b_out]      (residual set)
  *
+ * or three, when ssm_decode_xproj_blocks(dim, rank + 2*nstate) = P > 0: the
+ * in-projection call then also takes W_x and writes P fp32 partials of
+ * W_x @ xc, and the state-update call adds them in place of params.
+ *
  * Every tensor except state has element type `dtype` (weights and the norm,
  * conv, dt and A/D parameters included); state (batch, dim, nstate) is fp32.
  * Row-major throughout.
@@ -217,7 +221,24 @@ int ssm_decode_in_proj_conv(int64_t batch, int64_t dim, int64_t in_dim, int64_t 
                             const void* in_proj_weight, const void* x, const void* norm_weight,
                             float norm_eps, const void* in_proj_bias, const void* conv_weight,
                             const void* conv_bias, void* conv_window, void* xz, void* xc,
+                            const void* x_proj_weight, int64_t params_dim, float* xproj_partials,
                             void* stream);
+
+/*
+ * The x-projection folded into the two calls around it (no counterpart call
+ * in the reference; it is modules/mamba.py:216-221's x_proj).  Returns the
+ * number P of partial blocks, or 0 when the folded form does not apply
+ * (params_dim = rank + 2*nstate above 256, or dim not a multiple of 16).
+ * With x_proj_weight (params_dim, dim) non-NULL, ssm_decode_in_proj_conv
+ * also writes xproj_partials, fp32 (P, batch, params_dim rounded up to 4):
+ * block p holds sum over the 16 channels c of block p of
+ * x_proj_weight[j, c] * xc[b, c].  ssm_decode_ssm_step with params_blocks = P
+ * reads params = xproj_partials and adds the P blocks in a fixed order
+ * (the result is bit-reproducible), rounding the sums to dtype as the
+ * unfolded x-projection output is.  x_proj_weight and xproj_partials are
+ * 16-byte aligned.
+ */
+int64_t ssm_decode_xproj_blocks(int64_t dim, int64_t params_dim);
 
 /*
  * Step-size projection, state update and gate (modules/mamba.py:223-240 with
@@ -225,14 +246,16 @@ int ssm_decode_in_proj_conv(int64_t batch, int64_t dim, int64_t in_dim, int64_t 
  * params[:, :rank]; delta' = softplus(delta + dt_bias); A = -exp(log_A);
  * state = exp(delta' A) state + delta' xc B with B = params[:, rank:rank+nstate];
  * y = (sum_n C state + D xc) * silu(z), C = params[:, rank+nstate:],
- * z = xz[:, dim:2*dim] (row stride ld_xz).  params (batch, rank + 2*nstate);
- * state (batch, dim, nstate) fp32 updated in place; y (batch, dim).  dt_bias,
- * D nullable; nstate in {4, 8, 16, 32, 64}.
+ * z = xz[:, dim:2*dim] (row stride ld_xz).  params (batch, rank + 2*nstate)
+ * with params_blocks = 0, or the x-projection partials of
+ * ssm_decode_in_proj_conv with params_blocks = ssm_decode_xproj_blocks(dim,
+ * rank + 2*nstate); state (batch, dim, nstate) fp32 updated in place; y
+ * (batch, dim).  dt_bias, D nullable; nstate in {4, 8, 16, 32, 64}.
  */
 int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank, int dtype,
-                        const void* params, const void* dt_proj_weight, const void* dt_bias,
-                        const void* log_A, const void* D, const void* xc, const void* xz,
-                        int64_t ld_xz, float* state, void* y, void* stream);
+                        const void* params, int64_t params_blocks, const void* dt_proj_weight,
+                        const void* dt_bias, const void* log_A, const void* D, const void* xc,
+                        const void* xz, int64_t ld_xz, float* state, void* y, void* stream);
 
 #ifdef __cplusplus
 }

@@ -74,11 +74,15 @@ SIGNATURES = {
         _i64, _i64, _i64, _i64, _i32,          # batch, dim, in_dim, width, dtype
         _p, _p, _p, ctypes.c_float, _p,        # in_proj_weight, x, norm_weight, norm_eps, in_proj_bias
         _p, _p, _p,                            # conv_weight, conv_bias, window
-        _p, _p, _p,                            # xz, xc, stream
+        _p, _p,                                # xz, xc
+        _p, _i64, _p,                          # x_proj_weight, params_dim, xproj_partials
+        _p,                                    # stream
     ]),
+    "ssm_decode_xproj_blocks": (_i64, [_i64, _i64]),
     "ssm_decode_ssm_step": (_i32, [
         _i64, _i64, _i64, _i64, _i32,          # batch, dim, nstate, rank, dtype
-        _p, _p, _p, _p, _p,                    # params, dt_proj_weight, dt_bias, log_A, D
+        _p, _i64,                              # params, params_blocks
+        _p, _p, _p, _p,                        # dt_proj_weight, dt_bias, log_A, D
         _p, _p, _i64,                          # xc, xz, ld_xz
         _p, _p, _p,                            # state, y, stream
     ]),
@@ -88,7 +92,7 @@ SIGNATURES = {
     ]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 def lib() -> ctypes.CDLL:

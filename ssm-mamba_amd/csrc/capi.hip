@@ -24,17 +24,19 @@ size_t fwd_seg_floats(int batch, int dim, int nstate, int seqlen);
 int fwd_summary_split(int batch, int nblk, int nseg);
 int conv1d_max_width();
 int decode_max_batch();
+int decode_xproj_blocks(int64_t dim, int64_t nout);
 hipError_t launch_decode_gemv(int bf16, const void* W, const void* x, const void* nw, float eps,
                               const void* bias, const void* res, void* y, int B, int O, int K,
                               hipStream_t st);
 hipError_t launch_decode_in_proj_conv(int bf16, const void* W, const void* x, const void* nw,
                                       float eps, const void* bias, void* xz, int B, int dim, int K,
                                       int width, void* ctx, const void* cw, const void* cb,
-                                      void* xc, hipStream_t st);
-hipError_t launch_decode_ssm_step(int bf16, const void* p, int nout, int R, const void* Wdt,
-                                  const void* dtb, const void* logA, const void* D, const void* xc,
-                                  const void* xz, int ld, float* state, void* y, int B, int dim,
-                                  int nstate, bool vecR, hipStream_t st);
+                                      void* xc, const void* Wx, int nout, float* part,
+                                      hipStream_t st);
+hipError_t launch_decode_ssm_step(int bf16, const void* p, int nout, int nparts, int R,
+                                  const void* Wdt, const void* dtb, const void* logA, const void* D,
+                                  const void* xc, const void* xz, int ld, float* state, void* y,
+                                  int B, int dim, int nstate, bool vecR, hipStream_t st);
 hipError_t launch_rms_norm_cm(int bf16, const void* x, const void* w, float eps, void* out, int B,
                               int C, int L, bool pair, hipStream_t st);
 hipError_t launch_causal_conv1d_fwd(int batch, int dim, int L, int K, int dtype_bf16,
@@ -190,7 +192,7 @@ extern "C" {
 
 const char* ssm_last_error(void) { return g_err.c_str(); }
 
-int ssm_abi_version(void) { return 3; }
+int ssm_abi_version(void) { return 4; }
 
 int ssm_profile_begin(void) {
   g_err.clear();
@@ -417,10 +419,15 @@ int ssm_decode_gemv(int64_t batch, int64_t out_dim, int64_t in_dim, int dtype, c
                     "decode_gemv launch");
 }
 
+int64_t ssm_decode_xproj_blocks(int64_t dim, int64_t params_dim) {
+  return ssm::decode_xproj_blocks(dim, params_dim);
+}
+
 int ssm_decode_in_proj_conv(int64_t batch, int64_t dim, int64_t in_dim, int64_t width, int dtype,
                             const void* in_proj_weight, const void* x, const void* norm_weight,
                             float norm_eps, const void* in_proj_bias, const void* conv_weight,
                             const void* conv_bias, void* conv_window, void* xz, void* xc,
+                            const void* x_proj_weight, int64_t params_dim, float* xproj_partials,
                             void* stream) {
   int rc = check_decode(batch, dtype);
   if (rc != SSM_OK) return rc;
@@ -437,17 +444,29 @@ int ssm_decode_in_proj_conv(int64_t batch, int64_t dim, int64_t in_dim, int64_t 
                 ssm::conv1d_max_width(), (long long)width);
   if (!aligned16(in_proj_weight) || !aligned16(x) || !aligned16(norm_weight))
     return fail(SSM_ERR_UNSUPPORTED, "decode_in_proj_conv needs 16-byte aligned weight, x and norm_weight");
+  if ((x_proj_weight != nullptr) != (xproj_partials != nullptr))
+    return fail(SSM_ERR_INVALID, "x_proj_weight and xproj_partials go together");
+  if (x_proj_weight) {
+    if (ssm::decode_xproj_blocks(dim, params_dim) == 0)
+      return fail(SSM_ERR_UNSUPPORTED,
+                  "the folded x-projection needs ssm_decode_xproj_blocks(dim, params_dim) > 0 "
+                  "(got dim %lld, params_dim %lld)", (long long)dim, (long long)params_dim);
+    if (!aligned16(x_proj_weight) || !aligned16(xproj_partials))
+      return fail(SSM_ERR_UNSUPPORTED, "decode_in_proj_conv needs 16-byte aligned x_proj_weight and xproj_partials");
+  }
   return hip_status(ssm::launch_decode_in_proj_conv(dtype == SSM_BF16, in_proj_weight, x, norm_weight,
                                                     norm_eps, in_proj_bias, xz, (int)batch, (int)dim,
                                                     (int)in_dim, (int)width, conv_window, conv_weight,
-                                                    conv_bias, xc, static_cast<hipStream_t>(stream)),
+                                                    conv_bias, xc, x_proj_weight,
+                                                    x_proj_weight ? (int)params_dim : 0, xproj_partials,
+                                                    static_cast<hipStream_t>(stream)),
                     "decode_in_proj_conv launch");
 }
 
 int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank, int dtype,
-                        const void* params, const void* dt_proj_weight, const void* dt_bias,
-                        const void* log_A, const void* D, const void* xc, const void* xz,
-                        int64_t ld_xz, float* state, void* y, void* stream) {
+                        const void* params, int64_t params_blocks, const void* dt_proj_weight,
+                        const void* dt_bias, const void* log_A, const void* D, const void* xc,
+                        const void* xz, int64_t ld_xz, float* state, void* y, void* stream) {
   int rc = check_decode(batch, dtype);
   if (rc != SSM_OK) return rc;
   if (!params || !dt_proj_weight || !log_A || !xc || !xz || !state || !y)
@@ -460,9 +479,17 @@ int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank
     return fail(SSM_ERR_UNSUPPORTED,
                 "decode_ssm_step needs dim >= 1, rank >= 1, rank + 2 * nstate <= 16384, ld_xz >= 2 * dim");
   if (!aligned16(state)) return fail(SSM_ERR_UNSUPPORTED, "decode_ssm_step needs a 16-byte aligned state");
+  if (params_blocks) {
+    if (params_blocks != ssm::decode_xproj_blocks(dim, nout))
+      return fail(SSM_ERR_INVALID, "params_blocks must be 0 or ssm_decode_xproj_blocks(dim, rank + 2 * nstate) = %d (got %lld)",
+                  ssm::decode_xproj_blocks(dim, nout), (long long)params_blocks);
+    if (!aligned16(params))
+      return fail(SSM_ERR_UNSUPPORTED, "decode_ssm_step needs 16-byte aligned x-projection partials");
+  }
   const bool vecR = rank % elems16(dtype) == 0 && rank <= 16 * elems16(dtype) &&
                     aligned16(dt_proj_weight);
-  return hip_status(ssm::launch_decode_ssm_step(dtype == SSM_BF16, params, (int)nout, (int)rank,
+  return hip_status(ssm::launch_decode_ssm_step(dtype == SSM_BF16, params, (int)nout,
+                                                (int)params_blocks, (int)rank,
                                                 dt_proj_weight, dt_bias, log_A, D, xc, xz, (int)ld_xz,
                                                 state, y, (int)batch, (int)dim, (int)nstate, vecR,
                                                 static_cast<hipStream_t>(stream)),

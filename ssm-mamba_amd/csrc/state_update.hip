@@ -56,7 +56,13 @@ __global__ __launch_bounds__(256) void state_update_vec_kernel(
   Elem<T>::load4(Bp + bo, Bv);
   Elem<T>::load4(Cp + bo, Cv);
   float4 h4[kRows], a4[kRows];
-  float xv[kRows], dtv[kRows], bias[kRows];
+  float xv[kRows], dtv[kRows], bias[kRows], dv[kRows], zv[kRows];
+  // optional operands are read from a valid stand-in address when absent, so
+  // every load of the thread issues here, unconditionally, and the waits are
+  // counted (a load inside a branch is waited for inside it)
+  const float* __restrict__ bq = biasp ? biasp : Ap;
+  const float* __restrict__ dq = Dp ? Dp : Ap;
+  const T* __restrict__ zq = zp ? zp : xp;
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
     const int d = min(dbase + r * kRW, dim - 1);
@@ -68,14 +74,16 @@ __global__ __launch_bounds__(256) void state_update_vec_kernel(
     a4[r] = *reinterpret_cast<const float4*>(Ap + (unsigned)d * N + n0);
     xv[r] = Elem<T>::load1(xp + bd);
     dtv[r] = Elem<T>::load1(dtp + bd);
-    bias[r] = biasp ? biasp[d] : 0.0f;
+    bias[r] = bq[d];
+    dv[r] = dq[d];
+    zv[r] = Elem<T>::load1(zq + bd);
   }
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
     const int dr = dbase + r * kRW;
     const int d = min(dr, dim - 1);
     const unsigned bd = (unsigned)b * dim + d;
-    const float v = dtv[r] + bias[r];
+    const float v = dtv[r] + (biasp ? bias[r] : 0.0f);
     const float delta = softplus ? softplus_t20(v) : v;
     const float dx = delta * xv[r], dl2 = delta * kLog2e;
     float hv[4] = {h4[r].x, h4[r].y, h4[r].z, h4[r].w};
@@ -93,8 +101,8 @@ __global__ __launch_bounds__(256) void state_update_vec_kernel(
       *reinterpret_cast<float4*>(new_state + bd * (unsigned)N + n0) =
           make_float4(hv[0], hv[1], hv[2], hv[3]);
       if (q == 0) {
-        float y = fmaf(Dp ? Dp[d] : 0.0f, xv[r], part);
-        if (zp) y *= silu_f(Elem<T>::load1(zp + bd));
+        float y = fmaf(Dp ? dv[r] : 0.0f, xv[r], part);
+        if (zp) y *= silu_f(zv[r]);
         Elem<T>::store1(out + bd, y);
       }
     }
@@ -127,8 +135,13 @@ __global__ __launch_bounds__(256) void state_update_kernel(
   const unsigned bo = (unsigned)b * N + n0;         // B / C offset
 
   float part = 0.0f;
+  // optional operands from a valid stand-in address when absent (all loads
+  // issue up front)
   const float x = Elem<T>::load1(xp + bd);
-  const float v = Elem<T>::load1(dtp + bd) + (biasp ? biasp[d] : 0.0f);
+  const float bv = (biasp ? biasp : Ap)[d];
+  const float dv = (Dp ? Dp : Ap)[d];
+  const float zv = Elem<T>::load1((zp ? zp : xp) + bd);
+  const float v = Elem<T>::load1(dtp + bd) + (biasp ? bv : 0.0f);
   const float delta = softplus ? softplus_t20(v) : v;
   const float dx = delta * x, dl2 = delta * kLog2e;
 #pragma unroll
@@ -141,8 +154,8 @@ __global__ __launch_bounds__(256) void state_update_kernel(
   }
   part = lane_group_sum<kQ>(part);
   if (q == 0) {
-    float y = fmaf(Dp ? Dp[d] : 0.0f, x, part);
-    if (zp) y *= silu_f(Elem<T>::load1(zp + bd));
+    float y = fmaf(Dp ? dv : 0.0f, x, part);
+    if (zp) y *= silu_f(zv);
     Elem<T>::store1(out + bd, y);
   }
 }

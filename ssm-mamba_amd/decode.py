@@ -1,8 +1,8 @@
 """Host side of the fused decode-step kernels (``ssm_decode_*`` in
-include/ssm_mamba.h): one Mamba block step per token in four launches
-instead of the reference's per-op sequence (``modules/block.py:80-86``,
-``modules/mamba.py:189-243``), plus the LM-head GEMV with the final RMSNorm
-(``models/causal_lm.py:93-104``).
+include/ssm_mamba.h): one Mamba block step per token in three launches (four
+when the x-projection cannot be folded) instead of the reference's per-op
+sequence (``modules/block.py:80-86``, ``modules/mamba.py:189-243``), plus the
+LM-head GEMV with the final RMSNorm (``models/causal_lm.py:93-104``).
 
 These are inference kernels (no autograd).  ``block_step_supported`` says
 whether a layer and an input qualify; callers fall back to the op-by-op path
@@ -23,6 +23,9 @@ _STATE_SIZES = (4, 8, 16, 32, 64)
 # The model harness takes the fused path whenever it qualifies; set False to
 # force the op-by-op path (used to compare the two).
 ENABLED = True
+# Fold the x-projection into the in-projection and state-update kernels where
+# ssm_decode_xproj_blocks allows; False keeps it a GEMV of its own.
+FOLD_XPROJ = True
 
 
 def _elems16(dtype: torch.dtype) -> int:
@@ -56,35 +59,54 @@ def gemv(weight: torch.Tensor, x: torch.Tensor, norm_weight: Optional[torch.Tens
     return y
 
 
+def xproj_blocks(dim: int, params_dim: int) -> int:
+    """Partial blocks of the folded x-projection (0: it does not apply)."""
+    return int(N.lib().ssm_decode_xproj_blocks(dim, params_dim))
+
+
 def in_proj_conv(weight: torch.Tensor, x: torch.Tensor, norm_weight: Optional[torch.Tensor],
                  eps: float, bias: Optional[torch.Tensor], conv_weight: torch.Tensor,
-                 conv_bias: Optional[torch.Tensor], window: torch.Tensor):
+                 conv_bias: Optional[torch.Tensor], window: torch.Tensor,
+                 x_proj_weight: Optional[torch.Tensor] = None):
     """(xz (batch, 2*dim), xc (batch, dim)) of the in-projection and conv step;
-    the conv window advances in place."""
+    the conv window advances in place.  With x_proj_weight (params_dim, dim)
+    also the fp32 x-projection partials (P, batch, params_dim rounded up to 4)
+    as a third output, for ssm_step."""
     batch, k = x.shape
     dim = weight.shape[0] // 2
     width = conv_weight.shape[-1]
     xz = torch.empty(batch, 2 * dim, device=x.device, dtype=x.dtype)
     xc = torch.empty(batch, dim, device=x.device, dtype=x.dtype)
+    part, nout = None, 0
+    if x_proj_weight is not None:
+        nout = x_proj_weight.shape[0]
+        nparts = xproj_blocks(dim, nout)
+        if not nparts:
+            raise RuntimeError(f"the x-projection cannot be folded at dim {dim}, params_dim {nout}")
+        part = torch.empty(nparts, batch, (nout + 3) // 4 * 4, device=x.device, dtype=torch.float32)
     with torch.cuda.device(x.device):
         N.check(N.lib().ssm_decode_in_proj_conv(batch, dim, k, width, _DTYPES[x.dtype],
                                                 weight.data_ptr(), x.data_ptr(), _ptr(norm_weight),
                                                 float(eps), _ptr(bias), conv_weight.data_ptr(),
                                                 _ptr(conv_bias), window.data_ptr(), xz.data_ptr(),
-                                                xc.data_ptr(), _stream(x.device)))
-    return xz, xc
+                                                xc.data_ptr(), _ptr(x_proj_weight), nout,
+                                                _ptr(part), _stream(x.device)))
+    return (xz, xc) if part is None else (xz, xc, part)
 
 
 def ssm_step(params: torch.Tensor, rank: int, dt_proj_weight: torch.Tensor,
              dt_bias: Optional[torch.Tensor], log_A: torch.Tensor, D: Optional[torch.Tensor],
              xc: torch.Tensor, xz: torch.Tensor, state: torch.Tensor) -> torch.Tensor:
-    """y (batch, dim) of the state update + gate; state advances in place."""
+    """y (batch, dim) of the state update + gate; state advances in place.
+    params is (batch, rank + 2*nstate), or the 3-d fp32 partials of
+    in_proj_conv."""
     batch, dim = xc.shape
     nstate = state.shape[-1]
+    blocks = params.shape[0] if params.dim() == 3 else 0
     y = torch.empty_like(xc)
     with torch.cuda.device(xc.device):
         N.check(N.lib().ssm_decode_ssm_step(batch, dim, nstate, rank, _DTYPES[xc.dtype],
-                                            params.data_ptr(), dt_proj_weight.data_ptr(),
+                                            params.data_ptr(), blocks, dt_proj_weight.data_ptr(),
                                             _ptr(dt_bias), log_A.data_ptr(), _ptr(D),
                                             xc.data_ptr(), xz.data_ptr(), xz.stride(0),
                                             state.data_ptr(), y.data_ptr(), _stream(xc.device)))
@@ -138,9 +160,15 @@ def block_step(ssm, x: torch.Tensor, norm_weight: Optional[torch.Tensor] = None,
                eps: float = 1e-6, residual: bool = False) -> torch.Tensor:
     """Mamba.step(norm(x)) (+ x when residual): the fused path of
     ``Block.step`` (norm_weight and residual given) or ``Mamba.step``."""
-    xz, xc = in_proj_conv(ssm.input_proj.weight, x, norm_weight, eps, ssm.input_proj.bias,
-                          ssm.conv.weight, ssm.conv.bias, ssm._conv_context)
-    params = gemv(ssm.ssm_param_proj.weight, xc)                          # (batch, R + 2N)
+    wx = ssm.ssm_param_proj.weight
+    if FOLD_XPROJ and xproj_blocks(ssm.inner_dim, wx.shape[0]):
+        xz, xc, params = in_proj_conv(ssm.input_proj.weight, x, norm_weight, eps,
+                                      ssm.input_proj.bias, ssm.conv.weight, ssm.conv.bias,
+                                      ssm._conv_context, x_proj_weight=wx)
+    else:
+        xz, xc = in_proj_conv(ssm.input_proj.weight, x, norm_weight, eps, ssm.input_proj.bias,
+                              ssm.conv.weight, ssm.conv.bias, ssm._conv_context)
+        params = gemv(wx, xc)                                             # (batch, R + 2N)
     y = ssm_step(params, ssm.delta_rank, ssm.delta_proj.weight, ssm.delta_proj.bias, ssm.log_A,
                  ssm.D, xc, xz, ssm._ssm_hiddens)
     return gemv(ssm.out_proj.weight, y, bias=ssm.out_proj.bias, residual=x if residual else None)

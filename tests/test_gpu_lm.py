@@ -184,18 +184,22 @@ def test_training_gradients_fp32(cuda):
         _close(names[k].grad, gr, f"grad {k}", rtol=2e-3, atol=2e-4 * max(rms, 1e-3))
 
 
+@pytest.mark.parametrize("fold", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("batch,kw", [
     (1, dict(bias=True, conv_bias=True)),
     (3, dict(bias=False, conv_bias=False)),
     (8, dict(bias=True, conv_bias=False)),
 ])
-def test_fused_decode_matches_eager_and_oracle(cuda, dtype, batch, kw):
-    """The four fused decode kernels per layer (and the fused LM head) against
-    the op-by-op step and the oracle's step chain."""
+def test_fused_decode_matches_eager_and_oracle(cuda, dtype, batch, kw, fold):
+    """The fused decode kernels per layer (three with the x-projection folded
+    into its neighbours, four without) and the fused LM head against the
+    op-by-op step and the oracle's step chain."""
     from ssm_mamba_amd import decode as DEC
     m, cfg = make_lm(seed=20 + batch, vocab=67, model_dim=64, state_dim=16, layers=2, **kw)
     m = m.to(cuda, dtype)
+    ssm0 = m.layers[0].ssm
+    assert DEC.xproj_blocks(ssm0.inner_dim, ssm0.ssm_param_proj.weight.shape[0]) == 8
     sd = lm_state64(m)
     ids = _ids(batch, 19, cfg.vocab_size, seed=21)
     lengths = (ids != cfg.pad_token_id).sum(dim=1)
@@ -203,6 +207,7 @@ def test_fused_decode_matches_eager_and_oracle(cuda, dtype, batch, kw):
     outs = {}
     for fused in (True, False):
         DEC.ENABLED = fused
+        DEC.FOLD_XPROJ = fold
         try:
             with torch.no_grad():
                 m(ids.to(cuda), lengths.to(cuda), use_cache=True)
@@ -211,6 +216,7 @@ def test_fused_decode_matches_eager_and_oracle(cuda, dtype, batch, kw):
                 outs[(fused, "ctx")] = torch.stack([l.ssm._conv_context.float() for l in m.layers])
         finally:
             DEC.ENABLED = True
+            DEC.FOLD_XPROJ = True
     _, caches = LR.lm_forward(sd, ids, lengths, use_cache=True)
     if dtype == torch.float32:
         tol = dict(rtol=1e-3, atol=1e-4)
@@ -223,6 +229,64 @@ def test_fused_decode_matches_eager_and_oracle(cuda, dtype, batch, kw):
     _close(outs[(True, "state")], torch.stack([c[1] for c in caches]), "fused state", **tol)
     _close(outs[(True, "ctx")], torch.stack([c[0] for c in caches]), "fused window",
            rtol=tol["rtol"], atol=1e-6 if dtype == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batch,dim,rank,nstate", [
+    (1, 16, 3, 4),        # one block, params_dim 11 (padded to 12)
+    (3, 128, 4, 16),
+    (4, 2048, 64, 16),    # the 370M-class layer
+    (8, 1024, 160, 16),   # params_dim 192 (2.8B-class rank)
+    (2, 48, 248, 4),      # params_dim 256, the limit; rank past the register path
+])
+def test_folded_xproj(cuda, dtype, batch, dim, rank, nstate):
+    """The x-projection folded into the in-projection (fp32 partials per
+    16-channel block) and the state update (fixed-order sum): the partials
+    against float64 products of the kernel's own xc, zero padding, the
+    update's output and state against the unfolded chain (in-projection,
+    GEMV, update), and bit-identical repeats."""
+    from ssm_mamba_amd import decode as DEC
+    g = torch.Generator().manual_seed(dim + rank + batch)
+    K, width = 64, 4
+    nout = rank + 2 * nstate
+    r = lambda *s, scale=1.0: (scale * torch.randn(*s, generator=g)).to(dtype).to(cuda)
+    W_in, x, nw = r(2 * dim, K, scale=0.2), r(batch, K), r(K, scale=0.3)
+    b_in, cw, cb = r(2 * dim, scale=0.1), r(dim, width, scale=0.5), r(dim, scale=0.1)
+    window = r(batch, dim, width - 1)
+    W_x, W_dt, dtb = r(nout, dim, scale=0.1), r(dim, rank, scale=0.2), r(dim, scale=0.5)
+    log_A = (torch.rand(dim, nstate, generator=g) * 2).to(dtype).to(cuda)
+    D = r(dim)
+    state = torch.randn(batch, dim, nstate, generator=g).to(cuda)
+    nparts = DEC.xproj_blocks(dim, nout)
+    assert nparts == dim // 16
+    with torch.no_grad():
+        w1, s1 = window.clone(), state.clone()
+        xz1, xc1 = DEC.in_proj_conv(W_in, x, nw, 1e-6, b_in, cw, cb, w1)
+        params = DEC.gemv(W_x, xc1)
+        y1 = DEC.ssm_step(params, rank, W_dt, dtb, log_A, D, xc1, xz1, s1)
+        runs = []
+        for _ in range(2):
+            w2, s2 = window.clone(), state.clone()
+            xz2, xc2, part = DEC.in_proj_conv(W_in, x, nw, 1e-6, b_in, cw, cb, w2, x_proj_weight=W_x)
+            y2 = DEC.ssm_step(part, rank, W_dt, dtb, log_A, D, xc2, xz2, s2)
+            runs.append((xz2, xc2, part, y2, s2, w2))
+    xz2, xc2, part, y2, s2, w2 = runs[0]
+    for a, b in zip(runs[0], runs[1]):
+        assert torch.equal(a, b), "folded decode step is not bit-reproducible"
+    assert part.shape == (nparts, batch, (nout + 3) // 4 * 4) and part.dtype == torch.float32
+    assert torch.equal(part[..., nout:], torch.zeros_like(part[..., nout:]))
+    ref = torch.einsum("jpc,bpc->pbj", W_x.double().cpu().view(nout, nparts, 16),
+                       xc2.double().cpu().view(batch, nparts, 16))
+    _close(part[..., :nout], ref, "partials", rtol=1e-5, atol=1e-6)
+    same = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
+    _close(xz2, xz1, "xz", **same)
+    _close(xc2, xc1, "xc", **same)
+    _close(w2, w1, "window", **same)
+    # the update sees round_T(sum of partials) for the GEMV's round_T(W_x @ xc):
+    # equal up to the last bit of those roundings
+    step = dict(rtol=1e-4, atol=1e-4) if dtype == torch.float32 else dict(rtol=3e-2, atol=3e-2)
+    _close(s2, s1, "state", **step)
+    _close(y2, y1, "y", rtol=step["rtol"], atol=step["atol"] * max(1.0, float(y1.abs().max())))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

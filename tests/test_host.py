@@ -84,6 +84,35 @@ def test_gate_arguments_are_checked():
     assert rc == 1 and b"out_ungated requires z" in lib.ssm_last_error()
 
 
+def test_folded_xproj_queries_and_checks():
+    """The folded x-projection: its block count (16 channels per block,
+    params_dim <= 256) and the argument checks of the two calls that carry it,
+    which return before any pointer is used (no GPU needed)."""
+    from ssm_mamba_amd import _native as N
+    lib = N.lib()
+    blocks = lib.ssm_decode_xproj_blocks
+    assert blocks(2048, 96) == 128 and blocks(16, 3) == 1 and blocks(2048, 256) == 128
+    assert blocks(24, 96) == 0 and blocks(2048, 257) == 0 and blocks(0, 96) == 0
+    assert blocks(2048, 0) == 0
+    P = 4096  # never dereferenced
+
+    def in_proj(dim, wx, nout, part):
+        return lib.ssm_decode_in_proj_conv(4, dim, 1024, 4, N.SSM_BF16, P, P, P, 1e-6, None, P,
+                                           None, P, P, P, wx, nout, part, None)
+
+    assert in_proj(2048, P, 96, None) == 1 and b"go together" in lib.ssm_last_error()
+    assert in_proj(2048, None, 96, P) == 1 and b"go together" in lib.ssm_last_error()
+    assert in_proj(24, P, 96, P) == 2 and b"folded x-projection" in lib.ssm_last_error()
+    assert in_proj(2048, P, 300, P) == 2 and b"folded x-projection" in lib.ssm_last_error()
+
+    def step(blocks_arg):
+        return lib.ssm_decode_ssm_step(4, 2048, 16, 64, N.SSM_BF16, P, blocks_arg, P, None, P,
+                                       None, P, P, 4096, P, P, None)
+
+    for b in (5, 127, -1):
+        assert step(b) == 1 and b"params_blocks must be 0 or" in lib.ssm_last_error()
+
+
 def _scan_args(batch=2, dim=4, seqlen=8, nstate=3):
     return dict(u=torch.randn(batch, dim, seqlen), A=torch.randn(dim, nstate),
                 B=torch.randn(batch, nstate, seqlen), C=torch.randn(batch, nstate, seqlen),
