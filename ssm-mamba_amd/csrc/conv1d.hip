@@ -69,7 +69,10 @@ __device__ __forceinline__ void load_taps(const T* __restrict__ w, const T* __re
                                           float (&wk)[K], float& bs) {
 #pragma unroll
   for (int j = 0; j < K; ++j) wk[j] = Elem<T>::load1(w + (size_t)c * K + j);
-  bs = bias ? Elem<T>::load1(bias + c) : 0.0f;
+  // an absent bias reads a valid stand-in and is dropped: a load in a branch
+  // would be waited for there
+  bs = Elem<T>::load1(bias ? bias + c : w);
+  if (!bias) bs = 0.0f;
 }
 
 // Sum of K+1 per-thread values over the workgroup; thread 0 gets the totals.
@@ -108,21 +111,40 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
   const int c = (int)(row % (size_t)dim);
   const T* __restrict__ xr = x + row * (size_t)L;
   T* __restrict__ orow = out + row * (size_t)L;
-  if (K > 1 && window && threadIdx.x < K - 1) {
-    const int b = (int)(row / (size_t)dim);
-    const int len = lengths ? (int)min<int64_t>(max<int64_t>(lengths[b], 0), L) : L;
-    const int idx = len - (K - 1) + (int)threadIdx.x;
-    Elem<T>::store1(window + row * (K - 1) + threadIdx.x, idx >= 0 ? Elem<T>::load1(xr + idx) : 0.0f);
-  }
   float wk[K], bs;
-  load_taps<K>(w, bias, c, wk, bs);
-  if constexpr (kVec) {
+  // the decode cache's row length, fetched now and used after the main loop
+  const int64_t len_in = lengths ? lengths[row / (size_t)dim] : (int64_t)L;
+  if (kVec && L <= kConvThreads * kConvChunk) {
+    // one chunk per thread (L <= 2048): its row loads issue before the taps
+    // are waited for, so the workgroup pays one memory round trip
+    const int t0 = threadIdx.x * kConvChunk;
+    const int tc = min(t0, L - kConvChunk);
+    float v[2 * kConvChunk];
+    load8<T>(xr + tc, v + kConvChunk);
+    load8<T>(xr + max(tc - kConvChunk, 0), v);
+    load_taps<K>(w, bias, c, wk, bs);
+    if (tc == 0) {
+#pragma unroll
+      for (int i = 0; i < kConvChunk; ++i) v[i] = 0.0f;
+    }
+    float o[kConvChunk];
+#pragma unroll
+    for (int i = 0; i < kConvChunk; ++i) {
+      float acc = bs;
+#pragma unroll
+      for (int j = 0; j < K; ++j) acc = fmaf(wk[j], v[kConvChunk + i - (K - 1) + j], acc);
+      o[i] = silu ? silu_f(acc) : acc;
+    }
+    if (t0 < L) store8<T>(orow + t0, o);
+  } else if constexpr (kVec) {
+    load_taps<K>(w, bias, c, wk, bs);
     for (int t0 = threadIdx.x * kConvChunk; t0 < L; t0 += kConvThreads * kConvChunk) {
       float v[2 * kConvChunk];
       load8<T>(xr + t0, v + kConvChunk);
-      if (t0 > 0) {
-        load8<T>(xr + t0 - kConvChunk, v);
-      } else {
+      // the previous chunk from a clamped address, zeroed at the row start
+      // (no load in a branch)
+      load8<T>(xr + max(t0 - kConvChunk, 0), v);
+      if (t0 == 0) {
 #pragma unroll
         for (int i = 0; i < kConvChunk; ++i) v[i] = 0.0f;
       }
@@ -137,6 +159,7 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
       store8<T>(orow + t0, o);
     }
   } else {
+    load_taps<K>(w, bias, c, wk, bs);
     for (int t = threadIdx.x; t < L; t += kConvThreads) {
       float acc = bs;
 #pragma unroll
@@ -146,6 +169,13 @@ __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
       }
       Elem<T>::store1(orow + t, silu ? silu_f(acc) : acc);
     }
+  }
+  // the decode cache last, off the main stream's path
+  if (K > 1 && window && threadIdx.x < K - 1) {
+    const int len = (int)min<int64_t>(max<int64_t>(len_in, 0), L);
+    const int idx = len - (K - 1) + (int)threadIdx.x;
+    const float v = Elem<T>::load1(xr + max(idx, 0));
+    Elem<T>::store1(window + row * (K - 1) + threadIdx.x, idx >= 0 ? v : 0.0f);
   }
 }
 

@@ -59,8 +59,9 @@ struct Pair<__hip_bfloat16> {
 };
 
 // Channel rows per lane kept in registers between the two passes (the rest
-// are re-read from L2).
-constexpr int kHold = 8;
+// are re-read from L2, kBatch rows at a time): 16 cover d_model 1024 whole.
+constexpr int kHold = 16;
+constexpr int kBatch = 8;
 
 // kPL = 2 and kPair: L even and rows 4-byte (bf16) / 8-byte (fp32) aligned,
 // so a lane's two positions load and store as one element pair.  kShare:
@@ -94,32 +95,61 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_cm_kernel(
   constexpr int kStride = kNormWaves * kRPL;  // channel rows per workgroup sweep
   const int c_first = wave * kRPL + crow;
 
-  auto load2 = [&](int c) -> float2 {
-    const T* p = xb + (size_t)c * L + t;
+  // Loads read clamped (always valid) addresses and out-of-range values are
+  // zeroed afterwards: all loads of a batch issue first, then pass through an
+  // empty asm (so the compiler cannot turn the zeroing back into a branch
+  // around the load, where it would be waited for at once), then are masked.
+  // A pair load at t <= L - 2 stays aligned (t and L even).
+  const int tp = kPair ? min(t, L - 2) : min(t, L - 1);
+  const int tq = min(t + 1, L - 1);
+  auto raw2 = [&](int c) -> float2 {
+    const T* p = xb + (size_t)min(c, C - 1) * L;
     if constexpr (kPL == 1) {
-      return make_float2(ok0 ? Elem<T>::load1(p) : 0.f, 0.f);
+      return make_float2(Elem<T>::load1(p + tp), 0.f);
     } else if constexpr (kPair) {
-      return ok0 ? Pair<T>::load(p) : make_float2(0.f, 0.f);
+      return Pair<T>::load(p + tp);
     } else {
-      return make_float2(ok0 ? Elem<T>::load1(p) : 0.f, ok1 ? Elem<T>::load1(p + 1) : 0.f);
+      return make_float2(Elem<T>::load1(p + tp), Elem<T>::load1(p + tq));
     }
   };
+  auto mask2 = [&](int c, float2 v) -> float2 {
+    const bool okc = c < C;
+    return make_float2(okc && ok0 ? v.x : 0.f, okc && ok1 ? v.y : 0.f);
+  };
+  auto scale_of = [&](int c) { return 1.0f + Elem<T>::load1(w + min(c, C - 1)); };
+  auto pin = [](float2& v) { asm volatile("" : "+v"(v.x), "+v"(v.y)); };
 
-  // the first kHold channel rows of a lane stay in registers for pass 2
+  // the first kHold channel rows of a lane stay in registers for pass 2, with
+  // their weights
   float2 held[kHold];
-  float s0 = 0.f, s1 = 0.f;
+  float gw_held[kHold];
 #pragma unroll
   for (int i = 0; i < kHold; ++i) {
-    const int c = c_first + i * kStride;
-    held[i] = c < C ? load2(c) : make_float2(0.f, 0.f);
+    held[i] = raw2(c_first + i * kStride);
+    gw_held[i] = scale_of(c_first + i * kStride);
+  }
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kHold; ++i) pin(held[i]);
+#pragma unroll
+  for (int i = 0; i < kHold; ++i) {
+    held[i] = mask2(c_first + i * kStride, held[i]);
     s0 = fmaf(held[i].x, held[i].x, s0);
     s1 = fmaf(held[i].y, held[i].y, s1);
   }
-#pragma unroll 8
-  for (int c = c_first + kHold * kStride; c < C; c += kStride) {
-    const float2 v = load2(c);
-    s0 = fmaf(v.x, v.x, s0);
-    s1 = fmaf(v.y, v.y, s1);
+  // the remaining rows, kBatch loads in flight per lane (rows past C read 0)
+  for (int c0 = c_first + kHold * kStride; c0 < C; c0 += kBatch * kStride) {
+    float2 v[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) v[j] = raw2(c0 + j * kStride);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) pin(v[j]);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      v[j] = mask2(c0 + j * kStride, v[j]);
+      s0 = fmaf(v[j].x, v[j].x, s0);
+      s1 = fmaf(v[j].y, v[j].y, s1);
+    }
   }
   // rows of the wave that hold the same positions: lanes prow + k * kLPR
 #pragma unroll
@@ -140,8 +170,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_cm_kernel(
   }
   const float r0 = rsqrtf(q0 / (float)C + eps);
   const float r1 = rsqrtf(q1 / (float)C + eps);
-  auto put = [&](int c, float2 v) {
-    const float gw = 1.0f + Elem<T>::load1(w + c);
+  auto put = [&](int c, float2 v, float gw) {
     T* p = ob + (size_t)c * L + t;
     if constexpr (kPL == 1) {
       if (ok0) Elem<T>::store1(p, v.x * r0 * gw);
@@ -155,10 +184,20 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_cm_kernel(
 #pragma unroll
   for (int i = 0; i < kHold; ++i) {
     const int c = c_first + i * kStride;
-    if (c < C) put(c, held[i]);
+    if (c < C) put(c, held[i], gw_held[i]);
   }
-#pragma unroll 8
-  for (int c = c_first + kHold * kStride; c < C; c += kStride) put(c, load2(c));
+  for (int c0 = c_first + kHold * kStride; c0 < C; c0 += kBatch * kStride) {
+    float2 v[kBatch];
+    float gw[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      v[j] = raw2(c0 + j * kStride);
+      gw[j] = scale_of(c0 + j * kStride);
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      if (c0 + j * kStride < C) put(c0 + j * kStride, v[j], gw[j]);
+  }
 }
 
 template <typename T, int kPos, int kPL, bool kPair>
