@@ -144,10 +144,10 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
 
   __shared__ float4 sDelta[kT4][kBlockCh];  // delta (0 at padded steps)
   __shared__ float4 sDu[kT4][kBlockCh];     // delta * u
-  __shared__ float4 sSg[kT4][kBlockCh];     // softplus'(x) (0 at padded steps)
-  // sDout and sU are written in phase A by one thread group and read in
+  // sDout, sU and sSg are written in phase A by one thread group and read in
   // phase C by the other, with no barrier between a tile's phase C and the
   // next tile's phase A: they alternate between two buffers by tile parity
+  __shared__ float4 sSg[2][kT4][kBlockCh];  // softplus'(x) (0 at padded steps)
   __shared__ float4 sDout[2][kT4][kBlockCh];  // masked dout (after the z gate)
   __shared__ float4 sU[2][kT4][kBlockCh];
   // one slice per wave of the per-position sums over that wave's states,
@@ -203,9 +203,9 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     }
 
   // ---- tile-phase mapping.  Group 0 (waves 0-3) owns the u / delta side
-  // (softplus, staging, then du, ddelta, dD, dbias); group 1 (waves 4-7) the
-  // dout / z side (the gate, staging dout, dz).  Item = (channel row, 4
-  // consecutive steps) in both groups.
+  // (softplus and staging, then du and dD); group 1 (waves 4-7) the dout / z
+  // side (the gate, staging dout, dz), then ddelta and dbias.  Item =
+  // (channel row, 4 consecutive steps) in both groups.
   const bool grp1 = w >= kWaves / 2;
   const int item = tid % kItems;
   const int a_row = item / kT4;
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   };
 
   float hc[kSG][2];
-  float dzo[4];  // group 1: dz of the tile, stored in phase C
+  float dzo[4];  // group 1: dz of the tile, stored at the end of phase A
   // ---- phase A: stage a tile's per-position quantities in LDS and take its
   // saved states and B/C blocks
   auto phase_a = [&](const int tile) {
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       sDelta[a_q][a_sw] = make_float4(de[0], de[1], de[2], de[3]);
       sDu[a_q][a_sw] = make_float4(du[0], du[1], du[2], du[3]);
       sU[par][a_q][a_sw] = make_float4(v1[0], v1[1], v1[2], v1[3]);
-      sSg[a_q][a_sw] = make_float4(sg[0], sg[1], sg[2], sg[3]);
+      sSg[par][a_q][a_sw] = make_float4(sg[0], sg[1], sg[2], sg[3]);
     } else {  // dy = v1, z = v2, y = v3
       float dov[4], v3[4];
       if constexpr (kHasZ) decode4(n3, v3);
@@ -312,6 +312,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         }
       }
       sDout[par][a_q][a_sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
+      store4_nb<T, kAligned>(dzp + (rb + a_ch) * L, t0 + a_col, L, kHasZ && a_ok, dummy, dzo);
     }
 #pragma unroll
     for (int g = 0; g < kSG; ++g) {
@@ -393,44 +394,55 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     }
   };
 
-  // ---- phase C: per-position gradients.  Both groups issue two stores
-  // (group 1: dz and one to the dummy slot) so every path has the same
-  // memory-operation count.
+  // ---- phase C: per-position gradients.  Both groups add the slices of
+  // sum_n G B; group 0 then writes du (and accumulates dD), group 1 adds the
+  // slices of sum_n A G a h as well and writes ddelta (and accumulates
+  // dbias).  One store each, so every path has the same memory-operation
+  // count; the split evens out the work of the two groups between the
+  // barriers (group 0 also runs the softplus in phase A, group 1 the gate).
+  // Waves w and w + 4 share a SIMD, so an uneven split leaves each SIMD with
+  // one wave to issue from.
   auto phase_c = [&](const int tile) {
     const int t0 = tile * kTileB;
     const int par = tile & 1;
     const int t = t0 + a_col;
+    float4 gb = sGB[0][a_q][a_sw];
+#pragma unroll
+    for (int ww = 1; ww < kWaves; ++ww) {
+      const float4 q1 = sGB[ww][a_q][a_sw];
+      gb.x += q1.x; gb.y += q1.y; gb.z += q1.z; gb.w += q1.w;
+    }
+    const float gbv[4] = {gb.x, gb.y, gb.z, gb.w};
+    float uu[4];
+    f4_to(sU[par][a_q][a_sw], uu);
     if (!grp1) {
-      float4 gb = sGB[0][a_q][a_sw];
+      float de[4], dov[4];
+      f4_to(sDelta[a_q][a_sw], de);
+      f4_to(sDout[par][a_q][a_sw], dov);
+      float duo[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        duo[j] = fmaf(Dv, dov[j], de[j] * gbv[j]);
+        accD = fmaf(dov[j], uu[j], accD);  // dov is 0 at padded steps
+      }
+      store4_nb<T, kAligned>(dup + (rb + a_ch) * L, t, L, a_ok, dummy, duo);
+    } else {
       float4 gd = sDD[0][a_q][a_sw];
 #pragma unroll
       for (int ww = 1; ww < kWaves; ++ww) {
-        const float4 q1 = sGB[ww][a_q][a_sw];
         const float4 q2 = sDD[ww][a_q][a_sw];
-        gb.x += q1.x; gb.y += q1.y; gb.z += q1.z; gb.w += q1.w;
         gd.x += q2.x; gd.y += q2.y; gd.z += q2.z; gd.w += q2.w;
       }
-      const float gbv[4] = {gb.x, gb.y, gb.z, gb.w};
       const float gdv[4] = {gd.x, gd.y, gd.z, gd.w};
-      float de[4], uu[4], dov[4], sg[4];
-      f4_to(sDelta[a_q][a_sw], de);
-      f4_to(sU[par][a_q][a_sw], uu);
-      f4_to(sDout[par][a_q][a_sw], dov);
-      f4_to(sSg[a_q][a_sw], sg);
-      float duo[4], ddo[4];
+      float sg[4];
+      f4_to(sSg[par][a_q][a_sw], sg);
+      float ddo[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float dd = fmaf(uu[j], gbv[j], gdv[j]) * sg[j];  // sg is 0 at padded steps
-        duo[j] = fmaf(Dv, dov[j], de[j] * gbv[j]);
-        ddo[j] = dd;
-        accD = fmaf(dov[j], uu[j], accD);  // dov is 0 at padded steps
-        accB += dd;
+        ddo[j] = fmaf(uu[j], gbv[j], gdv[j]) * sg[j];  // sg is 0 at padded steps
+        accB += ddo[j];
       }
-      store4_nb<T, kAligned>(dup + (rb + a_ch) * L, t, L, a_ok, dummy, duo);
       store4_nb<T, kAligned>(ddp + (rb + a_ch) * L, t, L, a_ok, dummy, ddo);
-    } else {
-      store4_nb<T, kAligned>(dzp + (rb + a_ch) * L, t, L, kHasZ && a_ok, dummy, dzo);
-      store4_nb<T, kAligned>(dzp, t, L, false, dummy, dzo);
     }
   };
 
@@ -461,14 +473,11 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         if (dh_init && seg == 0) dh_init[(rb + ch) * N + n] = gam[g][s];
       }
     }
-  // the 4 items of a channel row are 4 consecutive lanes of group 0
-  if (!grp1) {
-    const float sd = group_sum<kT4>(accD);
-    const float sb = group_sum<kT4>(accB);
-    if (a_ok && a_q == 0) {
-      ws_D[srow * Dm + a_ch] = sd;
-      ws_bias[srow * Dm + a_ch] = sb;
-    }
+  // the 4 items of a channel row are 4 consecutive lanes of a group: dD
+  // from group 0, dbias from group 1
+  {
+    const float sv = group_sum<kT4>(grp1 ? accB : accD);
+    if (a_ok && a_q == 0) (grp1 ? ws_bias : ws_D)[srow * Dm + a_ch] = sv;
   }
 }
 
