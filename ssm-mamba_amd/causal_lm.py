@@ -48,8 +48,12 @@ def _proj_cm(weight: torch.Tensor, x: torch.Tensor, bias: Optional[torch.Tensor]
     """``weight @ x`` for channel-major x (batch, in, L) -> (batch, out, L):
     one strided-batched GEMM with the weight broadcast over the batch (batch
     stride 0), contiguous result.  (``torch.matmul`` would fold a weight that
-    requires grad through transposed copies of x and of the result.)"""
-    x = x.contiguous()
+    requires grad through transposed copies of x and of the result.)  A view
+    whose per-batch (in, L) matrices are contiguous, such as a channel slice
+    of a larger activation, is passed as it is: the GEMM takes its batch
+    stride."""
+    if not (x.stride(2) == 1 and x.stride(1) == x.shape[2]):
+        x = x.contiguous()
     w = weight.expand(x.shape[0], weight.shape[0], weight.shape[1])
     if bias is None:
         return torch.bmm(w, x)
