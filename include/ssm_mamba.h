@@ -77,11 +77,17 @@ size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, 
  * D, delta_bias, h_init, length, z are nullable.  padding_right: 1 = valid
  * positions are t < length[b], 0 = t >= seqlen - length[b] (lengths are
  * clamped to [0, seqlen]); padded steps leave the state unchanged.
+ * B and C: rows of seqlen, nstate rows per batch row, batch row b starting
+ * bc_batch_stride elements after row b-1 (0: nstate * seqlen, contiguous).
+ * The reference takes B/C batch strides too (B_batch_stride,
+ * csrc/selective_scan/selective_scan.cpp:83-87); a channel slice of the
+ * x-projection output can be passed in place.
  * nstate <= 256.  workspace: ssm_scan_fwd_workspace_bytes() bytes.
  */
 int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
                            const void* u, const void* delta, const float* A, const void* B,
-                           const void* C, const float* D, const float* delta_bias,
+                           const void* C, int64_t bc_batch_stride, const float* D,
+                           const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
                            const void* z, int delta_softplus, void* out, void* out_ungated,
                            float* h_chunks, float* h_last, void* workspace, size_t workspace_bytes,
@@ -93,7 +99,8 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
  * csrc/selective_scan/selective_scan.h:86-99) behind selective_scan.backward
  * (csrc/selective_scan/bindings.cpp:7).
  *
- * Inputs as for the forward plus h_chunks (from the forward), dout (the
+ * Inputs as for the forward (B and C with bc_batch_stride; dB and dC are
+ * written contiguous) plus h_chunks (from the forward), dout (the
  * upstream gradient of out; ignored at padded positions) and dh_last
  * (nullable = zero).  Writes du, ddelta, dA, dB, dC (all overwritten), and
  * when non-NULL dD, ddelta_bias and dh_init (requires h_init).  With z,
@@ -104,7 +111,8 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
  */
 int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
                            const void* u, const void* delta, const float* A, const void* B,
-                           const void* C, const float* D, const float* delta_bias,
+                           const void* C, int64_t bc_batch_stride, const float* D,
+                           const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
                            const void* z, const void* out_ungated, int delta_softplus,
                            const float* h_chunks, const void* dout, const float* dh_last,

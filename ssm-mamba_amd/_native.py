@@ -35,14 +35,16 @@ SIGNATURES = {
     "ssm_scan_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "ssm_selective_scan_fwd": (_i32, [
         _i64, _i64, _i64, _i64, _i32,          # batch, dim, seqlen, nstate, dtype
-        _p, _p, _p, _p, _p, _p, _p, _p, _p,    # u, delta, A, B, C, D, delta_bias, h_init, length
+        _p, _p, _p, _p, _p, _i64,              # u, delta, A, B, C, bc_batch_stride
+        _p, _p, _p, _p,                        # D, delta_bias, h_init, length
         _i32, _p, _i32,                        # padding_right, z, delta_softplus
         _p, _p, _p, _p,                        # out, out_ungated, h_chunks, h_last
         _p, _sz, _p,                           # workspace, bytes, stream
     ]),
     "ssm_selective_scan_bwd": (_i32, [
         _i64, _i64, _i64, _i64, _i32,
-        _p, _p, _p, _p, _p, _p, _p, _p, _p,    # u, delta, A, B, C, D, delta_bias, h_init, length
+        _p, _p, _p, _p, _p, _i64,              # u, delta, A, B, C, bc_batch_stride
+        _p, _p, _p, _p,                        # D, delta_bias, h_init, length
         _i32, _p, _p, _i32,                    # padding_right, z, out_ungated, delta_softplus
         _p, _p, _p,                            # h_chunks, dout, dh_last
         _p, _p, _p, _p, _p, _p, _p, _p, _p,    # du, ddelta, dA, dB, dC, dD, ddelta_bias, dh_init, dz
@@ -92,7 +94,7 @@ SIGNATURES = {
     ]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 def lib() -> ctypes.CDLL:

@@ -250,8 +250,9 @@ class Mamba(nn.Module):
             self._conv_context = window
         params = _proj_cm(self.ssm_param_proj.weight, xc)           # (batch, R + 2N, L)
         delta = _proj_cm(self.delta_proj.weight, params[:, :rank])
-        Bm = params[:, rank:rank + nstate].contiguous()
-        Cm = params[:, rank + nstate:].contiguous()
+        # B and C go to the scan as slices of params (one shared batch stride)
+        Bm = params[:, rank:rank + nstate]
+        Cm = params[:, rank + nstate:]
         A, D, dt_bias = self._scan_params()
         # padding_side "left" is the reference's default at this call
         # (modules/mamba.py:170-175 passes no padding argument)

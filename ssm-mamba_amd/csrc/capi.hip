@@ -124,7 +124,8 @@ int check_common(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int
 
 ssm::ScanParams make_scan_params(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate,
                                  const void* u, const void* delta, const float* A, const void* B,
-                                 const void* C, const float* D, const float* delta_bias,
+                                 const void* C, int64_t bc_batch_stride, const float* D,
+                                 const float* delta_bias,
                                  const float* h_init, const int64_t* length, int padding_right,
                                  const void* z, int delta_softplus) {
   ssm::ScanParams p{};
@@ -141,6 +142,7 @@ ssm::ScanParams make_scan_params(int64_t batch, int64_t dim, int64_t seqlen, int
   p.A = A;
   p.B = B;
   p.C = C;
+  p.bc_bstride = bc_batch_stride ? bc_batch_stride : nstate * seqlen;
   p.D = D;
   p.bias = delta_bias;
   p.h_init = h_init;
@@ -192,7 +194,7 @@ extern "C" {
 
 const char* ssm_last_error(void) { return g_err.c_str(); }
 
-int ssm_abi_version(void) { return 4; }
+int ssm_abi_version(void) { return 5; }
 
 int ssm_profile_begin(void) {
   g_err.clear();
@@ -269,7 +271,8 @@ size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, 
 
 int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
                            const void* u, const void* delta, const float* A, const void* B,
-                           const void* C, const float* D, const float* delta_bias,
+                           const void* C, int64_t bc_batch_stride, const float* D,
+                           const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
                            const void* z, int delta_softplus, void* out, void* out_ungated,
                            float* h_chunks, float* h_last, void* workspace, size_t workspace_bytes,
@@ -282,7 +285,11 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   const size_t need = ssm_scan_fwd_workspace_bytes(batch, dim, seqlen, nstate);
   if (!workspace || workspace_bytes < need)
     return fail(SSM_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-  ssm::ScanParams p = make_scan_params(batch, dim, seqlen, nstate, u, delta, A, B, C, D, delta_bias,
+  if (bc_batch_stride != 0 && bc_batch_stride < nstate * seqlen)
+    return fail(SSM_ERR_INVALID, "bc_batch_stride must be 0 (contiguous) or at least nstate * seqlen (got %lld)",
+                (long long)bc_batch_stride);
+  ssm::ScanParams p = make_scan_params(batch, dim, seqlen, nstate, u, delta, A, B, C,
+                                       bc_batch_stride, D, delta_bias,
                                        h_init, length, padding_right, z, delta_softplus);
   p.out = out;
   p.out_ungated = out_ungated;
@@ -305,7 +312,8 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
 
 int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
                            const void* u, const void* delta, const float* A, const void* B,
-                           const void* C, const float* D, const float* delta_bias,
+                           const void* C, int64_t bc_batch_stride, const float* D,
+                           const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
                            const void* z, const void* out_ungated, int delta_softplus,
                            const float* h_chunks, const void* dout, const float* dh_last,
@@ -325,7 +333,11 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   const size_t need = ssm_scan_bwd_workspace_bytes(batch, dim, seqlen, nstate);
   if (!workspace || workspace_bytes < need)
     return fail(SSM_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-  ssm::ScanParams p = make_scan_params(batch, dim, seqlen, nstate, u, delta, A, B, C, D, delta_bias,
+  if (bc_batch_stride != 0 && bc_batch_stride < nstate * seqlen)
+    return fail(SSM_ERR_INVALID, "bc_batch_stride must be 0 (contiguous) or at least nstate * seqlen (got %lld)",
+                (long long)bc_batch_stride);
+  ssm::ScanParams p = make_scan_params(batch, dim, seqlen, nstate, u, delta, A, B, C,
+                                       bc_batch_stride, D, delta_bias,
                                        h_init, length, padding_right, z, delta_softplus);
   p.h_chunks_in = h_chunks;
   p.dout = dout;

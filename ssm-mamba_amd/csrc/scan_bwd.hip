@@ -171,8 +171,8 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   const int ngroups = (N + 1) / 2;
   const size_t rb = (size_t)b * Dm;
   const size_t nBC = (size_t)p.batch * N * L;
-  const T* __restrict__ Braw = Bp + (size_t)b * N * L;
-  const T* __restrict__ Craw = Cp + (size_t)b * N * L;
+  const T* __restrict__ Braw = Bp + (size_t)b * p.bc_bstride;
+  const T* __restrict__ Craw = Cp + (size_t)b * p.bc_bstride;
   float* const dummyf = static_cast<float*>(dummy);
 
   int vlo, vhi;

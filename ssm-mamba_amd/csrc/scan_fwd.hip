@@ -41,6 +41,7 @@ __global__ __launch_bounds__(256) void bc_prep_kernel(const int batch, const int
                                                       const int npair, const int Lp,
                                                       const T* __restrict__ Bp,
                                                       const T* __restrict__ Cp,
+                                                      const int64_t bstride,
                                                       float* __restrict__ bc) {
   const size_t total = (size_t)batch * npair * Lp;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
@@ -54,7 +55,7 @@ __global__ __launch_bounds__(256) void bc_prep_kernel(const int batch, const int
     for (int s = 0; s < 2; ++s) {
       const int n = G * 2 + s;
       const bool ok = n < N && t < L;
-      const size_t src = ((size_t)b * N + n) * L + t;
+      const size_t src = (size_t)b * bstride + (size_t)n * L + t;
       v[2 * s] = ok ? Elem<T>::load1(Bp + src) : 0.0f;
       v[2 * s + 1] = ok ? Elem<T>::load1(Cp + src) : 0.0f;
     }
@@ -204,8 +205,8 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   constexpr int kBCItems = kSubF * kWaves * kTileF;
   constexpr int kBCPer = kBCItems / kThreads;
   static_assert(kBCItems % kThreads == 0, "whole B/C items per thread");
-  const T* __restrict__ Braw = static_cast<const T*>(Bp) + (size_t)b * N * L;
-  const T* __restrict__ Craw = static_cast<const T*>(Cp) + (size_t)b * N * L;
+  const T* __restrict__ Braw = static_cast<const T*>(Bp) + (size_t)b * p.bc_bstride;
+  const T* __restrict__ Craw = static_cast<const T*>(Cp) + (size_t)b * p.bc_bstride;
   float qbc[kBCPer][4];
   auto issue = [&](int T0) {
 #pragma unroll
@@ -735,10 +736,10 @@ hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t
   if (dtype == 1)
     hipLaunchKernelGGL(bc_prep_kernel<__hip_bfloat16>, dim3(blocks), dim3(256), 0, st, p.batch,
                        p.nstate, p.seqlen, npair, Lp, (const __hip_bfloat16*)p.B,
-                       (const __hip_bfloat16*)p.C, bc);
+                       (const __hip_bfloat16*)p.C, p.bc_bstride, bc);
   else
     hipLaunchKernelGGL(bc_prep_kernel<float>, dim3(blocks), dim3(256), 0, st, p.batch, p.nstate,
-                       p.seqlen, npair, Lp, (const float*)p.B, (const float*)p.C, bc);
+                       p.seqlen, npair, Lp, (const float*)p.B, (const float*)p.C, p.bc_bstride, bc);
   return hipGetLastError();
 }
 

@@ -31,6 +31,7 @@ struct ScanDims {
   int seg_len;  // steps per sequence segment (a multiple of the forward super-tile)
   int nseg;     // segments (1: the whole row in one workgroup)
   int sub_k;    // forward summaries per segment (sub-segments of seg_len / sub_k steps)
+  int64_t bc_bstride;  // elements between batch rows of B and of C (rows of a batch are seqlen apart)
 };
 
 struct ScanParams {
@@ -43,6 +44,7 @@ struct ScanParams {
   const float* A;
   const void* B;
   const void* C;
+  int64_t bc_bstride;  // elements between batch rows of B and of C
   const float* D;      // nullable
   const float* bias;   // nullable
   const float* h_init; // nullable
@@ -108,7 +110,7 @@ struct UpdateParams {
 
 inline ScanDims dims_of(const ScanParams& p) {
   return ScanDims{p.batch,    p.dim,     p.seqlen,  p.nstate, p.nchunks, p.nblk,
-                  p.pad_right, p.softplus, p.seg_len, p.nseg,   p.sub_k};
+                  p.pad_right, p.softplus, p.seg_len, p.nseg,   p.sub_k,  p.bc_bstride};
 }
 
 }  // namespace ssm

@@ -71,7 +71,12 @@ class _SelectiveScanExtFn(torch.autograd.Function):
     def forward(ctx, u, delta, A, B, C, D, z, delta_bias, h_init, length, delta_softplus,
                 padding_side):
         io = u.dtype
-        u, delta, B, C, z = (ensure_contiguous(_as(t, io)) for t in (u, delta, B, C, z))
+        u, delta, z = (ensure_contiguous(_as(t, io)) for t in (u, delta, z))
+        B, C = _as(B, io), _as(C, io)
+        # batch-strided B / C views (a slice of the x-projection output) go to
+        # the kernels as they are; other layouts are made contiguous
+        if not selective_scan.bc_batch_strided(B, C):
+            B, C = ensure_contiguous(B), ensure_contiguous(C)
         A32, D32, bias32, h0 = (ensure_contiguous(_as(t, torch.float32))
                                 for t in (A, D, delta_bias, h_init))
         length = ensure_contiguous(length)

@@ -41,15 +41,37 @@ def _check_dim(x: torch.Tensor, n: int, name: str) -> None:
         raise RuntimeError(f"{name} must be a {n}D tensor")
 
 
-def _check(x: torch.Tensor, name: str, shape, shape_txt: str, dtypes, dtype_txt: str) -> None:
+def _check(x: torch.Tensor, name: str, shape, shape_txt: str, dtypes, dtype_txt: str,
+           contiguous: bool = True) -> None:
     if not x.is_cuda:
         raise RuntimeError(f"{name} must be a CUDA tensor")
     if x.dtype not in dtypes:
         raise RuntimeError(f"{name} must be {dtype_txt} tensor")
-    if not x.is_contiguous():
+    if contiguous and not x.is_contiguous():
         raise RuntimeError(f"{name} must be contiguous")
     if tuple(x.shape) != tuple(shape):
         raise RuntimeError(f"{name} must have shape ({shape_txt})")
+
+
+def bc_batch_strided(B: torch.Tensor, C: torch.Tensor) -> bool:
+    """Whether B and C (batch, state_dim, seq_len) can be passed as they are:
+    rows contiguous, the rows of a batch row seq_len apart, one batch stride
+    shared by B and C (a channel slice of the x-projection output is)."""
+    if B.dim() != 3 or C.dim() != 3 or B.shape != C.shape:
+        return False
+    batch, nstate, seqlen = B.shape
+    for x in (B, C):
+        if x.stride(2) != 1 or (nstate > 1 and x.stride(1) != seqlen):
+            return False
+        if batch > 1 and x.stride(0) < nstate * seqlen:
+            return False
+    return batch == 1 or B.stride(0) == C.stride(0)
+
+
+def _bc_stride(B: torch.Tensor) -> int:
+    """The bc_batch_stride argument (0: contiguous)."""
+    batch, nstate, seqlen = B.shape
+    return 0 if (batch == 1 or B.stride(0) == nstate * seqlen) else B.stride(0)
 
 
 def _ptr(x: Optional[torch.Tensor]):
@@ -84,8 +106,12 @@ def _validate(u, A, B, C, D, delta, delta_bias, h_init, length, z):
     io = (u.dtype,)
     io_txt = str(u.dtype).replace("torch.", "") + " (the dtype of u)"
     _check(A, "A", (dim, nstate), "num_channels, state_dim", f32, "float32")
-    _check(B, "B", (batch, nstate, seqlen), "batch_size, state_dim, seq_len", io, io_txt)
-    _check(C, "C", (batch, nstate, seqlen), "batch_size, state_dim, seq_len", io, io_txt)
+    # B and C may also be batch-strided views (bc_batch_strided)
+    bc_ok = bc_batch_strided(B, C)
+    _check(B, "B", (batch, nstate, seqlen), "batch_size, state_dim, seq_len", io,
+           io_txt, contiguous=not bc_ok)
+    _check(C, "C", (batch, nstate, seqlen), "batch_size, state_dim, seq_len", io, io_txt,
+           contiguous=not bc_ok)
     if D is not None:
         _check(D, "D", (dim,), "num_channels", f32, "float32")
     _check(delta, "delta", (batch, dim, seqlen), "batch_size, num_channels, seq_len", io, io_txt)
@@ -149,8 +175,8 @@ def forward(u: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
         N.check(L.ssm_selective_scan_fwd(
             batch, dim, seqlen, nstate, _STREAM_DTYPES[u.dtype],
             u.data_ptr(), delta.data_ptr(), A.data_ptr(), B.data_ptr(), C.data_ptr(),
-            _ptr(D), _ptr(delta_bias), _ptr(h_init), _ptr(length), padding_right, _ptr(z),
-            1 if delta_softplus else 0, out.data_ptr(), _ptr(out_ungated), _ptr(h_chunks),
+            _bc_stride(B), _ptr(D), _ptr(delta_bias), _ptr(h_init), _ptr(length), padding_right,
+            _ptr(z), 1 if delta_softplus else 0, out.data_ptr(), _ptr(out_ungated), _ptr(h_chunks),
             _ptr(h_last), ws.data_ptr(), wsb, _stream(dev)))
     return [out, h]
 
@@ -202,8 +228,8 @@ def backward(u: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
         N.check(L.ssm_selective_scan_bwd(
             batch, dim, seqlen, nstate, _STREAM_DTYPES[u.dtype],
             u.data_ptr(), delta.data_ptr(), A.data_ptr(), B.data_ptr(), C.data_ptr(),
-            _ptr(D), _ptr(delta_bias), _ptr(h_init), _ptr(length), padding_right, _ptr(z),
-            _ptr(out_ungated), 1 if delta_softplus else 0, h.data_ptr(), dout.data_ptr(),
+            _bc_stride(B), _ptr(D), _ptr(delta_bias), _ptr(h_init), _ptr(length), padding_right,
+            _ptr(z), _ptr(out_ungated), 1 if delta_softplus else 0, h.data_ptr(), dout.data_ptr(),
             _ptr(dh_last),
             du.data_ptr(), ddelta.data_ptr(), dA.data_ptr(), dB.data_ptr(), dC.data_ptr(),
             _ptr(dD), _ptr(dbias), _ptr(dh_init), _ptr(dz), ws.data_ptr(), wsb, _stream(dev)))

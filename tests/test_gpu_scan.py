@@ -254,3 +254,42 @@ def test_functional_alias(cuda):
                      None, True, c["z"], True)
     assert_close(out, ref["y"], torch.float32, "out")
     assert_close(last, ref["h_last"], torch.float32, "last", scale_atol=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batch,dim,seqlen,nstate", [
+    (2, 64, 300, 16),     # split path (few workgroups), partial last tile
+    (4, 512, 256, 16),    # one segment per row
+    (3, 128, 64, 5),      # odd state count
+    (1, 64, 48, 16),      # batch 1 (the stride is never used)
+])
+def test_batch_strided_bc(cuda, dtype, batch, dim, seqlen, nstate):
+    """B and C passed as channel slices of one larger activation (the
+    x-projection output of the model): rows contiguous, one batch stride
+    larger than nstate * seqlen.  Forward and backward must equal the
+    contiguous copies bit for bit (the kernels read the same values)."""
+    from ssm_mamba_amd.ops import selective_scan_fn
+    from ssm_mamba_amd.selective_scan import bc_batch_strided
+    g = torch.Generator().manual_seed(batch * 1000 + dim + seqlen + nstate)
+    rank = 8
+    P = torch.randn(batch, rank + 2 * nstate, seqlen, generator=g).to(dtype).to(cuda)
+    u = torch.randn(batch, dim, seqlen, generator=g).to(dtype).to(cuda)
+    delta = (0.5 * torch.randn(batch, dim, seqlen, generator=g)).to(dtype).to(cuda)
+    z = torch.randn(batch, dim, seqlen, generator=g).to(dtype).to(cuda)
+    A = (-torch.rand(dim, nstate, generator=g) - 0.5).to(cuda)
+    D = torch.randn(dim, generator=g).to(cuda)
+    bias = (0.3 * torch.randn(dim, generator=g)).to(cuda)
+    dout = torch.randn(batch, dim, seqlen, generator=g).to(dtype).to(cuda)
+    Bv, Cv = P[:, rank:rank + nstate], P[:, rank + nstate:]
+    assert bc_batch_strided(Bv, Cv) and (batch == 1 or not Bv.is_contiguous())
+    outs = []
+    for B, C in ((Bv, Cv), (Bv.contiguous(), Cv.contiguous())):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (u, delta, B, C, z)]
+        lu, ld, lB, lC, lz = leaves
+        y, last = selective_scan_fn(lu, ld, A, lB, lC, D, z=lz, delta_bias=bias,
+                                    return_last_state=True)
+        y.backward(dout)
+        outs.append([y.detach(), last.detach()] + [t.grad for t in leaves])
+    names = ["out", "last", "du", "ddelta", "dB", "dC", "dz"]
+    for n, a, b in zip(names, outs[0], outs[1]):
+        assert torch.equal(a, b), f"{n} differs between strided and contiguous B/C"

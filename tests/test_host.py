@@ -43,19 +43,23 @@ def test_invalid_arguments_return_errors():
     """The C ABI rejects bad sizes before touching any pointer (no GPU needed)."""
     from ssm_mamba_amd import _native as N
     lib = N.lib()
-    rc = lib.ssm_selective_scan_fwd(1, 1, 1, 300, 0, *([None] * 9), 1, None, 1, None, None, None,
-                                    None, None, 0, None)
+    rc = lib.ssm_selective_scan_fwd(1, 1, 1, 300, 0, *([None] * 5), 0,
+                                    *([None] * 4), 1, None, 1, None, None, None, None, None, 0,
+                                    None)
     assert rc == 2 and b"state_dim <= 256" in lib.ssm_last_error()
-    rc = lib.ssm_selective_scan_fwd(1, 1, 0, 16, 0, *([None] * 9), 1, None, 1, None, None, None,
-                                    None, None, 0, None)
+    rc = lib.ssm_selective_scan_fwd(1, 1, 0, 16, 0, *([None] * 5), 0,
+                                    *([None] * 4), 1, None, 1, None, None, None, None, None, 0,
+                                    None)
     assert rc == 1 and b">= 1" in lib.ssm_last_error()
-    rc = lib.ssm_selective_scan_fwd(1, 1, 1, 16, 7, *([None] * 9), 1, None, 1, None, None, None,
-                                    None, None, 0, None)
+    rc = lib.ssm_selective_scan_fwd(1, 1, 1, 16, 7, *([None] * 5), 0,
+                                    *([None] * 4), 1, None, 1, None, None, None, None, None, 0,
+                                    None)
     assert rc == 1 and b"dtype" in lib.ssm_last_error()
-    rc = lib.ssm_selective_scan_fwd(1, 1, 1, 16, 0, *([None] * 9), 1, None, 1, None, None, None,
-                                    None, None, 0, None)
+    rc = lib.ssm_selective_scan_fwd(1, 1, 1, 16, 0, *([None] * 5), 0,
+                                    *([None] * 4), 1, None, 1, None, None, None, None, None, 0,
+                                    None)
     assert rc == 1 and b"non-NULL" in lib.ssm_last_error()
-    rc = lib.ssm_selective_scan_bwd(1, 1, 1, 65, 0, *([None] * 9), 1, None, None, 1, None, None,
+    rc = lib.ssm_selective_scan_bwd(1, 1, 1, 65, 0, *([None] * 5), 0, *([None] * 4), 1, None, None, 1, None, None,
                                     None, *([None] * 9), None, 0, None)
     assert rc == 2 and b"state_dim <= 64" in lib.ssm_last_error()
     rc = lib.ssm_selective_state_update(1, 1, 16, 0, *([None] * 10), 1, None, None)
@@ -71,7 +75,7 @@ def test_gate_arguments_are_checked():
     P = 4096  # never dereferenced: every call below fails its argument checks
 
     def bwd(z, y, dz):
-        return lib.ssm_selective_scan_bwd(1, 64, 16, 16, 0, P, P, P, P, P, None, None, None, None,
+        return lib.ssm_selective_scan_bwd(1, 64, 16, 16, 0, P, P, P, P, P, 0, None, None, None, None,
                                           1, z, y, 1, P, P, None, P, P, P, P, P, None, None, None,
                                           dz, P, 1 << 30, None)
 
@@ -79,7 +83,7 @@ def test_gate_arguments_are_checked():
         assert bwd(z, y, dz) == 1 and b"requires dz and out_ungated" in lib.ssm_last_error()
     for y, dz in ((P, None), (None, P), (P, P)):
         assert bwd(None, y, dz) == 1 and b"require z" in lib.ssm_last_error()
-    rc = lib.ssm_selective_scan_fwd(1, 64, 16, 16, 0, P, P, P, P, P, None, None, None, None, 1,
+    rc = lib.ssm_selective_scan_fwd(1, 64, 16, 16, 0, P, P, P, P, P, 0, None, None, None, None, 1,
                                     None, 1, P, P, P, None, P, 1 << 30, None)
     assert rc == 1 and b"out_ungated requires z" in lib.ssm_last_error()
 
@@ -111,6 +115,21 @@ def test_folded_xproj_queries_and_checks():
 
     for b in (5, 127, -1):
         assert step(b) == 1 and b"params_blocks must be 0 or" in lib.ssm_last_error()
+
+
+def test_bc_batch_stride_is_checked():
+    """A B/C batch stride below nstate * seqlen is rejected (0 means contiguous)."""
+    from ssm_mamba_amd import _native as N
+    lib = N.lib()
+    P = 4096  # never dereferenced
+    ws = 1 << 30
+    rc = lib.ssm_selective_scan_fwd(2, 64, 16, 16, 0, P, P, P, P, P, 16 * 16 - 8, None, None, None,
+                                    None, 1, None, 1, P, None, P, None, P, ws, None)
+    assert rc == 1 and b"bc_batch_stride" in lib.ssm_last_error()
+    rc = lib.ssm_selective_scan_bwd(2, 64, 16, 16, 0, P, P, P, P, P, 100, None, None, None, None,
+                                    1, None, None, 1, P, P, None, P, P, P, P, P, None, None, None,
+                                    None, P, ws, None)
+    assert rc == 1 and b"bc_batch_stride" in lib.ssm_last_error()
 
 
 def _scan_args(batch=2, dim=4, seqlen=8, nstate=3):
