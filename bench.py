@@ -35,8 +35,8 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB, the factors being what the same
 # counters read for a 256 MiB device-to-device copy.  Re-measure after a
 # kernel change.
-TRAFFIC_BYTES = {"scan_fwd": (2 * 105_437 + 286_332) * 1024,
-                 "scan_bwd": (2 * 591_735 + 410_885) * 1024}
+TRAFFIC_BYTES = {"scan_fwd": (2 * 103_763 + 277_650) * 1024,
+                 "scan_bwd": (2 * 519_607 + 376_340) * 1024}
 
 
 def inputs(batch, dim, seqlen, nstate, dtype, dev, seed, delta_shift=0.0):

@@ -122,6 +122,26 @@ __device__ __forceinline__ void bwd_reverse_block(int jq, const StepVals& sv, fl
 // 64 consecutive float4s).
 __device__ __forceinline__ constexpr int bcol_swz(int q) { return 4 * q + 2 * (q >> 1); }
 
+// two elements of an aligned row (the unaligned path keeps element stores)
+template <typename T, bool kAligned>
+__device__ __forceinline__ void store2_nb(T* __restrict__ row, int t, int L, bool ok,
+                                          void* __restrict__ dummy, const float (&v)[4]) {
+  if constexpr (kAligned) {
+    T* dst = (ok && t < L) ? row + t : static_cast<T*>(dummy);
+    if constexpr (sizeof(T) == 4) {
+      *reinterpret_cast<float2*>(dst) = make_float2(v[0], v[1]);
+    } else {
+      *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(v[0], v[1]);
+    }
+  } else {
+    if (ok) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (t + j < L) Elem<T>::store1(row + t + j, v[j]);
+    }
+  }
+}
+
 template <typename T, int kSG, bool kHasZ, bool kAligned>
 __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
@@ -268,7 +288,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   };
 
   float hc[kSG][2];
-  float dzo[4];  // group 1: dz of the tile, stored at the end of phase A
+  float dzo[4];  // group 1: dz of the tile, stored at the start of phase C
   // ---- phase A: stage a tile's per-position quantities in LDS and take its
   // saved states and B/C blocks
   auto phase_a = [&](const int tile) {
@@ -312,7 +332,6 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         }
       }
       sDout[par][a_q][a_sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
-      store4_nb<T, kAligned>(dzp + (rb + a_ch) * L, t0 + a_col, L, kHasZ && a_ok, dummy, dzo);
     }
 #pragma unroll
     for (int g = 0; g < kSG; ++g) {
@@ -395,17 +414,20 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   };
 
   // ---- phase C: per-position gradients.  Both groups add the slices of
-  // sum_n G B; group 0 then writes du (and accumulates dD), group 1 adds the
-  // slices of sum_n A G a h as well and writes ddelta (and accumulates
-  // dbias).  One store each, so every path has the same memory-operation
-  // count; the split evens out the work of the two groups between the
-  // barriers (group 0 also runs the softplus in phase A, group 1 the gate).
+  // sum_n G B; group 0 then writes du (and accumulates dD), group 1 writes
+  // dz, adds the slices of sum_n A G a h as well and writes ddelta (and
+  // accumulates dbias).  Two stores each (group 0 writes du as two halves),
+  // so every path has the same memory-operation count; the split evens out
+  // the work of the two groups between the barriers (group 0 also runs the
+  // softplus in phase A, group 1 the gate).
   // Waves w and w + 4 share a SIMD, so an uneven split leaves each SIMD with
   // one wave to issue from.
   auto phase_c = [&](const int tile) {
     const int t0 = tile * kTileB;
     const int par = tile & 1;
     const int t = t0 + a_col;
+    // group 1 writes the dz it computed in phase A first
+    if (grp1) store4_nb<T, kAligned>(dzp + (rb + a_ch) * L, t, L, kHasZ && a_ok, dummy, dzo);
     float4 gb = sGB[0][a_q][a_sw];
 #pragma unroll
     for (int ww = 1; ww < kWaves; ++ww) {
@@ -425,7 +447,11 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         duo[j] = fmaf(Dv, dov[j], de[j] * gbv[j]);
         accD = fmaf(dov[j], uu[j], accD);  // dov is 0 at padded steps
       }
-      store4_nb<T, kAligned>(dup + (rb + a_ch) * L, t, L, a_ok, dummy, duo);
+      // as two stores, so both groups issue two in phase C
+      const float du0[4] = {duo[0], duo[1], 0.0f, 0.0f};
+      const float du1[4] = {duo[2], duo[3], 0.0f, 0.0f};
+      store2_nb<T, kAligned>(dup + (rb + a_ch) * L, t, L, a_ok, dummy, du0);
+      store2_nb<T, kAligned>(dup + (rb + a_ch) * L, t + 2, L, a_ok, dummy, du1);
     } else {
       float4 gd = sDD[0][a_q][a_sw];
 #pragma unroll
