@@ -42,6 +42,8 @@ from typing import Optional
 import torch
 
 __all__ = [
+    "EPS32",
+    "error_bound",
     "softplus",
     "softplus_grad",
     "valid_mask",
@@ -106,14 +108,24 @@ def _prep(u, delta, A, B, C, D, delta_bias, h_init, z, dtype, keep_graph=False):
 
 def scan_fwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
              length=None, padding_right=True, z=None, delta_softplus=True,
-             chunk: Optional[int] = CHUNK, dtype=torch.float64, keep_graph: bool = False):
+             chunk: Optional[int] = CHUNK, dtype=torch.float64, keep_graph: bool = False,
+             magnitude: bool = False):
     """Reference forward (differentiable by autograd when ``keep_graph``; the
     inputs are detached otherwise).  Returns a dict with
 
     * ``out``   (B,D,L) pre-gate output D*u + sum_n C*h,
     * ``y``     (B,D,L) out * silu(z) (== out without z),
     * ``h_last``(B,D,N) state after the last position,
-    * ``h_chunks`` (B,D,nchunks,N) state at the end of each ``chunk`` steps.
+    * ``h_chunks`` (B,D,nchunks,N) state at the end of each ``chunk`` steps,
+    * ``prod_a`` (B,D,nchunks,N) product of the decays a_t from t = 0 to the
+      end of each chunk (the first half of the reference's (prod a, h) chunk
+      carry, ``forward_kernel.cu:225-228``).
+
+    With ``magnitude`` every signed factor is replaced by its absolute value
+    (the decays a = exp(delta*A) are positive and stay as they are), so each
+    output becomes the sum of the absolute values of the terms that make it
+    up: the scale of the rounding error of any evaluation of the same sums
+    (see ``error_bound``).
     """
     u, delta, A, B, C, D, delta_bias, h_init, z = _prep(
         u, delta, A, B, C, D, delta_bias, h_init, z, dtype, keep_graph)
@@ -123,7 +135,14 @@ def scan_fwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
     dt = softplus(x) if delta_softplus else x
     mask = valid_mask(batch, seqlen, length, padding_right)[:, None, :]
     dt = torch.where(mask, dt, torch.zeros_like(dt))
-    dtu = dt * u
+    gate = _silu(z) if z is not None else None
+    if magnitude:
+        u, B, C, D = u.abs(), B.abs(), C.abs(), D.abs()
+        h_init = None if h_init is None else h_init.abs()
+        gate = None if gate is None else gate.abs()
+    dtu = (dt.abs() if magnitude else dt) * u
+    dtsum = torch.zeros(batch, dim, dtype=dtype)
+    prods = []
     h = torch.zeros(batch, dim, nstate, dtype=dtype) if h_init is None else h_init.clone()
     out = torch.empty(batch, dim, seqlen, dtype=dtype)
     chunks = []
@@ -132,25 +151,32 @@ def scan_fwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
         b = dtu[:, :, t, None] * B[:, None, :, t]
         h = a * h + b
         out[:, :, t] = torch.einsum("bdn,bn->bd", h, C[:, :, t])
+        dtsum = dtsum + dt[:, :, t]
         if chunk and ((t + 1) % chunk == 0 or t == seqlen - 1):
             chunks.append(h.clone())
+            prods.append(torch.exp(dtsum[:, :, None] * A[None]))
     out = out + D[None, :, None] * u
-    y = out * _silu(z) if z is not None else out
+    y = out * gate if gate is not None else out
     res = {"out": out, "y": y, "h_last": h}
     if chunk:
-        res["h_chunks"] = (torch.stack(chunks, dim=2) if chunks
-                           else torch.zeros(batch, dim, 0, nstate, dtype=dtype))
+        empty = torch.zeros(batch, dim, 0, nstate, dtype=dtype)
+        res["h_chunks"] = torch.stack(chunks, dim=2) if chunks else empty
+        res["prod_a"] = torch.stack(prods, dim=2) if prods else empty
     return res
 
 
 def scan_bwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
              length=None, padding_right=True, z=None, delta_softplus=True,
-             dy=None, dh_last=None, seg: int = 64, dtype=torch.float64):
+             dy=None, dh_last=None, seg: int = 64, dtype=torch.float64,
+             magnitude: bool = False):
     """Reference backward by an explicit reverse loop with state checkpoints
     every ``seg`` steps (memory O(B*D*N*(L/seg + seg))).
 
     Returns a dict with du, ddelta, dA, dB, dC, dD, ddelta_bias, dh_init
-    (None without h_init) and dz (None without z).
+    (None without h_init) and dz (None without z).  ``magnitude``: as for
+    ``scan_fwd``, each result becomes the sum of the absolute values of its
+    terms (A enters the dA / ddelta terms by its absolute value, the decays
+    exp(delta*A) unchanged).
     """
     u, delta, A, B, C, D, delta_bias, h_init, z = _prep(
         u, delta, A, B, C, D, delta_bias, h_init, z, dtype)
@@ -165,9 +191,22 @@ def scan_bwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
     dsp = softplus_grad(x) if delta_softplus else torch.ones_like(x)
     mask = valid_mask(batch, seqlen, length, padding_right)[:, None, :]
     dt = torch.where(mask, dt_raw, torch.zeros_like(dt_raw))
-    dtu = dt * u
+    gate = _silu(z) if z is not None else None
+    gate_grad = _silu_grad(z) if z is not None else None
+    Aterm = A
+    if magnitude:
+        u, B, C, D, dy, dh_last = u.abs(), B.abs(), C.abs(), D.abs(), dy.abs(), dh_last.abs()
+        h_init = None if h_init is None else h_init.abs()
+        gate = None if gate is None else gate.abs()
+        if z is not None:  # silu'(z) = s (1 + z (1 - s)) by the sizes of its terms
+            sz = torch.sigmoid(z)
+            gate_grad = sz * (1.0 + z.abs() * (1.0 - sz))
+        Aterm = A.abs()
+        dsp = dsp.abs()
+    dtf = dt.abs() if magnitude else dt  # the step size as a factor (decays keep dt)
+    dtu = dtf * u
     dy = torch.where(mask, dy, torch.zeros_like(dy))
-    dout = dy * _silu(z) if z is not None else dy
+    dout = dy * gate if z is not None else dy
 
     # forward checkpoints: state before each segment
     h = torch.zeros(batch, dim, nstate, dtype=dtype) if h_init is None else h_init.clone()
@@ -201,9 +240,9 @@ def scan_bwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
             G = gam + dout[:, :, t, None] * Ct
             gB = (G * Bt).sum(-1)
             gah = G * a * h_prev
-            du[:, :, t] = D[None, :] * dout[:, :, t] + dt[:, :, t] * gB
-            dd[:, :, t] = u[:, :, t] * gB + (gah * A[None]).sum(-1)
-            dA += (gah * dt[:, :, t, None]).sum(0)
+            du[:, :, t] = D[None, :] * dout[:, :, t] + dtf[:, :, t] * gB
+            dd[:, :, t] = u[:, :, t] * gB + (gah * Aterm[None]).sum(-1)
+            dA += (gah * dtf[:, :, t, None]).sum(0)
             dB[:, :, t] = (G * dtu[:, :, t, None]).sum(1)
             dC[:, :, t] = (dout[:, :, t, None] * h_t).sum(1)
             gam = a * G
@@ -221,16 +260,17 @@ def scan_bwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
     }
     if z is not None:
         out_pre = out_pre + D[None, :, None] * u
-        res["dz"] = dy * out_pre * _silu_grad(z)
+        res["dz"] = dy * out_pre * gate_grad
     return res
 
 
 def update(state, x, dt, A, B, C, D=None, dt_bias=None, z=None,
-           dt_softplus=True, dtype=torch.float64):
+           dt_softplus=True, dtype=torch.float64, magnitude: bool = False):
     """Single decode step (``selective_update/kernel.cu:39-71``):
     delta = softplus(dt + bias); h' = exp(delta*A)*h + delta*x*B;
     out = D*x + sum_n C*h' (then * silu(z) when z is given).  Returns
-    (out, new_state); ``state`` is not modified."""
+    (out, new_state); ``state`` is not modified.  ``magnitude``: as for
+    ``scan_fwd`` (sums of the absolute values of the terms)."""
     cv = lambda t: None if t is None else t.detach().to("cpu", dtype)
     state, x, dt, A, B, C, D, dt_bias, z = map(cv, (state, x, dt, A, B, C, D, dt_bias, z))
     batch, dim = x.shape
@@ -241,11 +281,37 @@ def update(state, x, dt, A, B, C, D=None, dt_bias=None, z=None,
     v = dt + dt_bias[None, :]
     delta = softplus(v) if dt_softplus else v
     a = torch.exp(delta[:, :, None] * A[None])
+    gate = _silu(z) if z is not None else None
+    if magnitude:
+        state, x, B, C, D, delta = state.abs(), x.abs(), B.abs(), C.abs(), D.abs(), delta.abs()
+        gate = None if gate is None else gate.abs()
     new = a * state + (delta * x)[:, :, None] * B[:, None, :]
     out = torch.einsum("bdn,bn->bd", new, C) + D[None, :] * x
-    if z is not None:
-        out = out * _silu(z)
+    if gate is not None:
+        out = out * gate
     return out, new
+
+
+# Unit roundoff of float32 (round to nearest).
+EPS32 = 2.0 ** -24
+
+
+def error_bound(ref: torch.Tensor, mag: Optional[torch.Tensor], rtol: float, atol: float,
+                c: float) -> torch.Tensor:
+    """Per-element tolerance for a float32 evaluation of a result whose
+    float64 value is ``ref`` and whose terms have absolute values summing to
+    ``mag`` (the ``magnitude`` mode of this module):
+    atol + rtol * |ref| + c * EPS32 * mag.  The last term is the classical
+    bound on the rounding error of a sum (or recurrence) of terms evaluated in
+    float32, (number of roundings along the longest chain) * u * sum |terms|
+    (Higham, "Accuracy and Stability of Numerical Algorithms", 2nd ed., §4.2),
+    with c standing for that chain length; it matters only where the terms
+    cancel, so that |ref| is small against their sizes."""
+    r = ref.detach().double().cpu()
+    b = atol + rtol * r.abs()
+    if mag is not None:
+        b = b + c * EPS32 * mag.detach().double().cpu()
+    return b
 
 
 def algorithmic_bytes_scan(batch, dim, seqlen, nstate, s_in, s_bc, has_z):

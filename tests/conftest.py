@@ -27,3 +27,14 @@ def cuda():
         pytest.skip("no GPU")
     import torch
     return torch.device("cuda:0")
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Parity margins of every GPU-vs-oracle comparison, per tensor."""
+    try:
+        from tests.helpers import MARGINS, margin_summary
+    except Exception:
+        return
+    if MARGINS:
+        terminalreporter.write_sep("-", "parity margins (err / bound, 1.0 = at the tolerance)")
+        terminalreporter.write_line(margin_summary())

@@ -24,6 +24,20 @@ def _ref(x, w, b, silu):
     return F.silu(pre) if silu else pre
 
 
+def _wgrad_magnitude(x, w, b, dy, silu):
+    """Sums of |terms| of the weight and bias gradients (float64): dweight[c, j]
+    = sum_{b,t} dpre * x[t - (k-1) + j] and dbias = sum dpre, dpre = dy *
+    act'(pre), taken by their absolute values (the error-bound scale)."""
+    xd, wd = x.double(), w.double()
+    bd = None if b is None else b.double()
+    pre = LR.causal_conv(xd, wd, bd).requires_grad_(True)
+    (F.silu(pre) if silu else pre).backward(dy.double())
+    dpre = pre.grad.abs()
+    wl = wd.clone().requires_grad_(True)
+    LR.causal_conv(xd.abs(), wl, None).backward(dpre)
+    return wl.grad, dpre.sum((0, 2))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("seqlen", [1, 3, 37, 64, 2048, 2056])
 @pytest.mark.parametrize("width", [1, 2, 4, 8])
@@ -80,8 +94,9 @@ def test_backward(cuda, dtype, seqlen, width):
     _ref(xr, wr, br, True).backward(dy.double())
     assert_close(xg.grad, xr.grad, dtype, "dx")
     # weight / bias gradients are sums over batch x seqlen terms
-    assert_close(wg.grad, wr.grad, dtype, "dweight", scale_atol=True)
-    assert_close(bg.grad, br.grad, dtype, "dbias", scale_atol=True)
+    mw, mb = _wgrad_magnitude(x, w, b, dy, True)
+    assert_close(wg.grad, wr.grad, dtype, "dweight", mw)
+    assert_close(bg.grad, br.grad, dtype, "dbias", mb)
 
 
 def test_backward_without_bias_or_activation(cuda):
@@ -93,7 +108,8 @@ def test_backward_without_bias_or_activation(cuda):
     xr, wr = x.double().requires_grad_(True), w.double().requires_grad_(True)
     _ref(xr, wr, None, False).backward(dy.double())
     assert_close(xg.grad, xr.grad, torch.float32, "dx")
-    assert_close(wg.grad, wr.grad, torch.float32, "dweight", scale_atol=True)
+    mw, _ = _wgrad_magnitude(x, w, None, dy, False)
+    assert_close(wg.grad, wr.grad, torch.float32, "dweight", mw)
 
 
 def test_deterministic_and_rejects_bad_width(cuda):

@@ -294,3 +294,87 @@ def test_byte_formulas_match_baseline_table():
     f3, b3 = R.algorithmic_bytes_scan(1, 2560, 16384, 16, 4, 4, True)
     assert (f3, b3) == (673_533_952, 1_179_131_904)
     assert R.algorithmic_bytes_update(64, 5120, 16, 2, 2, True) == 44_937_216
+
+
+def test_prod_a_is_the_running_product_of_decays():
+    """prod_a (the first half of the reference's (prod a, h) chunk carry) is the
+    product of exp(delta_t A) from t = 0 to each chunk end, padded steps
+    counting as 1: checked against a scalar product loop, and through the
+    B = 0 closed form h_t = (prod a) h_init."""
+    c = rand_case(batch=2, dim=3, seqlen=37, nstate=4, seed=21)
+    length = torch.tensor([29, 11])
+    for pr in (True, False):
+        res = R.scan_fwd(**c, length=length, padding_right=pr, chunk=16)
+        pa = res["prod_a"]
+        assert pa.shape == (2, 3, 3, 4)
+        for b in range(2):
+            ln = int(length[b])
+            for d in range(3):
+                for n in range(4):
+                    p = 1.0
+                    ends = {15: 0, 31: 1, 36: 2}
+                    for t in range(37):
+                        valid = (t < ln) if pr else (t >= 37 - ln)
+                        if valid:
+                            x = float(c["delta"][b, d, t] + c["delta_bias"][d])
+                            x = x if x > 20 else math.log1p(math.exp(x))
+                            p *= math.exp(x * float(c["A"][d, n]))
+                        if t in ends:
+                            assert abs(p - float(pa[b, d, ends[t], n])) <= 1e-12 * max(1.0, p)
+        zb = {**c, "B": torch.zeros_like(c["B"])}
+        r0 = R.scan_fwd(**zb, length=length, padding_right=pr, chunk=16)
+        torch.testing.assert_close(r0["h_chunks"], r0["prod_a"] * c["h_init"][:, :, None, :])
+
+
+def test_magnitude_mode_bounds_and_equals_for_nonnegative_terms():
+    """magnitude=True gives sums of |terms|: it bounds |value| everywhere, and it
+    equals the value when every term is already non-negative (u, B, C, D,
+    h_init, dy, dh_last >= 0, no gate; for the backward also A's sign flipped
+    inside the dA / ddelta terms, which the magnitude takes as |A|)."""
+    c = rand_case(batch=2, dim=3, seqlen=23, nstate=4, seed=22)
+    g = torch.Generator().manual_seed(23)
+    dy = torch.randn(2, 3, 23, generator=g, dtype=torch.float64)
+    dl = torch.randn(2, 3, 4, generator=g, dtype=torch.float64)
+    v = R.scan_fwd(**c)
+    m = R.scan_fwd(**c, magnitude=True)
+    for k in ("y", "out", "h_chunks", "h_last"):
+        assert bool((m[k] >= v[k].abs() * (1 - 1e-12)).all()), k
+    vb = R.scan_bwd(**c, dy=dy, dh_last=dl)
+    mb = R.scan_bwd(**c, dy=dy, dh_last=dl, magnitude=True)
+    for k, x in vb.items():
+        if x is not None:
+            assert bool((mb[k] >= x.abs() * (1 - 1e-12)).all()), k
+    pos = {k: (None if x is None else (x.abs() if k in ("u", "B", "C", "D", "h_init") else x))
+           for k, x in c.items()}
+    pos["z"] = None
+    vp, mp = R.scan_fwd(**pos), R.scan_fwd(**pos, magnitude=True)
+    for k in ("y", "h_chunks"):
+        torch.testing.assert_close(mp[k], vp[k], rtol=1e-12, atol=0)
+    # backward, nonnegative terms: dB, dC, du, dD are sums of products of
+    # non-negative factors (the decays keep their sign)
+    vbp = R.scan_bwd(**pos, dy=dy.abs(), dh_last=dl.abs())
+    mbp = R.scan_bwd(**pos, dy=dy.abs(), dh_last=dl.abs(), magnitude=True)
+    for k in ("du", "dB", "dC", "dD", "dh_init"):
+        torch.testing.assert_close(mbp[k], vbp[k], rtol=1e-12, atol=0)
+
+
+def test_error_bound_admits_float32_and_rejects_a_planted_mistake():
+    """The float32 oracle stays within error_bound (rtol 1e-4, atol 1e-5, c = 64)
+    of the float64 one on every output; a dropped term (the dh_last carry)
+    does not."""
+    c = R.make_inputs(2, 16, 300, 16, seed=24, with_z=True, h_init=True)
+    g = torch.Generator().manual_seed(25)
+    dy = torch.randn(2, 16, 300, generator=g)
+    dl = torch.randn(2, 16, 16, generator=g)
+    args = (c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["delta_bias"], c["h_init"])
+    r64 = R.scan_bwd(*args, z=c["z"], dy=dy, dh_last=dl)
+    r32 = R.scan_bwd(*args, z=c["z"], dy=dy, dh_last=dl, dtype=torch.float32)
+    mag = R.scan_bwd(*args, z=c["z"], dy=dy, dh_last=dl, magnitude=True)
+    for k, v in r64.items():
+        if v is None:
+            continue
+        bnd = R.error_bound(v, mag[k], 1e-4, 1e-5, 64.0)
+        assert bool(((r32[k].double() - v).abs() <= bnd).all()), k
+    bad = R.scan_bwd(*args, z=c["z"], dy=dy, dh_last=None)
+    bnd = R.error_bound(r64["dh_init"], mag["dh_init"], 1e-4, 1e-5, 64.0)
+    assert not bool(((bad["dh_init"] - r64["dh_init"]).abs() <= bnd).all())
