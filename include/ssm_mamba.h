@@ -106,8 +106,11 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
  * when non-NULL dD, ddelta_bias and dh_init (requires h_init).  With z,
  * out_ungated (the forward's ungated output) and dz are required; without z
  * both must be NULL.
- * nstate <= 64.  workspace: ssm_scan_bwd_workspace_bytes() bytes.  The result
- * is deterministic (fixed-order reductions, no atomics on global memory).
+ * nstate <= 256, as the reference's backward dispatch (csrc/static_switch.h:
+ * 15-37, csrc/selective_scan/backward_kernel.cu:456-478); past 64 states the
+ * kernels run in chunks of 64 states.  workspace: ssm_scan_bwd_workspace_bytes()
+ * bytes.  The result is deterministic (fixed-order reductions, no atomics on
+ * global memory).
  */
 int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
                            const void* u, const void* delta, const float* A, const void* B,

@@ -106,6 +106,13 @@ bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr
 
 size_t round256(size_t bytes) { return (bytes + 255) & ~(size_t)255; }
 
+// state chunks of the backward past ssm::kBwdChunkStates states (0: one pass)
+size_t bwd_chunks(int64_t nstate) {
+  return nstate > ssm::kBwdChunkStates
+             ? (size_t)((nstate + ssm::kBwdChunkStates - 1) / ssm::kBwdChunkStates)
+             : 0;
+}
+
 int check_common(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
                  int max_nstate) {
   if (dtype != SSM_F32 && dtype != SSM_BF16)
@@ -266,6 +273,7 @@ size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, 
          2 * round256(rows * dim * sizeof(float)) +
          round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) *
                   sizeof(float)) +
+         2 * round256(bwd_chunks(nstate) * batch * dim * seqlen * sizeof(float)) +
          ssm::kDummyBytes;
 }
 
@@ -322,7 +330,7 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                            float* dh_init, void* dz, void* workspace, size_t workspace_bytes,
                            void* stream) {
   g_err.clear();
-  if (int e = check_common(batch, dim, seqlen, nstate, dtype, 64)) return e;
+  if (int e = check_common(batch, dim, seqlen, nstate, dtype, 256)) return e;
   if (!u || !delta || !A || !B || !C || !h_chunks || !dout || !du || !ddelta || !dA || !dB || !dC)
     return fail(SSM_ERR_INVALID,
                 "u, delta, A, B, C, h_chunks, dout, du, ddelta, dA, dB and dC must be non-NULL");
@@ -371,6 +379,11 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   p.seg_h = reinterpret_cast<float*>(ws);
   p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * batch * nstate * dim;
   ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));
+  p.nsc = (int)bwd_chunks(nstate);
+  const size_t part_bytes = round256(p.nsc * (size_t)batch * dim * seqlen * sizeof(float));
+  p.ws_gb = p.nsc ? reinterpret_cast<float*>(ws) : nullptr;
+  p.ws_gd = p.nsc ? reinterpret_cast<float*>(ws + part_bytes) : nullptr;
+  ws += 2 * part_bytes;
   p.dummy = ws;
   const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out_ungated, dout, du, ddelta, dz});
   return hip_status(ssm::launch_scan_bwd(p, dtype, aligned, bc, static_cast<hipStream_t>(stream)),

@@ -142,7 +142,14 @@ __device__ __forceinline__ void store2_nb(T* __restrict__ row, int t, int L, boo
   }
 }
 
-template <typename T, int kSG, bool kHasZ, bool kAligned>
+//
+// kPart (state counts past 64): the workgroup covers the 64 states of state
+// chunk sc = blockIdx.z / nseg (blockIdx.z % nseg is the segment) and writes
+// its per-position sums over those states, sum_n G B and sum_n A G a h, as
+// fp32 partials (ws_gb, ws_gd: (nsc, batch, dim, seqlen)); du, ddelta, dD
+// and dbias then come from scan_bwd_combine_kernel, which adds the chunks'
+// partials in a fixed order.  dz (state-independent) is written by chunk 0.
+template <typename T, int kSG, bool kHasZ, bool kAligned, bool kPart>
 __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
     const float* __restrict__ Ap, const T* __restrict__ Bp, const T* __restrict__ Cp,
@@ -153,7 +160,8 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const float* __restrict__ dh_last, T* __restrict__ dup, T* __restrict__ ddp,
     T* __restrict__ dzp, float* __restrict__ dh_init, float* __restrict__ ws_bc,
     float* __restrict__ ws_A, float* __restrict__ ws_D, float* __restrict__ ws_bias,
-    void* __restrict__ dummy, const float* __restrict__ seg_g, const float* __restrict__ seg_dt) {
+    void* __restrict__ dummy, const float* __restrict__ seg_g, const float* __restrict__ seg_dt,
+    float* __restrict__ ws_gb, float* __restrict__ ws_gd) {
   using R4 = typename Raw4<T>::type;
   constexpr int kT4 = kTileB / 4;         // 4-step columns per tile (4)
   constexpr int kItems = kBlockCh * kT4;  // (row, column) items per tile (256)
@@ -182,8 +190,11 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   const int blk = blockIdx.x;
   const int d0 = blk * kBlockCh;
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
-  // sequence split: this workgroup's tiles [tile_beg, tile_end) of segment seg
-  const int seg = blockIdx.z;
+  // sequence split: this workgroup's tiles [tile_beg, tile_end) of segment
+  // seg; state chunk sc (kPart) covers states n0 .. n0 + 2 * kWaves * kSG - 1
+  const int seg = kPart ? (int)blockIdx.z % p.nseg : (int)blockIdx.z;
+  const int sc = kPart ? (int)blockIdx.z / p.nseg : 0;
+  const int n0 = sc * (2 * kWaves * kSG);
   const int ntiles = (L + kTileB - 1) / kTileB;
   const int tile_beg = seg * (p.seg_len / kTileB);
   const int tile_end = min(ntiles, tile_beg + p.seg_len / kTileB);
@@ -207,7 +218,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   for (int g = 0; g < kSG; ++g)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int n = (g * kWaves + w) * 2 + s;
+      const int n = n0 + (g * kWaves + w) * 2 + s;
       const bool ok = ch_ok && n < N;
       dA[g][s] = 0.0f;
       Av[g][s] = ok ? Ap[(size_t)ch * N + n] : 0.0f;
@@ -271,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       // element e = (B|C, state, step) of the tile, clamped into the rows
       // (states past N are zeroed in phase A, steps past L meet delta = 0)
       const int e = g * kThreads + tid;
-      const int n = min((e / kTileB) % kBCStates, N - 1);
+      const int n = min(n0 + (e / kTileB) % kBCStates, N - 1);
       const int t = min(tile * kTileB + e % kTileB, L - 1);
       bcn[g] = Elem<T>::load1((e / (kTileB * kBCStates) ? Craw : Braw) + (size_t)n * L + t);
     }
@@ -279,7 +290,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     for (int g = 0; g < kSG; ++g)
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int nc = min((g * kWaves + w) * 2 + s, N - 1);
+        const int nc = min(n0 + (g * kWaves + w) * 2 + s, N - 1);
         const float* src = tile > 0
             ? h_chunks + (((size_t)b * p.nchunks + (tile - 1)) * N + nc) * Dm + chc
             : (h_init ? h_init + (rb + chc) * N + nc : h_chunks);
@@ -337,13 +348,13 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     for (int g = 0; g < kSG; ++g) {
       const int e = g * kThreads + tid;
       const int j = e % kTileB, n = (e / kTileB) % kBCStates, kind = e / (kTileB * kBCStates);
-      sBlk[n >> 1][j >> 2][(j & 3) * 4 + (n & 1) * 2 + kind] = n < N ? bcn[g] : 0.0f;
+      sBlk[n >> 1][j >> 2][(j & 3) * 4 + (n & 1) * 2 + kind] = n0 + n < N ? bcn[g] : 0.0f;
     }
 #pragma unroll
     for (int g = 0; g < kSG; ++g)
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int n = (g * kWaves + w) * 2 + s;
+        const int n = n0 + (g * kWaves + w) * 2 + s;
         hc[g][s] = (ch_ok && n < N && (tile > 0 || h_init)) ? hcn[g][s] : 0.0f;
       }
   };
@@ -355,7 +366,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
 #pragma unroll
     for (int g = 0; g < kSG; ++g) {
       const int G = g * kWaves + w;
-      if (g > 0 && G >= ngroups) {  // wave-uniform (pair 0..7 always runs: zero B/C)
+      if (g > 0 && n0 / 2 + G >= ngroups) {  // wave-uniform (pairs n0/2 + 0..7 always run: zero B/C)
         continue;
       }
       float a[2][kChunk], H[2][kChunk];
@@ -381,7 +392,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       // 16 (kind = dB/dC, state, step); quads hold the same value
       const int vi = lane >> 2;
       const int rkind = vi >> 3, rs = (vi >> 2) & 1, rj = vi & 3;
-      const int rn = G * 2 + rs;
+      const int rn = n0 + G * 2 + rs;
       float* const wsb = ws_bc + ((size_t)rkind * p.nblk + blk) * nBC + ((size_t)b * N + rn) * L;
       auto rev = [&](int jq, const StepVals& sv) {
         float gB[4], gD[4], vals[16];
@@ -427,7 +438,21 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     const int par = tile & 1;
     const int t = t0 + a_col;
     // group 1 writes the dz it computed in phase A first
-    if (grp1) store4_nb<T, kAligned>(dzp + (rb + a_ch) * L, t, L, kHasZ && a_ok, dummy, dzo);
+    if (grp1) store4_nb<T, kAligned>(dzp + (rb + a_ch) * L, t, L, kHasZ && a_ok && sc == 0, dummy,
+                                     dzo);
+    if constexpr (kPart) {
+      // the chunk's per-position sums over its states, fp32
+      float4 acc = grp1 ? sDD[0][a_q][a_sw] : sGB[0][a_q][a_sw];
+#pragma unroll
+      for (int ww = 1; ww < kWaves; ++ww) {
+        const float4 q1 = grp1 ? sDD[ww][a_q][a_sw] : sGB[ww][a_q][a_sw];
+        acc.x += q1.x; acc.y += q1.y; acc.z += q1.z; acc.w += q1.w;
+      }
+      const float av[4] = {acc.x, acc.y, acc.z, acc.w};
+      float* dst = (grp1 ? ws_gd : ws_gb) + (((size_t)sc * p.batch + b) * Dm + a_chc) * L;
+      store4_nb<float, kAligned>(dst, t, L, a_ok, dummy, av);
+      return;
+    }
     float4 gb = sGB[0][a_q][a_sw];
 #pragma unroll
     for (int ww = 1; ww < kWaves; ++ww) {
@@ -493,17 +518,90 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   for (int g = 0; g < kSG; ++g)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int n = (g * kWaves + w) * 2 + s;
+      const int n = n0 + (g * kWaves + w) * 2 + s;
       if (ch_ok && n < N) {
         ws_A[(srow * Dm + ch) * N + n] = dA[g][s];
         if (dh_init && seg == 0) dh_init[(rb + ch) * N + n] = gam[g][s];
       }
     }
   // the 4 items of a channel row are 4 consecutive lanes of a group: dD
-  // from group 0, dbias from group 1
-  {
+  // from group 0, dbias from group 1 (kPart: scan_bwd_combine_kernel)
+  if constexpr (!kPart) {
     const float sv = group_sum<kT4>(grp1 ? accB : accD);
     if (a_ok && a_q == 0) (grp1 ? ws_bias : ws_D)[srow * Dm + a_ch] = sv;
+  }
+}
+
+// ---------------------------------------------------------------- state chunks
+
+// After the kPart backward: per (batch row b, channel d), the per-position
+// gradients from the state chunks' sums (added in chunk order):
+//   gb = sum_n G B, gd = sum_n A G a h_{t-1};
+//   du = D * dout + delta * gb;  ddelta = softplus'(x) * (u * gb + gd);
+// with dout the masked (and gated) upstream gradient as in the main kernel,
+// and the row's dD = sum_t dout u and dbias = sum_t ddelta written as the
+// (segment 0, b) partial rows (the other segments' rows are zeroed).
+template <typename T, bool kHasZ>
+__global__ __launch_bounds__(256) void scan_bwd_combine_kernel(
+    const ScanDims p, const int nsc, const T* __restrict__ u, const T* __restrict__ dl,
+    const T* __restrict__ dyp, const T* __restrict__ zp, const float* __restrict__ Dp,
+    const float* __restrict__ biasp, const int64_t* __restrict__ length,
+    const float* __restrict__ ws_gb, const float* __restrict__ ws_gd, T* __restrict__ dup,
+    T* __restrict__ ddp, float* __restrict__ ws_D, float* __restrict__ ws_bias) {
+  __shared__ float red[2][256 / 64];
+  const int d = blockIdx.x, b = blockIdx.y;
+  const int L = p.seqlen, Dm = p.dim;
+  const size_t row = ((size_t)b * Dm + d) * L;
+  const size_t cstride = (size_t)p.batch * Dm * L;
+  int vlo, vhi;
+  valid_window(length, p.pad_right, b, L, vlo, vhi);
+  const float Dv = Dp ? Dp[d] : 0.0f;
+  const float Bias = biasp ? biasp[d] : 0.0f;
+  const bool softplus = p.softplus != 0;
+  float accD = 0.0f, accB = 0.0f;
+  for (int t = threadIdx.x; t < L; t += blockDim.x) {
+    const bool valid = t >= vlo && t < vhi;
+    const float uu = Elem<T>::load1(u + row + t);
+    const float x = Elem<T>::load1(dl + row + t) + Bias;
+    float dt = x, sg = 1.0f;
+    if (softplus) softplus_and_grad_t20(x, dt, sg);
+    float dout = valid ? Elem<T>::load1(dyp + row + t) : 0.0f;
+    if constexpr (kHasZ) {
+      const float zz = Elem<T>::load1(zp + row + t);
+      dout *= zz * sigmoidf_fast(zz);
+    }
+    float gb = 0.0f, gd = 0.0f;
+    for (int c = 0; c < nsc; ++c) {
+      gb += ws_gb[c * cstride + row + t];
+      gd += ws_gd[c * cstride + row + t];
+    }
+    const float de = valid ? dt : 0.0f;
+    const float du = fmaf(Dv, dout, de * gb);
+    const float dd = valid ? fmaf(uu, gb, gd) * sg : 0.0f;
+    accD = fmaf(dout, uu, accD);
+    accB += dd;
+    Elem<T>::store1(dup + row + t, du);
+    Elem<T>::store1(ddp + row + t, dd);
+  }
+  accD = group_sum<64>(accD);
+  accB = group_sum<64>(accB);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[0][w] = accD;
+    red[1][w] = accB;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sd = 0.0f, sb = 0.0f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) {
+      sd += red[0][i];
+      sb += red[1][i];
+    }
+    for (int s = 0; s < p.nseg; ++s) {
+      const size_t r = ((size_t)s * p.batch + b) * Dm + d;
+      ws_D[r] = s == 0 ? sd : 0.0f;
+      ws_bias[r] = s == 0 ? sb : 0.0f;
+    }
   }
 }
 
@@ -538,7 +636,10 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_segsum_kernel(
   const int w = wave_id_uniform();
   const int b = blockIdx.y;
   const int d0 = blockIdx.x * kBlockCh;
-  const int seg = blockIdx.z + 1;
+  // blockIdx.z = (state chunk sc) * (nseg - 1) + segment - 1; sc > 0 only
+  // for the state chunks of the kPart backward (states n0 .. n0 + 63)
+  const int seg = (int)blockIdx.z % (p.nseg - 1) + 1;
+  const int n0 = (int)blockIdx.z / (p.nseg - 1) * (2 * kWaves * kSG);
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
   const int Tbeg = seg * p.seg_len;
   const int Lend = min(L, Tbeg + p.seg_len);
@@ -555,7 +656,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_segsum_kernel(
   for (int g = 0; g < kSG; ++g)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int n = (g * kWaves + w) * 2 + s;
+      const int n = n0 + (g * kWaves + w) * 2 + s;
       A2[g][s] = (ch_ok && n < N) ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
       gam[g][s] = 0.0f;
     }
@@ -648,7 +749,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_segsum_kernel(
         const int tb = min(T0 + 4 * k, Lp - 4);
 #pragma unroll
         for (int g = 0; g < kSG; ++g) {
-          const int G = g * kWaves + w;
+          const int G = n0 / 2 + g * kWaves + w;
           if (G < npair) {
             const float4* __restrict__ q = bc4 + ((size_t)b * npair + G) * Lp + tb;
 #pragma unroll
@@ -670,13 +771,13 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_segsum_kernel(
     for (int g = 0; g < kSG; ++g)
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int n = (g * kWaves + w) * 2 + s;
+        const int n = n0 + (g * kWaves + w) * 2 + s;
         if (n < N) seg_g[(sb * N + n) * Dm + ch] = gam[g][s];
       }
   }
 #pragma unroll
   for (int m = 1; m < kT4; m <<= 1) dtsum += __shfl_xor(dtsum, m, 64);
-  if (a_q == 0 && a_ok) seg_dt[sb * Dm + a_ch] = dtsum;
+  if (a_q == 0 && a_ok && n0 == 0) seg_dt[sb * Dm + a_ch] = dtsum;
 }
 
 // Adds the partial sums: dB/dC over channel blocks, dA/dD/dbias over the
@@ -745,36 +846,47 @@ __global__ __launch_bounds__(256) void scan_bwd_reduce_kernel(
 size_t bc_prep_floats(int batch, int nstate, int seqlen);
 hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t st);
 
-template <typename T, int kSG, bool kHasZ, bool kAligned>
+template <typename T, int kSG, bool kHasZ, bool kAligned, bool kPart>
 static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t st) {
+  const int nsc = kPart ? p.nsc : 1;
   if (p.nseg > 1) {
     ProfScope prof("scan_bwd_segsum", st);
     hipLaunchKernelGGL((scan_bwd_segsum_kernel<T, kSG, kHasZ, kAligned>),
-                       dim3(p.nblk, p.batch, p.nseg - 1), dim3(kThreads), 0, st, dims_of(p),
-                       (const T*)p.delta, (const T*)p.dout, (const T*)p.z, p.A, bc, p.bias,
-                       p.length, p.seg_h, p.seg_dt);
+                       dim3(p.nblk, p.batch, (p.nseg - 1) * nsc), dim3(kThreads), 0, st,
+                       dims_of(p), (const T*)p.delta, (const T*)p.dout, (const T*)p.z, p.A, bc,
+                       p.bias, p.length, p.seg_h, p.seg_dt);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  dim3 grid(p.nblk, p.batch, p.nseg);
-  ProfScope prof("scan_bwd", st);
-  hipLaunchKernelGGL((scan_bwd_kernel<T, kSG, kHasZ, kAligned>), grid, dim3(kThreads), 0, st,
-                     dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, (const T*)p.B,
-                     (const T*)p.C, p.D, p.bias,
-                     p.h_init, p.length, (const T*)p.z, (const T*)p.out_ungated, p.h_chunks_in,
-                     (const T*)p.dout,
-                     p.dh_last, (T*)p.du, (T*)p.ddelta, (T*)p.dz, p.dh_init, p.ws_bc, p.ws_A,
-                     p.ws_D, p.ws_bias, p.dummy, p.seg_h, p.seg_dt);
+  dim3 grid(p.nblk, p.batch, p.nseg * nsc);
+  {
+    ProfScope prof("scan_bwd", st);
+    hipLaunchKernelGGL((scan_bwd_kernel<T, kSG, kHasZ, kAligned, kPart>), grid, dim3(kThreads), 0,
+                       st, dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, (const T*)p.B,
+                       (const T*)p.C, p.D, p.bias, p.h_init, p.length, (const T*)p.z,
+                       (const T*)p.out_ungated, p.h_chunks_in, (const T*)p.dout, p.dh_last,
+                       (T*)p.du, (T*)p.ddelta, (T*)p.dz, p.dh_init, p.ws_bc, p.ws_A, p.ws_D,
+                       p.ws_bias, p.dummy, p.seg_h, p.seg_dt, p.ws_gb, p.ws_gd);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if constexpr (kPart) {
+    ProfScope prof("scan_bwd_combine", st);
+    hipLaunchKernelGGL((scan_bwd_combine_kernel<T, kHasZ>), dim3(p.dim, p.batch), dim3(256), 0,
+                       st, dims_of(p), p.nsc, (const T*)p.u, (const T*)p.delta, (const T*)p.dout,
+                       (const T*)p.z, p.D, p.bias, p.length, p.ws_gb, p.ws_gd, (T*)p.du,
+                       (T*)p.ddelta, p.ws_D, p.ws_bias);
+  }
   return hipGetLastError();
 }
 
-template <typename T, int kSG>
+template <typename T, int kSG, bool kPart = false>
 static hipError_t launch_bwd3(const ScanParams& p, const float* bc, bool aligned, hipStream_t st) {
   if (p.z)
-    return aligned ? launch_bwd4<T, kSG, true, true>(p, bc, st)
-                   : launch_bwd4<T, kSG, true, false>(p, bc, st);
-  return aligned ? launch_bwd4<T, kSG, false, true>(p, bc, st)
-                 : launch_bwd4<T, kSG, false, false>(p, bc, st);
+    return aligned ? launch_bwd4<T, kSG, true, true, kPart>(p, bc, st)
+                   : launch_bwd4<T, kSG, true, false, kPart>(p, bc, st);
+  return aligned ? launch_bwd4<T, kSG, false, true, kPart>(p, bc, st)
+                 : launch_bwd4<T, kSG, false, false, kPart>(p, bc, st);
 }
 
 template <typename T>
@@ -782,7 +894,8 @@ static hipError_t launch_bwd2(const ScanParams& p, const float* bc, bool aligned
   hipError_t e;
   if (p.nstate <= 16) e = launch_bwd3<T, 1>(p, bc, aligned, st);
   else if (p.nstate <= 32) e = launch_bwd3<T, 2>(p, bc, aligned, st);
-  else e = launch_bwd3<T, 4>(p, bc, aligned, st);
+  else if (p.nstate <= kBwdChunkStates) e = launch_bwd3<T, 4>(p, bc, aligned, st);
+  else e = launch_bwd3<T, 4, true>(p, bc, aligned, st);
   if (e != hipSuccess) return e;
   const size_t nBC = (size_t)p.batch * p.nstate * p.seqlen;
   const uintptr_t vec_align = 4 * sizeof(T);
@@ -803,7 +916,7 @@ static hipError_t launch_bwd2(const ScanParams& p, const float* bc, bool aligned
 }
 
 // bc must hold bc_prep_floats() floats; ws_* are laid out by the caller.
-// nstate <= 64.
+// nstate <= 256 (past 64: p.nsc chunks with p.ws_gb / p.ws_gd).
 hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* bc,
                            hipStream_t st) {
   if (p.nseg > 1) {  // only the segment summaries read the prepped layout

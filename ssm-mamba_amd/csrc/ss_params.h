@@ -89,7 +89,17 @@ struct ScanParams {
   int seg_len, nseg, sub_k;
   float* seg_h;
   float* seg_dt;
+
+  // backward past 64 states: nsc chunks of 64 states, each leaving its
+  // per-position sums over its states, (nsc, batch, dim, seqlen) fp32
+  int nsc;
+  float* ws_gb;  // sum_n G B
+  float* ws_gd;  // sum_n A G a h_{t-1}
 };
+
+// states per backward workgroup (8 waves x 4 pairs); larger counts run in
+// chunks of this many
+constexpr int kBwdChunkStates = 64;
 
 constexpr size_t kDummyBytes = 256;
 

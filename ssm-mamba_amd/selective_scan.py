@@ -199,8 +199,6 @@ def backward(u: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
     if out_ungated is not None:
         _check(out_ungated, "out_ungated", (batch, dim, seqlen), "batch_size, num_channels, seq_len",
                (u.dtype,), str(u.dtype).replace("torch.", "") + " (the dtype of u)")
-    if nstate > 64:
-        raise RuntimeError("selective_scan backward only supports state_dim <= 64")
     _check_dim(h, 4, "h")
     _check(h, "h", (batch, nchunks(seqlen), nstate, dim),
            "batch_size, num_chunks, state_dim, num_channels", (torch.float32,), "float32")

@@ -59,9 +59,14 @@ def test_invalid_arguments_return_errors():
                                     *([None] * 4), 1, None, 1, None, None, None, None, None, 0,
                                     None)
     assert rc == 1 and b"non-NULL" in lib.ssm_last_error()
-    rc = lib.ssm_selective_scan_bwd(1, 1, 1, 65, 0, *([None] * 5), 0, *([None] * 4), 1, None, None, 1, None, None,
+    rc = lib.ssm_selective_scan_bwd(1, 1, 1, 257, 0, *([None] * 5), 0, *([None] * 4), 1, None, None, 1, None, None,
                                     None, *([None] * 9), None, 0, None)
-    assert rc == 2 and b"state_dim <= 64" in lib.ssm_last_error()
+    assert rc == 2 and b"state_dim <= 256" in lib.ssm_last_error()
+    # past 64 states the backward runs in chunks: its workspace holds the
+    # chunks' per-position sums (2 x chunks x batch x dim x seqlen fp32)
+    w64 = lib.ssm_scan_bwd_workspace_bytes(2, 64, 80, 64)
+    w65 = lib.ssm_scan_bwd_workspace_bytes(2, 64, 80, 65)
+    assert w65 - w64 >= 2 * 2 * 2 * 64 * 80 * 4
     rc = lib.ssm_selective_state_update(1, 1, 16, 0, *([None] * 10), 1, None, None)
     assert rc == 1 and b"non-NULL" in lib.ssm_last_error()
 
