@@ -18,7 +18,13 @@
  * ddelta_bias (dim); h_init/h_last/dh_last/dh_init (batch, dim, nstate);
  * h_chunks (batch, ssm_scan_nchunks(seqlen), nstate, dim): the state after
  * each SSM_CHUNK steps, channel-contiguous (h_chunks[:, -1] transposed is the
- * final state); length (batch) int64.
+ * final state); or, with h_pairs = 1, (batch, ssm_scan_nchunks(seqlen),
+ * 2 * nstate, dim) holding for each state n the product of the decays
+ * exp(delta_t A) from step 0 to the chunk end in row 2n and the state in row
+ * 2n + 1 -- the reference's (prod a, h) chunk carry
+ * (csrc/selective_scan/forward_kernel.cu:225-228) with its
+ * (batch, dim, nchunks, 2 * nstate) index order as a strided view;
+ * length (batch) int64.
  */
 #ifndef SSM_MAMBA_H_
 #define SSM_MAMBA_H_
@@ -68,8 +74,9 @@ size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, 
  *   out      = (D*u + sum_n C*h) [* silu(z)]  with h_t = exp(delta_t*A) h_{t-1}
  *              + delta_t*u_t*B_t, delta = softplus(delta_raw + delta_bias)
  *              (no softplus when delta_softplus == 0)
- *   h_chunks = states after each SSM_CHUNK steps, or NULL (inference); then
- *              h_last (nullable) receives the final state.
+ *   h_chunks = states after each SSM_CHUNK steps (h_pairs = 1: with the
+ *              chunk decays, see above), or NULL (inference); then h_last
+ *              (nullable) receives the final state.
  *   out_ungated (nullable, requires z) = D*u + sum_n C*h, the output before
  *              the gate: the backward needs it for dz.  The reference gates
  *              outside the kernel (modules/mamba.py:182), where autograd
@@ -90,8 +97,8 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                            const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
                            const void* z, int delta_softplus, void* out, void* out_ungated,
-                           float* h_chunks, float* h_last, void* workspace, size_t workspace_bytes,
-                           void* stream);
+                           float* h_chunks, int h_pairs, float* h_last, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /*
  * Selective-scan backward.  Replaces selective_scan_backward
@@ -100,7 +107,8 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
  * (csrc/selective_scan/bindings.cpp:7).
  *
  * Inputs as for the forward (B and C with bc_batch_stride; dB and dC are
- * written contiguous) plus h_chunks (from the forward), dout (the
+ * written contiguous) plus h_chunks (from the forward, in the layout h_pairs
+ * names; only the states are read), dout (the
  * upstream gradient of out; ignored at padded positions) and dh_last
  * (nullable = zero).  Writes du, ddelta, dA, dB, dC (all overwritten), and
  * when non-NULL dD, ddelta_bias and dh_init (requires h_init).  With z,
@@ -118,10 +126,10 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                            const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
                            const void* z, const void* out_ungated, int delta_softplus,
-                           const float* h_chunks, const void* dout, const float* dh_last,
-                           void* du, void* ddelta, float* dA, void* dB, void* dC, float* dD,
-                           float* ddelta_bias, float* dh_init, void* dz, void* workspace,
-                           size_t workspace_bytes, void* stream);
+                           const float* h_chunks, int h_pairs, const void* dout,
+                           const float* dh_last, void* du, void* ddelta, float* dA, void* dB,
+                           void* dC, float* dD, float* ddelta_bias, float* dh_init, void* dz,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * One decode step.  Replaces selective_update

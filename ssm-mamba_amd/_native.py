@@ -38,7 +38,7 @@ SIGNATURES = {
         _p, _p, _p, _p, _p, _i64,              # u, delta, A, B, C, bc_batch_stride
         _p, _p, _p, _p,                        # D, delta_bias, h_init, length
         _i32, _p, _i32,                        # padding_right, z, delta_softplus
-        _p, _p, _p, _p,                        # out, out_ungated, h_chunks, h_last
+        _p, _p, _p, _i32, _p,                  # out, out_ungated, h_chunks, h_pairs, h_last
         _p, _sz, _p,                           # workspace, bytes, stream
     ]),
     "ssm_selective_scan_bwd": (_i32, [
@@ -46,7 +46,7 @@ SIGNATURES = {
         _p, _p, _p, _p, _p, _i64,              # u, delta, A, B, C, bc_batch_stride
         _p, _p, _p, _p,                        # D, delta_bias, h_init, length
         _i32, _p, _p, _i32,                    # padding_right, z, out_ungated, delta_softplus
-        _p, _p, _p,                            # h_chunks, dout, dh_last
+        _p, _i32, _p, _p,                      # h_chunks, h_pairs, dout, dh_last
         _p, _p, _p, _p, _p, _p, _p, _p, _p,    # du, ddelta, dA, dB, dC, dD, ddelta_bias, dh_init, dz
         _p, _sz, _p,                           # workspace, bytes, stream
     ]),
@@ -94,7 +94,7 @@ SIGNATURES = {
     ]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 def lib() -> ctypes.CDLL:

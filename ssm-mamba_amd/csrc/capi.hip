@@ -16,6 +16,7 @@
 namespace ssm {
 hipError_t launch_scan_fwd(const ScanParams& p, int dtype, bool aligned, float* bc, hipStream_t st);
 hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* bc, hipStream_t st);
+hipError_t launch_chunk_decay(const ScanParams& p, int dtype, float* pairs, hipStream_t st);
 hipError_t launch_state_update(const UpdateParams& p, int dtype, bool vecN, hipStream_t st);
 size_t bc_prep_floats(int batch, int nstate, int seqlen);
 size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen);
@@ -201,7 +202,7 @@ extern "C" {
 
 const char* ssm_last_error(void) { return g_err.c_str(); }
 
-int ssm_abi_version(void) { return 5; }
+int ssm_abi_version(void) { return 6; }
 
 int ssm_profile_begin(void) {
   g_err.clear();
@@ -283,13 +284,14 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                            const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
                            const void* z, int delta_softplus, void* out, void* out_ungated,
-                           float* h_chunks, float* h_last, void* workspace, size_t workspace_bytes,
-                           void* stream) {
+                           float* h_chunks, int h_pairs, float* h_last, void* workspace,
+                           size_t workspace_bytes, void* stream) {
   g_err.clear();
   if (int e = check_common(batch, dim, seqlen, nstate, dtype, 256)) return e;
   if (!u || !delta || !A || !B || !C || !out)
     return fail(SSM_ERR_INVALID, "u, delta, A, B, C and out must be non-NULL");
   if (out_ungated && !z) return fail(SSM_ERR_INVALID, "out_ungated requires z");
+  if (h_pairs && !h_chunks) return fail(SSM_ERR_INVALID, "h_pairs requires h_chunks");
   const size_t need = ssm_scan_fwd_workspace_bytes(batch, dim, seqlen, nstate);
   if (!workspace || workspace_bytes < need)
     return fail(SSM_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
@@ -301,7 +303,10 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                                        h_init, length, padding_right, z, delta_softplus);
   p.out = out;
   p.out_ungated = out_ungated;
-  p.h_chunks = h_chunks;
+  // pair layout: the states go to the odd slots (one row of dim in), the
+  // chunk decays to the even slots
+  p.h_chunks = (h_chunks && h_pairs) ? h_chunks + dim : h_chunks;
+  p.hs = h_pairs ? 2 : 1;
   p.h_last = h_last;
   // workspace: [prepped B/C][segment states and step sums][dummy]
   char* ws = static_cast<char*>(workspace) +
@@ -313,6 +318,12 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));
   p.dummy = ws;
   const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out, out_ungated});
+  if (h_pairs) {
+    if (int e = hip_status(ssm::launch_chunk_decay(p, dtype, h_chunks,
+                                                   static_cast<hipStream_t>(stream)),
+                           "selective_scan chunk decay launch"))
+      return e;
+  }
   return hip_status(ssm::launch_scan_fwd(p, dtype, aligned, static_cast<float*>(workspace),
                                          static_cast<hipStream_t>(stream)),
                     "selective_scan forward launch");
@@ -324,8 +335,8 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                            const float* delta_bias,
                            const float* h_init, const int64_t* length, int padding_right,
                            const void* z, const void* out_ungated, int delta_softplus,
-                           const float* h_chunks, const void* dout, const float* dh_last,
-                           void* du, void* ddelta,
+                           const float* h_chunks, int h_pairs, const void* dout,
+                           const float* dh_last, void* du, void* ddelta,
                            float* dA, void* dB, void* dC, float* dD, float* ddelta_bias,
                            float* dh_init, void* dz, void* workspace, size_t workspace_bytes,
                            void* stream) {
@@ -347,7 +358,8 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   ssm::ScanParams p = make_scan_params(batch, dim, seqlen, nstate, u, delta, A, B, C,
                                        bc_batch_stride, D, delta_bias,
                                        h_init, length, padding_right, z, delta_softplus);
-  p.h_chunks_in = h_chunks;
+  p.h_chunks_in = h_pairs ? h_chunks + dim : h_chunks;
+  p.hs = h_pairs ? 2 : 1;
   p.dout = dout;
   p.dh_last = dh_last;
   p.du = du;

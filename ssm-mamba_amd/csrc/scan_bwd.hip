@@ -292,7 +292,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       for (int s = 0; s < 2; ++s) {
         const int nc = min(n0 + (g * kWaves + w) * 2 + s, N - 1);
         const float* src = tile > 0
-            ? h_chunks + (((size_t)b * p.nchunks + (tile - 1)) * N + nc) * Dm + chc
+            ? h_chunks + (((size_t)b * p.nchunks + (tile - 1)) * N + nc) * p.hs * (size_t)Dm + chc
             : (h_init ? h_init + (rb + chc) * N + nc : h_chunks);
         hcn[g][s] = *src;
       }

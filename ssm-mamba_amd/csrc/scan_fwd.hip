@@ -189,6 +189,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   const T* __restrict__ z_row = zp + (rb + a_chc) * L;
   const bool softplus = p.softplus != 0;
   const bool save = h_chunks != nullptr;
+  const size_t hsD = (size_t)p.hs * Dm;  // floats between the saved rows of two states
   float* const dummyf = static_cast<float*>(dummy);
 
   // Raw row pieces of the next super-tile, all loads issued at once right
@@ -310,13 +311,13 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
           // layout (batch, nchunks, nstate, dim): each state is one
           // contiguous 256 B run of the wave's 64 channels
           const int c = (t0 + 4 * t4) / kChunk;
-          float* hc = h_chunks + ((size_t)b * p.nchunks + c) * N * (size_t)Dm + ch;
+          float* hc = h_chunks + ((size_t)b * p.nchunks + c) * N * hsD + ch;
 #pragma unroll
           for (int g = 0; g < kSG; ++g)
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
               const int n = (g * kWaves + w) * 2 + s;
-              if (n < N) hc[(size_t)n * Dm] = h[g][s];
+              if (n < N) hc[(size_t)n * hsD] = h[g][s];
             }
         }
       };
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
         const float4* __restrict__ cBC = sBC[i][w];
         const bool hc_ok = save && ch_ok && w < ngroups;
         const bool hc2_ok = hc_ok && 2 * w + 1 < N;
-        float* const hc = h_chunks + (((size_t)b * p.nchunks + t0 / kChunk) * N + 2 * w) * Dm + ch;
+        float* const hc = h_chunks + (((size_t)b * p.nchunks + t0 / kChunk) * N + 2 * w) * hsD + ch;
         BC2 bcb[2];
         float4 dlb[2], dub[2];
         lds_bc_block(cBC, 0, bcb[0]);
@@ -346,9 +347,9 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
           fwd_block(dlb[c], dub[c], bcb[c], A2[0], h[0], y);
           sY[w][k][lane ^ col_swz(k)] = make_float4(y[0], y[1], y[2], y[3]);
           if ((k & 3) == 3) {
-            const size_t off = (size_t)(k / 4) * N * Dm;
+            const size_t off = (size_t)(k / 4) * N * hsD;
             *(hc_ok ? hc + off : dummyf) = h[0][0];
-            *(hc2_ok ? hc + off + Dm : dummyf) = h[0][1];
+            *(hc2_ok ? hc + off + hsD : dummyf) = h[0][1];
           }
         }
       } else if constexpr (kSG == 1) {
@@ -359,7 +360,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
           // computed.
           const float4* __restrict__ cBC = sBC[i][w];
           float* hc = (save && ch_ok)
-                          ? h_chunks + (((size_t)b * p.nchunks + t0 / kChunk) * N + 2 * w) * Dm + ch
+                          ? h_chunks + (((size_t)b * p.nchunks + t0 / kChunk) * N + 2 * w) * hsD + ch
                           : nullptr;
           const bool second = 2 * w + 1 < N;
           BC2 bcb[2];
@@ -379,9 +380,9 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
             fwd_block(dlb[c], dub[c], bcb[c], A2[0], h[0], y);
             sY[w][k][lane ^ col_swz(k)] = make_float4(y[0], y[1], y[2], y[3]);
             if ((k & 3) == 3 && hc) {
-              float* q = hc + (size_t)(k / 4) * N * Dm;
+              float* q = hc + (size_t)(k / 4) * N * hsD;
               q[0] = h[0][0];
-              if (second) q[Dm] = h[0][1];
+              if (second) q[hsD] = h[0][1];
             }
           }
         } else if (w < ngroups) {
@@ -684,6 +685,102 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_segsum_kernel(
 #pragma unroll
   for (int m = 1; m < kT4; m <<= 1) dtsum += __shfl_xor(dtsum, m, 64);
   if (a_q == 0 && a_ok) seg_dt[sb * Dm + a_ch] = dtsum;
+}
+
+// ---------------------------------------------------------------- chunk decays
+
+// The first half of the reference's (prod a, h) chunk carry
+// (csrc/selective_scan/forward_kernel.cu:225-228): the product of the decays
+// a_t = exp(delta_t A) from step 0 to the end of each chunk, which is
+// exp(A * S_c) with S_c the sum of the step sizes over those steps (padded
+// steps count zero, as their decay is 1).  Written into the even slots of the
+// pair layout pairs (batch, nchunks, 2 * nstate, dim) fp32 by two kernels that
+// run before the scan, whose states then fill the odd slots.
+
+// Step-size sum of each chunk, per (b, d, chunk c), parked in the odd slot of
+// state 0 (the scan overwrites it); consecutive threads take consecutive
+// chunks of a row, so the row is read contiguously.
+template <typename T>
+__global__ __launch_bounds__(256) void chunk_dt_sum_kernel(const ScanDims p,
+                                                           const T* __restrict__ dl,
+                                                           const float* __restrict__ biasp,
+                                                           const int64_t* __restrict__ length,
+                                                           float* __restrict__ pairs) {
+  const int L = p.seqlen, Dm = p.dim, K = p.nchunks, N2 = 2 * p.nstate;
+  const size_t total = (size_t)p.batch * Dm * K;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % K);
+    const size_t bd = i / K;
+    const int d = (int)(bd % Dm), b = (int)(bd / Dm);
+    int vlo, vhi;
+    valid_window(length, p.pad_right, b, L, vlo, vhi);
+    const float bias = biasp ? biasp[d] : 0.0f;
+    const T* row = dl + bd * L;
+    const int t1 = min(L, (c + 1) * kChunk);
+    float acc = 0.0f;
+    for (int t = c * kChunk; t < t1; ++t) {
+      const float x = Elem<T>::load1(row + t) + bias;
+      const float dt = p.softplus ? softplus_t20(x) : x;
+      acc += (t >= vlo && t < vhi) ? dt : 0.0f;
+    }
+    pairs[(((size_t)b * K + c) * N2 + 1) * Dm + d] = acc;
+  }
+}
+
+// prod a per (b, d, state n) at every chunk end: a running sum of the chunk
+// step sums, and exp2(A log2(e) S) into the even slot of each state.  One
+// thread per (b, d, group of 4 states); consecutive threads take consecutive
+// channels, so the slot writes are contiguous.
+__global__ __launch_bounds__(256) void chunk_decay_kernel(const ScanDims p,
+                                                          const float* __restrict__ Ap,
+                                                          float* __restrict__ pairs) {
+  const int Dm = p.dim, K = p.nchunks, N = p.nstate, N2 = 2 * N;
+  const int ng = (N + 3) / 4;
+  const size_t total = (size_t)p.batch * ng * Dm;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int d = (int)(i % Dm);
+    const size_t r = i / Dm;
+    const int q = (int)(r % ng), b = (int)(r / ng);
+    float A2[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = 4 * q + j;
+      A2[j] = n < N ? Ap[(size_t)d * N + n] * kLog2e : 0.0f;
+    }
+    float S = 0.0f;
+    for (int c = 0; c < K; ++c) {
+      float* slot = pairs + ((size_t)b * K + c) * N2 * Dm + d;
+      S += slot[Dm];  // the chunk's step sum (odd slot of state 0)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = 4 * q + j;
+        if (n < N) slot[(size_t)2 * n * Dm] = fast_exp2(A2[j] * S);
+      }
+    }
+  }
+}
+
+hipError_t launch_chunk_decay(const ScanParams& p, int dtype, float* pairs, hipStream_t st) {
+  const size_t n1 = (size_t)p.batch * p.dim * p.nchunks;
+  {
+    ProfScope prof("chunk_dt_sum", st);
+    const int blocks = (int)std::min<size_t>((n1 + 255) / 256, 65535);
+    if (dtype == 1)
+      hipLaunchKernelGGL(chunk_dt_sum_kernel<__hip_bfloat16>, dim3(blocks), dim3(256), 0, st,
+                         dims_of(p), (const __hip_bfloat16*)p.delta, p.bias, p.length, pairs);
+    else
+      hipLaunchKernelGGL(chunk_dt_sum_kernel<float>, dim3(blocks), dim3(256), 0, st, dims_of(p),
+                         (const float*)p.delta, p.bias, p.length, pairs);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  ProfScope prof("chunk_decay", st);
+  const size_t n2 = (size_t)p.batch * ((p.nstate + 3) / 4) * p.dim;
+  const int blocks = (int)std::min<size_t>((n2 + 255) / 256, 65535);
+  hipLaunchKernelGGL(chunk_decay_kernel, dim3(blocks), dim3(256), 0, st, dims_of(p), p.A, pairs);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------- launch

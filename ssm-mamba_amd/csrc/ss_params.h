@@ -32,6 +32,7 @@ struct ScanDims {
   int nseg;     // segments (1: the whole row in one workgroup)
   int sub_k;    // forward summaries per segment (sub-segments of seg_len / sub_k steps)
   int64_t bc_bstride;  // elements between batch rows of B and of C (rows of a batch are seqlen apart)
+  int hs;              // h_chunks state-slot stride in rows of dim (1: states only; 2: (prod a, h) pairs)
 };
 
 struct ScanParams {
@@ -56,7 +57,13 @@ struct ScanParams {
 
   // forward outputs
   void* out;
-  float* h_chunks;  // nullable (then h_last)
+  // nullable (then h_last).  Row (b, chunk c, state n) of dim floats starts at
+  // h_chunks + ((b * nchunks + c) * nstate * hs + n * hs) * dim: hs = 1 is the
+  // (batch, nchunks, nstate, dim) state layout; hs = 2 interleaves a second
+  // row per state (the caller offsets h_chunks by one row to write the odd
+  // slots of a (batch, nchunks, 2 * nstate, dim) pair layout)
+  float* h_chunks;
+  int hs;
   float* h_last;    // nullable
 
   // backward
@@ -120,7 +127,8 @@ struct UpdateParams {
 
 inline ScanDims dims_of(const ScanParams& p) {
   return ScanDims{p.batch,    p.dim,     p.seqlen,  p.nstate, p.nchunks, p.nblk,
-                  p.pad_right, p.softplus, p.seg_len, p.nseg,   p.sub_k,  p.bc_bstride};
+                  p.pad_right, p.softplus, p.seg_len, p.nseg,   p.sub_k,  p.bc_bstride,
+                  p.hs > 1 ? p.hs : 1};
 }
 
 }  // namespace ssm

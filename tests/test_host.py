@@ -44,23 +44,23 @@ def test_invalid_arguments_return_errors():
     from ssm_mamba_amd import _native as N
     lib = N.lib()
     rc = lib.ssm_selective_scan_fwd(1, 1, 1, 300, 0, *([None] * 5), 0,
-                                    *([None] * 4), 1, None, 1, None, None, None, None, None, 0,
-                                    None)
+                                    *([None] * 4), 1, None, 1, None, None, None, 0, None, None,
+                                    0, None)
     assert rc == 2 and b"state_dim <= 256" in lib.ssm_last_error()
     rc = lib.ssm_selective_scan_fwd(1, 1, 0, 16, 0, *([None] * 5), 0,
-                                    *([None] * 4), 1, None, 1, None, None, None, None, None, 0,
-                                    None)
+                                    *([None] * 4), 1, None, 1, None, None, None, 0, None, None,
+                                    0, None)
     assert rc == 1 and b">= 1" in lib.ssm_last_error()
     rc = lib.ssm_selective_scan_fwd(1, 1, 1, 16, 7, *([None] * 5), 0,
-                                    *([None] * 4), 1, None, 1, None, None, None, None, None, 0,
-                                    None)
+                                    *([None] * 4), 1, None, 1, None, None, None, 0, None, None,
+                                    0, None)
     assert rc == 1 and b"dtype" in lib.ssm_last_error()
     rc = lib.ssm_selective_scan_fwd(1, 1, 1, 16, 0, *([None] * 5), 0,
-                                    *([None] * 4), 1, None, 1, None, None, None, None, None, 0,
-                                    None)
+                                    *([None] * 4), 1, None, 1, None, None, None, 0, None, None,
+                                    0, None)
     assert rc == 1 and b"non-NULL" in lib.ssm_last_error()
-    rc = lib.ssm_selective_scan_bwd(1, 1, 1, 257, 0, *([None] * 5), 0, *([None] * 4), 1, None, None, 1, None, None,
-                                    None, *([None] * 9), None, 0, None)
+    rc = lib.ssm_selective_scan_bwd(1, 1, 1, 257, 0, *([None] * 5), 0, *([None] * 4), 1, None, None, 1, None, 0,
+                                    None, None, *([None] * 9), None, 0, None)
     assert rc == 2 and b"state_dim <= 256" in lib.ssm_last_error()
     # past 64 states the backward runs in chunks: its workspace holds the
     # chunks' per-position sums (2 x chunks x batch x dim x seqlen fp32)
@@ -81,7 +81,7 @@ def test_gate_arguments_are_checked():
 
     def bwd(z, y, dz):
         return lib.ssm_selective_scan_bwd(1, 64, 16, 16, 0, P, P, P, P, P, 0, None, None, None, None,
-                                          1, z, y, 1, P, P, None, P, P, P, P, P, None, None, None,
+                                          1, z, y, 1, P, 0, P, None, P, P, P, P, P, None, None, None,
                                           dz, P, 1 << 30, None)
 
     for z, y, dz in ((P, None, P), (P, P, None), (P, None, None)):
@@ -89,8 +89,11 @@ def test_gate_arguments_are_checked():
     for y, dz in ((P, None), (None, P), (P, P)):
         assert bwd(None, y, dz) == 1 and b"require z" in lib.ssm_last_error()
     rc = lib.ssm_selective_scan_fwd(1, 64, 16, 16, 0, P, P, P, P, P, 0, None, None, None, None, 1,
-                                    None, 1, P, P, P, None, P, 1 << 30, None)
+                                    None, 1, P, P, P, 0, None, P, 1 << 30, None)
     assert rc == 1 and b"out_ungated requires z" in lib.ssm_last_error()
+    rc = lib.ssm_selective_scan_fwd(1, 64, 16, 16, 0, P, P, P, P, P, 0, None, None, None, None, 1,
+                                    None, 1, P, None, None, 1, None, P, 1 << 30, None)
+    assert rc == 1 and b"h_pairs requires h_chunks" in lib.ssm_last_error()
 
 
 def test_folded_xproj_queries_and_checks():
@@ -129,10 +132,10 @@ def test_bc_batch_stride_is_checked():
     P = 4096  # never dereferenced
     ws = 1 << 30
     rc = lib.ssm_selective_scan_fwd(2, 64, 16, 16, 0, P, P, P, P, P, 16 * 16 - 8, None, None, None,
-                                    None, 1, None, 1, P, None, P, None, P, ws, None)
+                                    None, 1, None, 1, P, None, P, 0, None, P, ws, None)
     assert rc == 1 and b"bc_batch_stride" in lib.ssm_last_error()
     rc = lib.ssm_selective_scan_bwd(2, 64, 16, 16, 0, P, P, P, P, P, 100, None, None, None, None,
-                                    1, None, None, 1, P, P, None, P, P, P, P, P, None, None, None,
+                                    1, None, None, 1, P, 0, P, None, P, P, P, P, P, None, None, None,
                                     None, P, ws, None)
     assert rc == 1 and b"bc_batch_stride" in lib.ssm_last_error()
 
@@ -175,3 +178,52 @@ def test_product_path_has_no_oracle_import():
             if f.endswith(".py"):
                 src = open(os.path.join(dp, f)).read()
                 assert "import oracle" not in src and "from oracle" not in src, f
+
+
+def _toplevel(name):
+    """The extension module under the reference's top-level name (its
+    directory on sys.path, as the reference's ops/ files import it)."""
+    import importlib
+    import sys
+    d = os.path.join(ROOT, "ssm-mamba_amd", "_ext")
+    if d not in sys.path:
+        sys.path.insert(0, d)
+    return importlib.import_module(name)
+
+
+def test_extension_modules_mirror_the_reference_bindings():
+    """selective_scan.{forward, backward} and selective_update.apply exist under
+    the reference's module names with its parameter order
+    (csrc/selective_scan/bindings.cpp:5-8, csrc/selective_update/bindings.cpp:5-7,
+    csrc/selective_scan/selective_scan.h:73-99, selective_update.h:32-41)."""
+    ss, su = _toplevel("selective_scan"), _toplevel("selective_update")
+
+    def params(f):
+        sig = f.__doc__.splitlines()[0]
+        return [a.split(":")[0].strip() for a in sig[sig.index("(") + 1:sig.rindex(")")].split(",")]
+
+    assert params(ss.forward) == ["u", "A", "B", "C", "D", "delta", "delta_bias", "h_init",
+                                  "length", "padding_side"]
+    assert params(ss.backward) == ["u", "A", "B", "C", "D", "delta", "delta_bias", "h", "h_init",
+                                   "dout", "dh_last", "length", "padding_side"]
+    assert params(su.apply) == ["u", "A", "B", "C", "D", "delta", "delta_bias", "h"]
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda a: a.update(u=a["u"][0]), "u must be a 3D tensor"),
+    (lambda a: a.update(D=a["D"][None]), "D must be a 1D tensor"),
+    (lambda a: a.update(A=torch.randn(4, 257)), "selective_scan only supports state_dim <= 256"),
+    (lambda a: None, "u must be a CUDA tensor"),
+])
+def test_toplevel_scan_module_validation(mutate, msg):
+    """The top-level module raises RuntimeError with the reference's messages
+    (csrc/selective_scan/selective_scan.cpp:15-32,251) before any launch."""
+    ss = _toplevel("selective_scan")
+    a = _scan_args()
+    mutate(a)
+    with pytest.raises(RuntimeError, match=msg):
+        ss.forward(a["u"], a["A"], a["B"], a["C"], a["D"], a["delta"], a["delta_bias"])
+    h = torch.zeros(2, 4, 1, 6)
+    with pytest.raises(RuntimeError, match=msg):
+        ss.backward(a["u"], a["A"], a["B"], a["C"], a["D"], a["delta"], a["delta_bias"], h, None,
+                    a["u"] if a["u"].dim() == 3 else torch.zeros(2, 4, 8), None)
