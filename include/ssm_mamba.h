@@ -101,6 +101,27 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                            size_t workspace_bytes, void* stream);
 
 /*
+ * Selective-scan forward that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  Arguments and results as ssm_selective_scan_fwd; the
+ * workspace is a static device array of SSM_NOALLOC_SCRATCH_BYTES per GPU,
+ * held until the process ends.  Shapes whose ssm_scan_fwd_workspace_bytes()
+ * exceeds that size are rejected (SSM_ERR_UNSUPPORTED).  The first call on a
+ * device looks the array up on that device (hipGetSymbolAddress); no call
+ * allocates.  Every call on one GPU shares its array, so calls that overlap
+ * on one GPU (concurrent streams or threads) race: serialize them.
+ */
+#define SSM_NOALLOC_SCRATCH_BYTES (32u << 20)
+int ssm_selective_scan_fwd_noalloc(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate,
+                                   int dtype, const void* u, const void* delta, const float* A,
+                                   const void* B, const void* C, int64_t bc_batch_stride,
+                                   const float* D, const float* delta_bias, const float* h_init,
+                                   const int64_t* length, int padding_right, const void* z,
+                                   int delta_softplus, void* out, void* out_ungated,
+                                   float* h_chunks, int h_pairs, float* h_last, void* stream);
+
+/*
  * Selective-scan backward.  Replaces selective_scan_backward
  * (csrc/selective_scan/selective_scan.cpp:294-380, declared at
  * csrc/selective_scan/selective_scan.h:86-99) behind selective_scan.backward

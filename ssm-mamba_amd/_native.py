@@ -23,6 +23,7 @@ _sz = ctypes.c_size_t
 SSM_F32 = 0
 SSM_BF16 = 1
 SSM_CHUNK = 16
+SSM_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
@@ -40,6 +41,14 @@ SIGNATURES = {
         _i32, _p, _i32,                        # padding_right, z, delta_softplus
         _p, _p, _p, _i32, _p,                  # out, out_ungated, h_chunks, h_pairs, h_last
         _p, _sz, _p,                           # workspace, bytes, stream
+    ]),
+    "ssm_selective_scan_fwd_noalloc": (_i32, [
+        _i64, _i64, _i64, _i64, _i32,          # batch, dim, seqlen, nstate, dtype
+        _p, _p, _p, _p, _p, _i64,              # u, delta, A, B, C, bc_batch_stride
+        _p, _p, _p, _p,                        # D, delta_bias, h_init, length
+        _i32, _p, _i32,                        # padding_right, z, delta_softplus
+        _p, _p, _p, _i32, _p,                  # out, out_ungated, h_chunks, h_pairs, h_last
+        _p,                                    # stream
     ]),
     "ssm_selective_scan_bwd": (_i32, [
         _i64, _i64, _i64, _i64, _i32,

@@ -198,6 +198,39 @@ bool scan_aligned(int dtype, int64_t seqlen, std::initializer_list<const void*> 
 
 }  // namespace
 
+// ---- static scratch of the allocation-free forward
+//
+// Device memory for ssm_selective_scan_fwd_noalloc's workspace (prepped B/C,
+// sequence-split summaries, store sink): every GPU the library runs on holds
+// its own copy for the life of the process.  Host code never uses the
+// array's name as an address: each device's copy is found once with
+// hipGetSymbolAddress (with that device current) and kept in g_scratch.
+static __device__ __align__(256) unsigned char scratch[SSM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// The device address of the current device's scratch copy.
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  if (int e = hip_status(hipGetDevice(&dev), "hipGetDevice")) return e;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(SSM_ERR_UNSUPPORTED, "device index %d out of range (< %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    if (int e = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                           "hipGetSymbolAddress(scratch)"))
+      return e;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return SSM_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char* ssm_last_error(void) { return g_err.c_str(); }
@@ -400,6 +433,32 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out_ungated, dout, du, ddelta, dz});
   return hip_status(ssm::launch_scan_bwd(p, dtype, aligned, bc, static_cast<hipStream_t>(stream)),
                     "selective_scan backward launch");
+}
+
+int ssm_selective_scan_fwd_noalloc(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate,
+                                   int dtype, const void* u, const void* delta, const float* A,
+                                   const void* B, const void* C, int64_t bc_batch_stride,
+                                   const float* D, const float* delta_bias, const float* h_init,
+                                   const int64_t* length, int padding_right, const void* z,
+                                   int delta_softplus, void* out, void* out_ungated,
+                                   float* h_chunks, int h_pairs, float* h_last, void* stream) {
+  g_err.clear();
+  if (int e = check_common(batch, dim, seqlen, nstate, dtype, 256)) return e;
+  const size_t need = ssm_scan_fwd_workspace_bytes(batch, dim, seqlen, nstate);
+  if (need > (size_t)SSM_NOALLOC_SCRATCH_BYTES)
+    return fail(SSM_ERR_UNSUPPORTED,
+                "selective_scan forward without allocation: this shape needs %zu bytes of "
+                "workspace, more than the %zu-byte static scratch (use ssm_selective_scan_fwd "
+                "with a caller workspace)",
+                need, (size_t)SSM_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (int e = scratch_on_current_device(&ws)) return e;
+  // every workspace byte the kernels read is written by this call first
+  // (prepped B/C, segment summaries), so nothing needs clearing
+  return ssm_selective_scan_fwd(batch, dim, seqlen, nstate, dtype, u, delta, A, B, C,
+                                bc_batch_stride, D, delta_bias, h_init, length, padding_right, z,
+                                delta_softplus, out, out_ungated, h_chunks, h_pairs, h_last, ws,
+                                (size_t)SSM_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int ssm_selective_state_update(int64_t batch, int64_t dim, int64_t nstate, int dtype,
