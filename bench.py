@@ -29,14 +29,23 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# fp32 VALU issue ceiling of the MI355X: 256 CUs x 4 SIMDs x 16 lanes per
+# clock at the 2.4 GHz peak engine clock, in lane-operations per second
+# (packed fp32 forms are not used by this build)
+VALU_PEAK_LANE_OPS = 256 * 4 * 16 * 2.4e9
 
-# HBM bytes per launch of the config-1 scan kernels from rocprofv3 counter runs
-# of `bench.py --profile-run` (profiles/scan_decode_hbm_bytes.md):
-# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB, the factors being what the same
-# counters read for a 256 MiB device-to-device copy.  Re-measure after a
-# kernel change.
+# Stored counter results for the config-1 scan kernels, from rocprofv3 runs of
+# `bench.py --profile-run` (commands and tables in
+# profiles/scan_decode_hbm_bytes.md and profiles/scan_sq_counters_config1.md);
+# counters cannot be read inside the timed run, so these are re-measured
+# after each kernel change and reported with their source.
+#   traffic: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB per dispatch, the factors
+#            being what the same counters read for a 256 MiB device copy;
+#   valu:    SQ_INSTS_VALU wave instructions per dispatch (x 64 lanes).
 TRAFFIC_BYTES = {"scan_fwd": (2 * 103_763 + 277_650) * 1024,
                  "scan_bwd": (2 * 519_607 + 376_340) * 1024}
+VALU_INSTS = {"scan_fwd": 7.22e7, "scan_bwd": 2.025e8}
+COUNTERS_SOURCE = "profiles/scan_decode_hbm_bytes.md, profiles/scan_sq_counters_config1.md"
 
 
 def inputs(batch, dim, seqlen, nstate, dtype, dev, seed, delta_shift=0.0):
@@ -148,6 +157,113 @@ def time_decode(su, dev, steps, cold):
     e1.record()
     torch.cuda.synchronize()
     return 1e3 * e0.elapsed_time(e1) / steps
+
+
+def time_decode_flush(su, dev, steps, flush_mb=512):
+    """Config 2 decode steps with the Infinity Cache flushed before each one:
+    a `flush_mb` MB fill kernel between consecutive steps, all captured in
+    one HIP graph; a second graph holds the fills alone, and the difference
+    of the two replays is the time of the steps.  Returns microseconds per
+    step."""
+    import math
+
+    import torch
+    batch, dim, nstate = 64, 5120, 16
+    g = torch.Generator().manual_seed(2)
+    state = (torch.randn(batch, dim, nstate, generator=g) * 0.1).to(dev)
+    A = -torch.arange(1, nstate + 1, dtype=torch.float32)[None].expand(dim, nstate).contiguous().to(dev)
+    dt0 = torch.exp(torch.rand(dim, generator=g) * (math.log(0.1) - math.log(1e-3))
+                    + math.log(1e-3)).clamp(min=1e-4)
+    bias = (dt0 + torch.log(-torch.expm1(-dt0))).to(dev)
+    D = torch.ones(dim, device=dev)
+    x, dt, z = (torch.randn(batch, dim, generator=g).bfloat16().to(dev) for _ in range(3))
+    B, C = (torch.randn(batch, nstate, generator=g).bfloat16().to(dev) for _ in range(2))
+    out = torch.empty(batch, dim, dtype=torch.bfloat16, device=dev)
+    # float32, so the fill is a kernel (a byte pattern could become a memset node)
+    junk = torch.empty((flush_mb << 20) // 4, dtype=torch.float32, device=dev)
+
+    def run(with_steps):
+        for k in range(steps):
+            junk.fill_(float(k))
+            if with_steps:
+                su.apply_ext(x, A, B, C, D, dt, bias, state, z=z, inplace=True, out=out)
+
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        run(True)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    times = []
+    for with_steps in (True, False):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run(with_steps)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+        del graph
+    del junk
+    return 1e3 * (times[0] - times[1]) / steps
+
+
+def time_host_overhead(dev, calls=200):
+    """Per-call cost of the operator API on the host next to the kernel time:
+    SelectiveUpdateFn.apply at config 2 (B=64, D=5120, N=16, bf16 vectors,
+    fp32 state) and SelectiveScanFn.apply (forward, inference) at batch 4,
+    2048 channels, L=2048, N=16 (the config-4 prefill shape).  host_us: time
+    to enqueue one call (Python, argument checks, allocation, launch);
+    wall_us: per call over a loop ended by a synchronize; kernel_us: the
+    library's kernel time from HIP events."""
+    import math
+
+    import torch
+
+    from ssm_mamba_amd import _native as N
+    from ssm_mamba_amd.ops import SelectiveScanFn, SelectiveUpdateFn
+    res = {}
+    g = torch.Generator().manual_seed(3)
+    b, d, n = 64, 5120, 16
+    st = (torch.randn(b, d, n, generator=g) * 0.1).to(dev)
+    A = -torch.arange(1, n + 1, dtype=torch.float32)[None].expand(d, n).contiguous().to(dev)
+    dt0 = torch.exp(torch.rand(d, generator=g) * (math.log(0.1) - math.log(1e-3))
+                    + math.log(1e-3)).clamp(min=1e-4)
+    bias = (dt0 + torch.log(-torch.expm1(-dt0))).to(dev)
+    D = torch.ones(d, device=dev)
+    u, dt = (torch.randn(b, d, generator=g).bfloat16().to(dev) for _ in range(2))
+    B, C = (torch.randn(b, n, generator=g).bfloat16().to(dev) for _ in range(2))
+    cases = {"SelectiveUpdateFn.apply config2":
+             lambda: SelectiveUpdateFn.apply(u, A, B, C, D, dt, bias, st)}
+    bs, ds, L = 4, 2048, 2048
+    us = torch.randn(bs, ds, L, generator=g).bfloat16().to(dev)
+    dls = torch.randn(bs, ds, L, generator=g).bfloat16().to(dev)
+    Bs, Cs = (torch.randn(bs, n, L, generator=g).bfloat16().to(dev) for _ in range(2))
+    As = A[:ds].contiguous()
+    cases["SelectiveScanFn.apply fwd B4 D2048 L2048"] = \
+        lambda: SelectiveScanFn.apply(us, As, Bs, Cs, D[:ds], dls, bias[:ds])
+    with torch.no_grad():
+        for name, fn in cases.items():
+            for _ in range(10):
+                fn()
+            torch.cuda.synchronize()
+            N.profile_begin()
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                fn()
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            prof = N.profile_end()
+            kern = sum(v[1] for v in prof.values()) / calls
+            res[name] = {"host_us": round(1e6 * (t1 - t0) / calls, 2),
+                         "wall_us": round(1e6 * (t2 - t0) / calls, 2),
+                         "kernel_us": round(1e3 * kern, 2)}
+    return res
 
 
 def decode_eager(su, dev, steps):
@@ -297,7 +413,9 @@ def cpu_baseline(seconds: float):
     import torch
 
     from oracle import scan_ref as R
-    threads = min(os.cpu_count() or 1, 16)
+    cpus = os.cpu_count() or 1
+    usable = _usable_cpus()
+    threads = min(cpus, usable)
     torch.set_num_threads(threads)
 
     def run(dim):
@@ -329,10 +447,37 @@ def cpu_baseline(seconds: float):
                    f"token-channel ({per_tc:.2f})"),
         "tokens_channels_per_s": round(tok_ch / t, 1),
         "cpu_model": _cpu_model(),
+        "cpu_count": cpus,
+        "cpus_usable": usable,
+        "threads_note": ("torch.set_num_threads(os.cpu_count()) as planned, capped at the "
+                         "CPUs this process may run on (affinity and cgroup quota)"),
     }
 
 
+def _usable_cpus() -> int:
+    """CPUs this process can run on at once: its affinity set, capped by the
+    cgroup CPU quota when one is set."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return max(1, n)
+
+
 def _cpu_model() -> str:
+    """The CPU model name as lscpu prints it (falls back to /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -401,6 +546,7 @@ def main():
     else:
         dom, dom_bytes, dom_ms = "scan_fwd", fwd_b, t_fwd
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    valu = VALU_INSTS[dom] * 64 / (dom_ms * 1e-3)
     res = {
         "metric": "scan fwd+bwd GB/s (% HBM peak) at 370M shape; state-update us/decode step",
         "value": round(gbs, 2),
@@ -424,17 +570,30 @@ def main():
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": TRAFFIC_BYTES.get(dom), "traffic_unit": "B",
+                     "traffic_source": "stored counter run: " + COUNTERS_SOURCE,
                      "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_ms": round(dom_ms, 4)},
+        # the ceiling the scan kernels actually meet: VALU instruction issue
+        "roofline_valu": {"kernel": dom, "bound": "valu",
+                          "achieved": round(valu / 1e12, 3), "peak": round(VALU_PEAK_LANE_OPS / 1e12, 3),
+                          "unit": "T lane-ops/s", "frac": round(valu / VALU_PEAK_LANE_OPS, 4),
+                          "valu_insts_per_launch": VALU_INSTS[dom],
+                          "source": "SQ_INSTS_VALU x 64 from " + COUNTERS_SOURCE},
     }
     if not args.no_extra:
         floor_us = 44_937_216 / (HBM_PEAK_GBS * 1e3)
         cold = time_decode(su, dev, 256, cold=True)
         warm = time_decode(su, dev, 256, cold=False)
+        flushed = time_decode_flush(su, dev, 256)
         res["decode"] = {"config": "B=64 D=5120 N=16, fp32 state, bf16 x/dt/z/B/C, 256 steps "
-                                   "replayed from one HIP graph (cold: 16 rotating states)",
-                         "us_per_step_cold": round(cold, 3), "us_per_step_warm": round(warm, 3),
-                         "floor_us": round(floor_us, 3), "cold_over_floor": round(cold / floor_us, 3),
-                         "cold_GBs": round(44_937_216 / (cold * 1e-6) / 1e9, 1)}
+                                   "replayed from one HIP graph; cold: a 512 MB fill between "
+                                   "steps (flush), and 16 rotating states (rotation)",
+                         "us_per_step_cold": round(flushed, 3),
+                         "us_per_step_cold_rotation": round(cold, 3),
+                         "us_per_step_warm": round(warm, 3),
+                         "floor_us": round(floor_us, 3),
+                         "cold_over_floor": round(flushed / floor_us, 3),
+                         "cold_GBs": round(44_937_216 / (flushed * 1e-6) / 1e9, 1)}
+        res["host_overhead"] = time_host_overhead(dev)
         x0 = inputs(2, 1536, 512, 16, torch.float32, dev, seed=0)
         ms0, k0 = time_scan(ss, N, x0, 20, 3, fwd_only=True)
         f0, _ = scan_bytes(2, 1536, 512, 16, 4)
