@@ -70,9 +70,11 @@ def layer_params(sd: Dict[str, torch.Tensor], i: int, dtype=torch.float64) -> Di
 
 def mamba_forward(p: Dict[str, torch.Tensor], x: torch.Tensor, state_dim: int, delta_rank: int,
                   h0: Optional[torch.Tensor] = None, lengths: Optional[torch.Tensor] = None,
-                  use_cache: bool = False, prefix: str = "ssm."):
+                  use_cache: bool = False, prefix: str = "ssm.", state_mag: Optional[list] = None):
     """x (batch, L, model_dim) -> (y (batch, L, model_dim), last state
-    (batch, inner, N), conv window (batch, inner, k-1) or None)."""
+    (batch, inner, N), conv window (batch, inner, k-1) or None).  With a list
+    ``state_mag``, the scan's magnitude run (sums of |terms| of the last
+    state, ``scan_fwd(..., magnitude=True)``) is appended to it."""
     g = lambda n: p.get(prefix + n)
     batch, seqlen, _ = x.shape
     w_in = g("input_proj.weight")
@@ -103,6 +105,23 @@ def mamba_forward(p: Dict[str, torch.Tensor], x: torch.Tensor, state_dim: int, d
     res = scan_fwd(xc, delta, A, Bm, Cm, g("D"), g("delta_proj.bias"), h0,
                    None if lengths is None else lengths.cpu(), padding_right=False, z=gate,
                    chunk=None, dtype=x.dtype, keep_graph=True)
+    if state_mag is not None:
+        sm = scan_fwd(xc, delta, A, Bm, Cm, g("D"), g("delta_proj.bias"), h0,
+                      None if lengths is None else lengths.cpu(), padding_right=False, z=gate,
+                      chunk=None, dtype=x.dtype, magnitude=True)["h_last"]
+        # the conv window holds in-projection outputs: their terms' sizes
+        wm = None
+        if ctx is not None:
+            xm = (x.abs() @ w_in[:inner].abs().t()).permute(0, 2, 1)
+            if g("input_proj.bias") is not None:
+                xm = xm + g("input_proj.bias")[:inner].abs()[None, :, None]
+            wm = torch.zeros_like(ctx)
+            for b in range(batch):
+                for j in range(k - 1):
+                    t = int(lens[b]) - (k - 1) + j
+                    if t >= 0:
+                        wm[b, :, j] = xm[b, :, t]
+        state_mag.append((sm, wm))
     y = res["y"].permute(0, 2, 1) @ g("out_proj.weight").t()
     if g("out_proj.bias") is not None:
         y = y + g("out_proj.bias")
@@ -147,27 +166,43 @@ def _dims(sd: Dict[str, torch.Tensor]) -> Tuple[int, int, int]:
 
 def lm_forward(sd: Dict[str, torch.Tensor], input_ids: torch.Tensor,
                lengths: Optional[torch.Tensor] = None, use_cache: bool = False,
-               dtype=torch.float64):
+               dtype=torch.float64, logits_at: Optional[torch.Tensor] = None,
+               extras: Optional[dict] = None):
     """logits (batch, L, vocab) and, with use_cache, the per-layer caches
-    [(window, state)] (``models/causal_lm.py:75-91``)."""
+    [(window, state)] (``models/causal_lm.py:75-91``).
+
+    logits_at (batch, P) int64: only the logits at those positions,
+    (batch, P, vocab) -- the LM head at every position of a long prompt is
+    most of the work.  extras (a dict): receives "hidden", the normalized
+    final hidden state at those positions (the LM head's input), and
+    "state_mag", per layer (the magnitude run of the scan's last state, the
+    sizes of the conv window's in-projection terms or None)."""
     n_layers, state_dim, delta_rank = _dims(sd)
     cv = lambda t: t.to("cpu", dtype)
     x = cv(sd["embedding.weight"])[input_ids.cpu()]
     caches: List[Tuple[torch.Tensor, torch.Tensor]] = []
+    mags = [] if extras is not None else None
     for i in range(n_layers):
         p = layer_params(sd, i, dtype)
         h = rms_norm(x, p["norm.weight"])
         y, last, ctx = mamba_forward(p, h, state_dim, delta_rank, lengths=lengths,
-                                     use_cache=use_cache)
+                                     use_cache=use_cache, state_mag=mags)
         x = x + y
         caches.append((ctx, last))
+    if logits_at is not None:
+        x = torch.gather(x, 1, logits_at.cpu()[:, :, None].expand(-1, -1, x.shape[-1]))
     x = rms_norm(x, cv(sd["norm.weight"]))
+    if extras is not None:
+        extras["hidden"] = x
+        extras["state_mag"] = mags
     return x @ cv(sd["lm_head.weight"]).t(), caches
 
 
-def lm_step(sd: Dict[str, torch.Tensor], input_ids: torch.Tensor, caches, dtype=torch.float64):
+def lm_step(sd: Dict[str, torch.Tensor], input_ids: torch.Tensor, caches, dtype=torch.float64,
+            extras: Optional[dict] = None):
     """logits (batch, vocab) for one token and the advanced caches
-    (``models/causal_lm.py:93-104``)."""
+    (``models/causal_lm.py:93-104``); extras (a dict) receives "hidden", the
+    LM head's input."""
     n_layers, state_dim, delta_rank = _dims(sd)
     cv = lambda t: t.detach().to("cpu", dtype)
     x = cv(sd["embedding.weight"])[input_ids.cpu()]
@@ -180,6 +215,8 @@ def lm_step(sd: Dict[str, torch.Tensor], input_ids: torch.Tensor, caches, dtype=
         x = x + y
         new.append((ctx, state))
     x = rms_norm(x, cv(sd["norm.weight"]))
+    if extras is not None:
+        extras["hidden"] = x
     return x @ cv(sd["lm_head.weight"]).t(), new
 
 

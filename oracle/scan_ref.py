@@ -297,7 +297,7 @@ EPS32 = 2.0 ** -24
 
 
 def error_bound(ref: torch.Tensor, mag: Optional[torch.Tensor], rtol: float, atol: float,
-                c: float) -> torch.Tensor:
+                c: float, eps: float = EPS32) -> torch.Tensor:
     """Per-element tolerance for a float32 evaluation of a result whose
     float64 value is ``ref`` and whose terms have absolute values summing to
     ``mag`` (the ``magnitude`` mode of this module):
@@ -306,11 +306,13 @@ def error_bound(ref: torch.Tensor, mag: Optional[torch.Tensor], rtol: float, ato
     float32, (number of roundings along the longest chain) * u * sum |terms|
     (Higham, "Accuracy and Stability of Numerical Algorithms", 2nd ed., §4.2),
     with c standing for that chain length; it matters only where the terms
-    cancel, so that |ref| is small against their sizes."""
+    cancel, so that |ref| is small against their sizes.  ``eps`` is the unit
+    roundoff of the arithmetic being bounded (2^-8 where the values pass
+    through bfloat16 between operations)."""
     r = ref.detach().double().cpu()
     b = atol + rtol * r.abs()
     if mag is not None:
-        b = b + c * EPS32 * mag.detach().double().cpu()
+        b = b + c * eps * mag.detach().double().cpu()
     return b
 
 
