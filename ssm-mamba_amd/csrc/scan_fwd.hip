@@ -508,6 +508,286 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
   }
 }
 
+// ---------------------------------------------------------------- forward, N <= 16
+
+// Role-split forward for up to 16 states.  A workgroup of 12 waves covers one
+// batch row b x 64 channels and walks its segment in 16-step tiles (one saved
+// chunk each):
+//   consumer waves 0..7   lane = channel, wave w = states 2w and 2w+1: the
+//                         recurrence over tile i, reading delta, delta*u and
+//                         B/C from LDS; each wave leaves its partial sums of
+//                         C*h in its own LDS slice;
+//   producer waves 8..11  wave 8+q = 4-step column q of every tile, lane =
+//                         channel: stage tile i+1 (softplus, delta*u, B and C)
+//                         and finish tile i-1 (the eight slices added in a
+//                         fixed order, D*u, the z gate, the stores).
+// Both roles run at the same time with one barrier per tile and
+// double-buffered LDS, so the producers' transcendental, conversion and store
+// work fills the issue slots the recurrence leaves (a SIMD runs two consumer
+// waves and one producer wave) instead of running between its steps.  The
+// arithmetic and its order are those of scan_fwd_kernel, so both kernels give
+// the same bits.
+//
+// Every tile is processed whole: the steps past the segment end are given
+// delta = 0 (identity steps), so the saved state of a partial last chunk is
+// the state at its last real step, and their outputs are never stored.
+constexpr int kWsTile = 16;   // steps per tile
+constexpr int kWsCons = 8;    // consumer waves
+constexpr int kWsProd = 4;    // producer waves
+constexpr int kWsThreads = 64 * (kWsCons + kWsProd);
+static_assert(kWsTile == kChunk, "a tile is one saved chunk");
+static_assert(kWsProd * 4 == kWsTile, "one producer wave per 4-step column");
+static_assert(2 * kWsCons * kWsTile == 64 * kWsProd, "one B/C value pair per producer lane");
+
+// LDS slot swizzle of the role-split kernel: column q of channel row r sits at
+// row index r ^ ws_swz(q).  The producers' four lanes of a row access the
+// four columns together, which would otherwise fall in the same banks (the
+// columns are 1 KiB apart); with it every 8 and every 16 consecutive lanes of
+// a 128-bit access touch distinct 16-byte bank groups.  The consumers access
+// whole columns, a permutation of 64 consecutive float4s.
+__device__ __forceinline__ constexpr int ws_swz(int q) { return 2 * q + 8 * (q & 1); }
+
+template <typename T>
+struct WsRows {  // one tile's raw loads of a producer lane
+  typename Raw4<T>::type u, d, z;
+  float B, C;
+};
+
+template <typename T, int kZ, bool kAligned>
+__global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
+    const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
+    const float* __restrict__ Ap, const T* __restrict__ Bp, const T* __restrict__ Cp,
+    const float* __restrict__ Dp, const float* __restrict__ biasp,
+    const float* __restrict__ h_init, const int64_t* __restrict__ length,
+    const T* __restrict__ zp, T* __restrict__ out, T* __restrict__ yu,
+    float* __restrict__ h_chunks, float* __restrict__ h_last, void* __restrict__ dummy,
+    const float* __restrict__ seg_h, const float* __restrict__ seg_dt) {
+  constexpr bool kHasZ = kZ != 0;
+  constexpr bool kSaveY = kZ == 2;
+  constexpr int kT4 = kWsTile / 4;
+  // tiles of rows a producer lane loads together (two sets in flight: fits
+  // the 168 VGPRs of three waves per SIMD)
+  constexpr int kWsBatch = sizeof(T) == 2 ? 4 : 2;
+
+  __shared__ float4 sDl[2][kT4][kBlockCh];                // delta, [tile parity][column][channel]
+  __shared__ float4 sDu[2][kT4][kBlockCh];                // delta * u
+  __shared__ float4 sBC[2][kWsCons][kWsTile];             // (B0, C0, B1, C1) per pair and step
+  __shared__ float4 sY[2][kWsCons][kT4][kBlockCh];        // per-wave partial sums of C*h
+
+  const int lane = threadIdx.x & 63;
+  const int w = wave_id_uniform();
+  const int b = blockIdx.y;
+  const int d0 = blockIdx.x * kBlockCh;
+  const int L = p.seqlen, Dm = p.dim, N = p.nstate;
+  const int seg = blockIdx.z;
+  const int Tbeg = seg * p.seg_len;  // a multiple of kWsTile
+  const int Lend = min(L, Tbeg + p.seg_len);
+  const int ntiles = (Lend - Tbeg + kWsTile - 1) / kWsTile;
+  const size_t rb = (size_t)b * Dm;
+  const int ch = d0 + lane;
+  const bool ch_ok = ch < Dm;
+
+  if (w < kWsCons) {
+    // ------------------------------------------------ consumer: the recurrence
+    float h[2], A2[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int n = 2 * w + s;
+      const bool ok = ch_ok && n < N;
+      A2[s] = ok ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
+      float hv = (ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
+      // carry in through the earlier sub-segments' affine maps, in order
+      for (int sp = 0; ok && sp < seg * p.sub_k; ++sp) {
+        const size_t sb = (size_t)sp * p.batch + b;
+        const float decay = fast_exp2(A2[s] * seg_dt[sb * Dm + ch]);
+        hv = fmaf(decay, hv, seg_h[(sb * N + n) * Dm + ch]);
+      }
+      h[s] = hv;
+    }
+    const bool save = h_chunks != nullptr;
+    const size_t hsD = (size_t)p.hs * Dm;  // floats between the saved rows of two states
+    const size_t cstride = (size_t)N * hsD;  // floats between the saves of two chunks
+    float* const hc = save ? h_chunks + ((size_t)b * p.nchunks + Tbeg / kChunk) * cstride +
+                                 (size_t)(2 * w) * hsD + ch
+                           : nullptr;
+    const bool ok0 = ch_ok && 2 * w < N, ok1 = ch_ok && 2 * w + 1 < N;
+    float* const dummyf = static_cast<float*>(dummy);
+
+    for (int i = 0; i <= ntiles; ++i) {
+      __syncthreads();
+      if (i == ntiles) break;
+      const int buf = i & 1;
+      const float4* __restrict__ cBC = sBC[buf][w];
+      const float4* __restrict__ cDl = sDl[buf][0];
+      const float4* __restrict__ cDu = sDu[buf][0];
+      float4* __restrict__ cY = sY[buf][w][0];
+      // block k+1's LDS reads are issued before block k is computed
+      BC2 bcb[2];
+      float4 dlb[2], dub[2];
+      lds_bc_block(cBC, 0, bcb[0]);
+      dlb[0] = cDl[lane ^ ws_swz(0)];
+      dub[0] = cDu[lane ^ ws_swz(0)];
+#pragma unroll
+      for (int k = 0; k < kT4; ++k) {
+        const int c = k & 1;
+        if (k + 1 < kT4) {
+          dlb[c ^ 1] = cDl[(k + 1) * kBlockCh + (lane ^ ws_swz(k + 1))];
+          dub[c ^ 1] = cDu[(k + 1) * kBlockCh + (lane ^ ws_swz(k + 1))];
+          lds_bc_block(cBC, 4 * (k + 1), bcb[c ^ 1]);
+        }
+        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        fwd_block(dlb[c], dub[c], bcb[c], A2, h, y);
+        cY[k * kBlockCh + (lane ^ ws_swz(k))] = make_float4(y[0], y[1], y[2], y[3]);
+      }
+      if (save) {
+        // layout (batch, nchunks, nstate, dim): one contiguous 256 B run per state
+        float* const q = hc + (size_t)i * cstride;
+        *(ok0 ? q : dummyf) = h[0];
+        *(ok1 ? q + hsD : dummyf) = h[1];
+      }
+    }
+    if (!save && h_last && Lend == L) {
+      if (ok0) h_last[(rb + ch) * N + 2 * w] = h[0];
+      if (ok1) h_last[(rb + ch) * N + 2 * w + 1] = h[1];
+    }
+    return;
+  }
+
+  // ------------------------------------------------ producer: staging and outputs
+  // producer lane pt -> channel row pt / 4 and 4-step column q = pt % 4 of
+  // every tile: the four lanes of a row read and write 16 consecutive steps
+  const int pt = (w - kWsCons) * 64 + lane;
+  const int row = pt / kT4;
+  const int q = pt % kT4;
+  const int sw = row ^ ws_swz(q);  // LDS slot of this row in column q
+  const int pch = d0 + row;
+  const bool pch_ok = pch < Dm;
+  const float Dv = (pch_ok && Dp) ? Dp[pch] : 0.0f;
+  const float Bias = (pch_ok && biasp) ? biasp[pch] : 0.0f;
+  // rows of the clamped channel (valid addresses; lanes past the last channel
+  // are masked to delta = 0 and never stored)
+  const int chc = min(pch, Dm - 1);
+  const T* __restrict__ u_row = u + (rb + chc) * L;
+  const T* __restrict__ d_row = dl + (rb + chc) * L;
+  const T* __restrict__ z_row = zp + (rb + chc) * L;
+  int vlo, vhi;
+  valid_window(length, p.pad_right, b, L, vlo, vhi);
+  vhi = min(vhi, Lend);  // steps past the segment are identity steps here
+  const bool softplus = p.softplus != 0;
+  const int last_t0 = Tbeg + (ntiles - 1) * kWsTile;
+  // B/C staging: producer lane pt -> (state 2G + half, step) of a tile
+  const int bc_half = pt / (kWsCons * kWsTile);
+  const int bc_G = (pt / kWsTile) % kWsCons;
+  const int bc_step = pt % kWsTile;
+  const int bc_n = 2 * bc_G + bc_half;
+  const bool bc_ok = bc_n < N;
+  const size_t bc_row = (size_t)b * p.bc_bstride + (size_t)min(bc_n, N - 1) * L;
+  const T* __restrict__ B_row = Bp + bc_row;
+  const T* __restrict__ C_row = Cp + bc_row;
+  float2* const bc_dst0 = reinterpret_cast<float2*>(&sBC[0][bc_G][bc_step]) + bc_half;
+  float2* const bc_dst1 = reinterpret_cast<float2*>(&sBC[1][bc_G][bc_step]) + bc_half;
+
+  // raw rows of tiles i0 .. i0 + kWsBatch - 1 (clamped to the last tile; the
+  // loads of tiles past it are never used)
+  auto issue = [&](WsRows<T> (&r)[kWsBatch], int i0) {
+#pragma unroll
+    for (int j = 0; j < kWsBatch; ++j) {
+      const int t0 = min(Tbeg + (i0 + j) * kWsTile, last_t0);
+      r[j].u = load_raw4_nb<T, kAligned>(u_row, t0 + 4 * q, L, pch_ok);
+      r[j].d = load_raw4_nb<T, kAligned>(d_row, t0 + 4 * q, L, pch_ok);
+      if constexpr (kHasZ) r[j].z = load_raw4_nb<T, kAligned>(z_row, t0 + 4 * q, L, pch_ok);
+      else r[j].z = typename Raw4<T>::type{};
+      const int tb = min(t0 + bc_step, L - 1);
+      r[j].B = Elem<T>::load1(B_row + tb);
+      r[j].C = Elem<T>::load1(C_row + tb);
+    }
+  };
+
+  // stage tile i: delta (softplus once per element, zero outside the valid
+  // window), delta * u, B and C; D*u and silu(z) are kept for its finish
+  auto stage = [&](const WsRows<T>& r, int i, float (&sk)[4], float (&gt)[4]) {
+    const int t = Tbeg + i * kWsTile + 4 * q;
+    float uv[4], dv[4], de[4], du[4];
+    decode4(r.u, uv);
+    decode4(r.d, dv);
+    if constexpr (kHasZ) {
+      float zv[4];
+      decode4(r.z, zv);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) gt[j] = silu_f(zv[j]);
+    }
+    // Rows past the last channel are left unmasked: the consumer lanes that
+    // read them store nothing.  The window mask is a bitwise AND rather than
+    // a select so that the compiler keeps the four elements in one block
+    // instead of branching around the softplus of masked lanes.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sk[j] = Dv * uv[j];
+      const float x = dv[j] + Bias;
+      const float sp = softplus_t20(x);
+      const float dt = softplus ? sp : x;
+      const uint32_t keep = (t + j >= vlo && t + j < vhi) ? 0xffffffffu : 0u;
+      de[j] = __uint_as_float(__float_as_uint(dt) & keep);
+      du[j] = de[j] * uv[j];
+    }
+    const int buf = i & 1;
+    sDl[buf][q][sw] = make_float4(de[0], de[1], de[2], de[3]);
+    sDu[buf][q][sw] = make_float4(du[0], du[1], du[2], du[3]);
+    *(buf ? bc_dst1 : bc_dst0) = bc_ok ? make_float2(r.B, r.C) : make_float2(0.0f, 0.0f);
+  };
+
+  // finish tile i: the eight slices in a fixed order, D*u, the gate, stores
+  auto finish = [&](int i, const float (&sk)[4], const float (&gt)[4]) {
+    const int t = Tbeg + i * kWsTile + 4 * q;
+    const int buf = i & 1;
+    float4 acc = sY[buf][0][q][sw];
+#pragma unroll
+    for (int ww = 1; ww < kWsCons; ++ww) {
+      const float4 v = sY[buf][ww][q][sw];
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    float y[4] = {sk[0] + acc.x, sk[1] + acc.y, sk[2] + acc.z, sk[3] + acc.w};
+    const bool st_ok = pch_ok && t < Lend;
+    if constexpr (kSaveY) store4_nb<T, kAligned>(yu + (rb + pch) * L, t, L, st_ok, dummy, y);
+    if constexpr (kHasZ) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[j] *= gt[j];
+    }
+    store4_nb<T, kAligned>(out + (rb + pch) * L, t, L, st_ok, dummy, y);
+  };
+
+  // Iteration i (0 .. ntiles) after barrier i: finish tile i-1 (its slices
+  // were written during iteration i-1), then stage tile i+1 (the consumers
+  // read it after barrier i+1).  Finishing first frees tile i-1's D*u / gate
+  // registers, which tile i+1 reuses (same parity).
+  //
+  // Rows are loaded kWsBatch tiles at a time, one batch ahead: the batch
+  // starting at tile i0 is in `cur`, the next one is loaded into `nxt` when
+  // iteration i0 begins; the two register sets swap roles every batch.
+  WsRows<T> ra[kWsBatch], rb2[kWsBatch];
+  float sk[2][4], gt[2][4];
+  const int niter = ntiles + 1;
+  auto batch = [&](WsRows<T> (&cur)[kWsBatch], WsRows<T> (&nxt)[kWsBatch], int i0) {
+    issue(nxt, i0 + kWsBatch);
+#pragma unroll
+    for (int j = 0; j < kWsBatch; ++j) {
+      const int i = i0 + j;
+      if (i < niter) {
+        __syncthreads();
+        if (i >= 1) finish(i - 1, sk[(j + 1) & 1], gt[(j + 1) & 1]);
+        if (i + 1 < ntiles)
+          stage(j + 1 < kWsBatch ? cur[j + 1] : nxt[0], i + 1, sk[(j + 1) & 1], gt[(j + 1) & 1]);
+      }
+    }
+  };
+  issue(ra, 0);
+  stage(ra[0], 0, sk[0], gt[0]);
+  for (int i0 = 0; i0 < niter; i0 += 2 * kWsBatch) {
+    batch(ra, rb2, i0);
+    if (i0 + kWsBatch < niter) batch(rb2, ra, i0 + kWsBatch);
+  }
+}
+
 // ---------------------------------------------------------------- segment summaries
 
 // For sub-segment j = blockIdx.z (seg_len / sub_k steps; the sub-segments
@@ -853,6 +1133,14 @@ static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t 
     if (e != hipSuccess) return e;
   }
   ProfScope prof("scan_fwd", st);
+  if constexpr (kSG == 1) {
+    hipLaunchKernelGGL((scan_fwd_ws_kernel<T, kZ, kAligned>), dim3(p.nblk, p.batch, p.nseg),
+                       dim3(kWsThreads), 0, st, dims_of(p), (const T*)p.u, (const T*)p.delta, p.A,
+                       (const T*)p.B, (const T*)p.C, p.D, p.bias, p.h_init, p.length,
+                       (const T*)p.z, (T*)p.out, (T*)p.out_ungated, p.h_chunks, p.h_last, p.dummy,
+                       p.seg_h, p.seg_dt);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kZ, kAligned>),
                      dim3(p.nblk, p.batch, p.nseg), dim3(kThreads), 0, st, dims_of(p),
                      (const T*)p.u, (const T*)p.delta, p.A, bc, (const T*)p.B, (const T*)p.C, p.D,

@@ -78,15 +78,16 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
-// log1p(e) for e >= 0 by Goldberg's correction: w = 1 + e rounded; when w != 1,
-// log(w) * e / (w - 1) recovers the digits lost in forming w (D. Goldberg,
-// "What every computer scientist should know about floating-point
-// arithmetic", 1991, Theorem 4).
+// log1p(e) for 0 <= e <= 1.  w = 1 + e rounds away c = (w - 1) - e, which is
+// exact (Sterbenz: w - 1 and e are within a factor of two of each other, or
+// w == 1 and c = -e); then log1p(e) = log(w) + log(1 - c / w), and
+// log(1 - c / w) = -c / w to within c^2 / 2, and 1 / w = 2 - w to within
+// (w - 1)^2.  With |c| <= 2^-24 and |c| <= e, both dropped terms stay below
+// 2^-24 relative to log1p(e): no reciprocal and no select are needed.
 __device__ __forceinline__ float log1p_pos(float e) {
-  float w = 1.0f + e;
-  float lw = fast_log2(w) * kLn2;
-  float r = lw * e * fast_rcp(w - 1.0f);
-  return (w == 1.0f) ? e : r;
+  const float w = 1.0f + e;
+  const float c = (w - 1.0f) - e;
+  return fmaf(fast_log2(w), kLn2, -c * (2.0f - w));
 }
 
 // softplus with the reference threshold: x <= 20 ? log1p(exp(x)) : x.
