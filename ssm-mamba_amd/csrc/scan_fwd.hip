@@ -517,16 +517,18 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
 //                         recurrence over tile i, reading delta, delta*u and
 //                         B/C from LDS; each wave leaves its partial sums of
 //                         C*h in its own LDS slice;
-//   producer waves 8..11  wave 8+q = 4-step column q of every tile, lane =
-//                         channel: stage tile i+1 (softplus, delta*u, B and C)
-//                         and finish tile i-1 (the eight slices added in a
-//                         fixed order, D*u, the z gate, the stores).
-// Both roles run at the same time with one barrier per tile and
-// double-buffered LDS, so the producers' transcendental, conversion and store
-// work fills the issue slots the recurrence leaves (a SIMD runs two consumer
-// waves and one producer wave) instead of running between its steps.  The
-// arithmetic and its order are those of scan_fwd_kernel, so both kernels give
-// the same bits.
+//   producer waves 8..11  lane -> (channel row, 4-step column): stage tile
+//                         i+2 (softplus, delta*u, B and C) and finish tile i-1
+//                         (the eight slices added in a fixed order, D*u, the z
+//                         gate, the stores).
+// Both roles run at the same time with one barrier per tile, so the
+// producers' transcendental, conversion and store work fills the issue slots
+// the recurrence leaves (a SIMD runs two consumer waves and one producer
+// wave).  Staging runs two tiles ahead (three LDS buffers), so a tile's data
+// is complete one barrier before it is needed: a consumer reads the first
+// block of tile i+1 at the end of tile i and starts each tile without waiting
+// for LDS.  The arithmetic and its order are those of scan_fwd_kernel, so
+// both kernels give the same bits.
 //
 // Every tile is processed whole: the steps past the segment end are given
 // delta = 0 (identity steps), so the saved state of a partial last chunk is
@@ -535,6 +537,8 @@ constexpr int kWsTile = 16;   // steps per tile
 constexpr int kWsCons = 8;    // consumer waves
 constexpr int kWsProd = 4;    // producer waves
 constexpr int kWsThreads = 64 * (kWsCons + kWsProd);
+constexpr int kWsStage = 3;   // staging buffers (tiles i, i+1 and i+2)
+constexpr int kWsRing = 4;    // producer register ring of raw rows, in tiles
 static_assert(kWsTile == kChunk, "a tile is one saved chunk");
 static_assert(kWsProd * 4 == kWsTile, "one producer wave per 4-step column");
 static_assert(2 * kWsCons * kWsTile == 64 * kWsProd, "one B/C value pair per producer lane");
@@ -547,11 +551,18 @@ static_assert(2 * kWsCons * kWsTile == 64 * kWsProd, "one B/C value pair per pro
 // whole columns, a permutation of 64 consecutive float4s.
 __device__ __forceinline__ constexpr int ws_swz(int q) { return 2 * q + 8 * (q & 1); }
 
+// One tile's raw loads of a producer lane, kept as loaded bits: converting
+// at the load would make the compiler wait for it right there.
 template <typename T>
-struct WsRows {  // one tile's raw loads of a producer lane
+struct WsRows {
   typename Raw4<T>::type u, d, z;
-  float B, C;
+  T B, C;
 };
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(__hip_bfloat16 x) {
+  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, x) << 16);
+}
 
 template <typename T, int kZ, bool kAligned>
 __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
@@ -565,14 +576,11 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   constexpr bool kHasZ = kZ != 0;
   constexpr bool kSaveY = kZ == 2;
   constexpr int kT4 = kWsTile / 4;
-  // tiles of rows a producer lane loads together (two sets in flight: fits
-  // the 168 VGPRs of three waves per SIMD)
-  constexpr int kWsBatch = sizeof(T) == 2 ? 4 : 2;
 
-  __shared__ float4 sDl[2][kT4][kBlockCh];                // delta, [tile parity][column][channel]
-  __shared__ float4 sDu[2][kT4][kBlockCh];                // delta * u
-  __shared__ float4 sBC[2][kWsCons][kWsTile];             // (B0, C0, B1, C1) per pair and step
-  __shared__ float4 sY[2][kWsCons][kT4][kBlockCh];        // per-wave partial sums of C*h
+  __shared__ float4 sDl[kWsStage][kT4][kBlockCh];          // delta, [buffer][column][channel]
+  __shared__ float4 sDu[kWsStage][kT4][kBlockCh];          // delta * u
+  __shared__ float4 sBC[kWsStage][kWsCons][kWsTile];       // (B0, C0, B1, C1) per pair and step
+  __shared__ float4 sY[2][kWsCons][kT4][kBlockCh];         // per-wave partial sums of C*h
 
   const int lane = threadIdx.x & 63;
   const int w = wave_id_uniform();
@@ -584,11 +592,11 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   const int Lend = min(L, Tbeg + p.seg_len);
   const int ntiles = (Lend - Tbeg + kWsTile - 1) / kWsTile;
   const size_t rb = (size_t)b * Dm;
-  const int ch = d0 + lane;
-  const bool ch_ok = ch < Dm;
 
   if (w < kWsCons) {
     // ------------------------------------------------ consumer: the recurrence
+    const int ch = d0 + lane;
+    const bool ch_ok = ch < Dm;
     float h[2], A2[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -613,38 +621,44 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     const bool ok0 = ch_ok && 2 * w < N, ok1 = ch_ok && 2 * w + 1 < N;
     float* const dummyf = static_cast<float*>(dummy);
 
-    for (int i = 0; i <= ntiles; ++i) {
+    // block 0 of a tile: read at the end of the previous tile
+    BC2 bcb[2];
+    float4 dlb[2], dub[2];
+    auto read_block = [&](int buf, int k, BC2& bc, float4& dl4, float4& du4) {
+      lds_bc_block(sBC[buf][w], 4 * k, bc);
+      dl4 = sDl[buf][k][lane ^ ws_swz(k)];
+      du4 = sDu[buf][k][lane ^ ws_swz(k)];
+    };
+    // as many barriers as the producers: 1 + 4 * ceil(ntiles / 4)
+    const int nbar = 1 + 4 * ((ntiles + 3) / 4);
+    int buf = 0;
+    for (int i = 0; i < nbar; ++i) {
       __syncthreads();
-      if (i == ntiles) break;
-      const int buf = i & 1;
-      const float4* __restrict__ cBC = sBC[buf][w];
-      const float4* __restrict__ cDl = sDl[buf][0];
-      const float4* __restrict__ cDu = sDu[buf][0];
-      float4* __restrict__ cY = sY[buf][w][0];
-      // block k+1's LDS reads are issued before block k is computed
-      BC2 bcb[2];
-      float4 dlb[2], dub[2];
-      lds_bc_block(cBC, 0, bcb[0]);
-      dlb[0] = cDl[lane ^ ws_swz(0)];
-      dub[0] = cDu[lane ^ ws_swz(0)];
+      if (i >= ntiles) continue;
+      if (i == 0) read_block(0, 0, bcb[0], dlb[0], dub[0]);
+      const int nbuf = buf == kWsStage - 1 ? 0 : buf + 1;
+      float4* __restrict__ cY = sY[i & 1][w][0];
+      // block k+1's LDS reads are issued before block k is computed; after
+      // the last block, the next tile's first block (staged one iteration
+      // ago, so complete since this tile's barrier)
 #pragma unroll
       for (int k = 0; k < kT4; ++k) {
         const int c = k & 1;
-        if (k + 1 < kT4) {
-          dlb[c ^ 1] = cDl[(k + 1) * kBlockCh + (lane ^ ws_swz(k + 1))];
-          dub[c ^ 1] = cDu[(k + 1) * kBlockCh + (lane ^ ws_swz(k + 1))];
-          lds_bc_block(cBC, 4 * (k + 1), bcb[c ^ 1]);
-        }
+        if (k + 1 < kT4) read_block(buf, k + 1, bcb[c ^ 1], dlb[c ^ 1], dub[c ^ 1]);
+        else read_block(nbuf, 0, bcb[c ^ 1], dlb[c ^ 1], dub[c ^ 1]);
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         fwd_block(dlb[c], dub[c], bcb[c], A2, h, y);
         cY[k * kBlockCh + (lane ^ ws_swz(k))] = make_float4(y[0], y[1], y[2], y[3]);
       }
+      // kT4 is even: the next tile's block 0 sits in buffer 0 again
+      static_assert(kT4 % 2 == 0, "block 0 of every tile in register set 0");
       if (save) {
         // layout (batch, nchunks, nstate, dim): one contiguous 256 B run per state
         float* const q = hc + (size_t)i * cstride;
         *(ok0 ? q : dummyf) = h[0];
         *(ok1 ? q + hsD : dummyf) = h[1];
       }
+      buf = nbuf;
     }
     if (!save && h_last && Lend == L) {
       if (ok0) h_last[(rb + ch) * N + 2 * w] = h[0];
@@ -684,29 +698,26 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   const size_t bc_row = (size_t)b * p.bc_bstride + (size_t)min(bc_n, N - 1) * L;
   const T* __restrict__ B_row = Bp + bc_row;
   const T* __restrict__ C_row = Cp + bc_row;
-  float2* const bc_dst0 = reinterpret_cast<float2*>(&sBC[0][bc_G][bc_step]) + bc_half;
-  float2* const bc_dst1 = reinterpret_cast<float2*>(&sBC[1][bc_G][bc_step]) + bc_half;
 
-  // raw rows of tiles i0 .. i0 + kWsBatch - 1 (clamped to the last tile; the
-  // loads of tiles past it are never used)
-  auto issue = [&](WsRows<T> (&r)[kWsBatch], int i0) {
-#pragma unroll
-    for (int j = 0; j < kWsBatch; ++j) {
-      const int t0 = min(Tbeg + (i0 + j) * kWsTile, last_t0);
-      r[j].u = load_raw4_nb<T, kAligned>(u_row, t0 + 4 * q, L, pch_ok);
-      r[j].d = load_raw4_nb<T, kAligned>(d_row, t0 + 4 * q, L, pch_ok);
-      if constexpr (kHasZ) r[j].z = load_raw4_nb<T, kAligned>(z_row, t0 + 4 * q, L, pch_ok);
-      else r[j].z = typename Raw4<T>::type{};
-      const int tb = min(t0 + bc_step, L - 1);
-      r[j].B = Elem<T>::load1(B_row + tb);
-      r[j].C = Elem<T>::load1(C_row + tb);
-    }
+  // raw rows of tile i (clamped to the last tile; the loads of tiles past it
+  // are never used)
+  auto issue = [&](WsRows<T>& r, int i) {
+    const int t0 = min(Tbeg + i * kWsTile, last_t0);
+    r.u = load_raw4_nb<T, kAligned>(u_row, t0 + 4 * q, L, pch_ok);
+    r.d = load_raw4_nb<T, kAligned>(d_row, t0 + 4 * q, L, pch_ok);
+    if constexpr (kHasZ) r.z = load_raw4_nb<T, kAligned>(z_row, t0 + 4 * q, L, pch_ok);
+    else r.z = typename Raw4<T>::type{};
+    const int tb = min(t0 + bc_step, L - 1);
+    r.B = B_row[tb];
+    r.C = C_row[tb];
   };
 
-  // stage tile i: delta (softplus once per element, zero outside the valid
-  // window), delta * u, B and C; D*u and silu(z) are kept for its finish
-  auto stage = [&](const WsRows<T>& r, int i, float (&sk)[4], float (&gt)[4]) {
-    const int t = Tbeg + i * kWsTile + 4 * q;
+  // stage tile i into buffer sb: delta (softplus once per element, zero
+  // outside the valid window), delta * u, B and C; D*u and silu(z) are kept
+  // for its finish
+  auto stage = [&](const WsRows<T>& r, int i, int sb, float (&sk)[4], float (&gt)[4]) {
+    const int t_tile = Tbeg + i * kWsTile;
+    const int t = t_tile + 4 * q;
     float uv[4], dv[4], de[4], du[4];
     decode4(r.u, uv);
     decode4(r.d, dv);
@@ -717,74 +728,114 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       for (int j = 0; j < 4; ++j) gt[j] = silu_f(zv[j]);
     }
     // Rows past the last channel are left unmasked: the consumer lanes that
-    // read them store nothing.  The window mask is a bitwise AND rather than
-    // a select so that the compiler keeps the four elements in one block
-    // instead of branching around the softplus of masked lanes.
+    // read them store nothing.  Tiles wholly inside the valid window (all but
+    // at most two per row) skip the window mask; the mask is a bitwise AND
+    // rather than a select so that the compiler keeps the four elements in
+    // one block instead of branching around the softplus of masked lanes.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       sk[j] = Dv * uv[j];
       const float x = dv[j] + Bias;
       const float sp = softplus_t20(x);
-      const float dt = softplus ? sp : x;
-      const uint32_t keep = (t + j >= vlo && t + j < vhi) ? 0xffffffffu : 0u;
-      de[j] = __uint_as_float(__float_as_uint(dt) & keep);
-      du[j] = de[j] * uv[j];
+      de[j] = softplus ? sp : x;
     }
-    const int buf = i & 1;
-    sDl[buf][q][sw] = make_float4(de[0], de[1], de[2], de[3]);
-    sDu[buf][q][sw] = make_float4(du[0], du[1], du[2], du[3]);
-    *(buf ? bc_dst1 : bc_dst0) = bc_ok ? make_float2(r.B, r.C) : make_float2(0.0f, 0.0f);
-  };
-
-  // finish tile i: the eight slices in a fixed order, D*u, the gate, stores
-  auto finish = [&](int i, const float (&sk)[4], const float (&gt)[4]) {
-    const int t = Tbeg + i * kWsTile + 4 * q;
-    const int buf = i & 1;
-    float4 acc = sY[buf][0][q][sw];
+    if (!(t_tile >= vlo && t_tile + kWsTile <= vhi)) {
 #pragma unroll
-    for (int ww = 1; ww < kWsCons; ++ww) {
-      const float4 v = sY[buf][ww][q][sw];
-      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-    }
-    float y[4] = {sk[0] + acc.x, sk[1] + acc.y, sk[2] + acc.z, sk[3] + acc.w};
-    const bool st_ok = pch_ok && t < Lend;
-    if constexpr (kSaveY) store4_nb<T, kAligned>(yu + (rb + pch) * L, t, L, st_ok, dummy, y);
-    if constexpr (kHasZ) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) y[j] *= gt[j];
-    }
-    store4_nb<T, kAligned>(out + (rb + pch) * L, t, L, st_ok, dummy, y);
-  };
-
-  // Iteration i (0 .. ntiles) after barrier i: finish tile i-1 (its slices
-  // were written during iteration i-1), then stage tile i+1 (the consumers
-  // read it after barrier i+1).  Finishing first frees tile i-1's D*u / gate
-  // registers, which tile i+1 reuses (same parity).
-  //
-  // Rows are loaded kWsBatch tiles at a time, one batch ahead: the batch
-  // starting at tile i0 is in `cur`, the next one is loaded into `nxt` when
-  // iteration i0 begins; the two register sets swap roles every batch.
-  WsRows<T> ra[kWsBatch], rb2[kWsBatch];
-  float sk[2][4], gt[2][4];
-  const int niter = ntiles + 1;
-  auto batch = [&](WsRows<T> (&cur)[kWsBatch], WsRows<T> (&nxt)[kWsBatch], int i0) {
-    issue(nxt, i0 + kWsBatch);
-#pragma unroll
-    for (int j = 0; j < kWsBatch; ++j) {
-      const int i = i0 + j;
-      if (i < niter) {
-        __syncthreads();
-        if (i >= 1) finish(i - 1, sk[(j + 1) & 1], gt[(j + 1) & 1]);
-        if (i + 1 < ntiles)
-          stage(j + 1 < kWsBatch ? cur[j + 1] : nxt[0], i + 1, sk[(j + 1) & 1], gt[(j + 1) & 1]);
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t keep = (t + j >= vlo && t + j < vhi) ? 0xffffffffu : 0u;
+        de[j] = __uint_as_float(__float_as_uint(de[j]) & keep);
       }
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) du[j] = de[j] * uv[j];
+    sDl[sb][q][sw] = make_float4(de[0], de[1], de[2], de[3]);
+    sDu[sb][q][sw] = make_float4(du[0], du[1], du[2], du[3]);
+    reinterpret_cast<float2*>(&sBC[sb][bc_G][bc_step])[bc_half] =
+        bc_ok ? make_float2(to_f32(r.B), to_f32(r.C)) : make_float2(0.0f, 0.0f);
   };
-  issue(ra, 0);
-  stage(ra[0], 0, sk[0], gt[0]);
-  for (int i0 = 0; i0 < niter; i0 += 2 * kWsBatch) {
-    batch(ra, rb2, i0);
-    if (i0 + kWsBatch < niter) batch(rb2, ra, i0 + kWsBatch);
+
+  // Output buffers of this wave's 16 channel rows (the launch guarantees
+  // 16 * L * sizeof(T) < 2^31, so the byte offsets fit).
+  const int wrow0 = d0 + (w - kWsCons) * (kBlockCh / kWsProd);
+  const uint32_t wbytes =
+      (uint32_t)(max(0, min(kBlockCh / kWsProd, Dm - wrow0)) * (size_t)L * sizeof(T));
+  const auto out_rsrc = raw_rsrc(out + ((size_t)rb + wrow0) * L, wbytes);
+  const auto yu_rsrc = raw_rsrc(kSaveY ? yu + ((size_t)rb + wrow0) * L : out, kSaveY ? wbytes : 0u);
+  const uint32_t row_off = (uint32_t)((row % (kBlockCh / kWsProd)) * (size_t)L * sizeof(T));
+
+  // finish tile i: the eight slices (read before the staging work of the
+  // same iteration, added after it) in a fixed order, D*u, the gate, stores
+  auto finish_read = [&](int i, float4 (&v)[kWsCons]) {
+#pragma unroll
+    for (int ww = 0; ww < kWsCons; ++ww) v[ww] = sY[i & 1][ww][q][sw];
+  };
+  auto finish = [&](int i, const float4 (&v)[kWsCons], const float (&sk)[4],
+                    const float (&gt)[4]) {
+    const int t = Tbeg + i * kWsTile + 4 * q;
+    float4 acc = v[0];
+#pragma unroll
+    for (int ww = 1; ww < kWsCons; ++ww) {
+      acc.x += v[ww].x; acc.y += v[ww].y; acc.z += v[ww].z; acc.w += v[ww].w;
+    }
+    float y[4] = {sk[0] + acc.x, sk[1] + acc.y, sk[2] + acc.z, sk[3] + acc.w};
+    if constexpr (kAligned) {
+      // range-checked stores: rows past the last channel lie outside the
+      // wave's buffer range, and steps past the segment get an offset past it
+      const uint32_t off = t < Lend ? row_off + (uint32_t)t * sizeof(T) : kOffDrop;
+      if constexpr (kSaveY) buffer_store4<T>(yu_rsrc, off, y);
+      if constexpr (kHasZ) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[j] *= gt[j];
+      }
+      buffer_store4<T>(out_rsrc, off, y);
+    } else {
+      const bool st_ok = pch_ok && t < Lend;
+      if constexpr (kSaveY) store4_nb<T, kAligned>(yu + (rb + pch) * L, t, L, st_ok, dummy, y);
+      if constexpr (kHasZ) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[j] *= gt[j];
+      }
+      store4_nb<T, kAligned>(out + (rb + pch) * L, t, L, st_ok, dummy, y);
+    }
+  };
+
+  // Iteration i after barrier i: read tile i-1's slices (written during
+  // iteration i-1), stage tile i+2 into buffer (i+2) % 3 (last read during
+  // iteration i-1), finish tile i-1.  Raw rows travel in a ring of kWsRing
+  // tiles: tile k's loads are issued when tile k - kWsRing is staged, kWsRing
+  // iterations ahead of their use.  D*u and the gates ride in a ring of 4
+  // tiles (staged at iteration k - 2, finished at k + 1).
+  //
+  // Iterations 1 .. 4m run in unrolled groups of four with no conditions
+  // around memory operations: the compiler's wait for a ring slot's loads
+  // then counts only the operations issued after them (a conditional path
+  // into the loop header makes it wait for nearly all of them).  Work past
+  // the last tile is harmless: its loads are clamped into the rows, its
+  // staging buffers are never read and its stores fall outside the range.
+  WsRows<T> rows[kWsRing];
+  float sk[4][4], gt[4][4];
+  float4 v[kWsCons];
+#pragma unroll
+  for (int k = 0; k < kWsRing; ++k) issue(rows[k], k);
+  stage(rows[0], 0, 0, sk[0], gt[0]);
+  issue(rows[0], kWsRing);
+  stage(rows[1], 1, 1, sk[1], gt[1]);
+  issue(rows[1], kWsRing + 1);
+  __syncthreads();  // iteration 0
+  stage(rows[2], 2, 2, sk[2], gt[2]);
+  issue(rows[2], kWsRing + 2);
+  int sbuf = 0;  // staging buffer of tile i + 2
+  for (int i0 = 1; i0 <= ntiles; i0 += 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j;  // (i + 2) % 4 == (j + 3) % 4, (i - 1) % 4 == j
+      __syncthreads();
+      finish_read(i - 1, v);
+      stage(rows[(j + 3) % kWsRing], i + 2, sbuf, sk[(j + 3) & 3], gt[(j + 3) & 3]);
+      issue(rows[(j + 3) % kWsRing], i + 2 + kWsRing);
+      finish(i - 1, v, sk[j], gt[j]);
+      sbuf = sbuf == kWsStage - 1 ? 0 : sbuf + 1;
+    }
   }
 }
 
@@ -1120,6 +1171,12 @@ hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t
   return hipGetLastError();
 }
 
+// The role-split forward serves N <= 16 when a wave's 16 rows of output fit
+// a buffer range (16 * L * elem < 2^31); the general kernel serves the rest.
+static bool ws_forward(const ScanParams& p, size_t elem) {
+  return p.nstate <= 16 && (size_t)(kBlockCh / kWsProd) * p.seqlen * elem < (1u << 31);
+}
+
 template <typename T, int kSG, int kZ, bool kAligned>
 static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t st) {
   if (p.nseg > 1) {
@@ -1133,7 +1190,7 @@ static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t 
     if (e != hipSuccess) return e;
   }
   ProfScope prof("scan_fwd", st);
-  if constexpr (kSG == 1) {
+  if (ws_forward(p, sizeof(T))) {
     hipLaunchKernelGGL((scan_fwd_ws_kernel<T, kZ, kAligned>), dim3(p.nblk, p.batch, p.nseg),
                        dim3(kWsThreads), 0, st, dims_of(p), (const T*)p.u, (const T*)p.delta, p.A,
                        (const T*)p.B, (const T*)p.C, p.D, p.bias, p.h_init, p.length,

@@ -21,11 +21,14 @@ constexpr float kLn2 = 0.6931471805599453f;
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
+
+// Two floats to bf16, round-to-nearest-even, lo in bits 0-15: one
+// v_cvt_pk_bf16_f32 on gfx950.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  // round-to-nearest-even; lowers to v_cvt_pk_bf16_f32 on gfx950
-  __hip_bfloat16 a = __float2bfloat16(lo);
-  __hip_bfloat16 b = __float2bfloat16(hi);
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  const f32x2_v v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
 }
 
 template <typename T> struct Elem;
@@ -92,11 +95,13 @@ __device__ __forceinline__ float log1p_pos(float e) {
 
 // softplus with the reference threshold: x <= 20 ? log1p(exp(x)) : x.
 // Evaluated as max(x,0) + log1p(exp(-|x|)), which is the same function and keeps
-// exp's argument non-positive.
+// exp's argument non-positive.  The threshold needs no select: above 20,
+// exp(-|x|) < 2.1e-9 rounds 1 + e to 1, log1p_pos returns e itself, and x + e
+// rounds to x (half an ulp of x is 9.5e-7 there); infinities and NaN pass
+// through as in the reference.
 __device__ __forceinline__ float softplus_t20(float x) {
-  float e = fast_exp2(-fabsf(x) * kLog2e);
-  float v = fmaxf(x, 0.0f) + log1p_pos(e);
-  return x > 20.0f ? x : v;
+  const float e = fast_exp2(-fabsf(x) * kLog2e);
+  return fmaxf(x, 0.0f) + log1p_pos(e);
 }
 
 __device__ __forceinline__ float sigmoidf_fast(float x) {
@@ -108,7 +113,7 @@ __device__ __forceinline__ float sigmoidf_fast(float x) {
 __device__ __forceinline__ void softplus_and_grad_t20(float x, float& sp, float& sg) {
   const float e = fast_exp2(-fabsf(x) * kLog2e);
   const float r = fast_rcp(1.0f + e);
-  sp = x > 20.0f ? x : fmaxf(x, 0.0f) + log1p_pos(e);
+  sp = fmaxf(x, 0.0f) + log1p_pos(e);  // equals x above 20 (see softplus_t20)
   sg = x > 20.0f ? 1.0f : (x >= 0.0f ? r : e * r);
 }
 

@@ -166,6 +166,44 @@ __device__ __forceinline__ void store4(T* __restrict__ row, int t, int L, const 
   }
 }
 
+// ---------------------------------------------------------------- raw buffer stores
+
+// A raw (untyped) buffer descriptor over `bytes` bytes at `base`, held in
+// scalar registers.  The hardware checks every access against `bytes`: a store
+// at a larger offset is dropped, so a masked lane needs no separate address.
+// Dword 3 = 0x00020000 selects a 32-bit data format (the gfx9-family value; an
+// untyped access ignores the format, but a zero format disables the buffer).
+// base and bytes must be wave-uniform; they are passed through readfirstlane
+// so that the descriptor is built in scalar registers (a descriptor the
+// compiler cannot prove uniform is used one lane value at a time instead).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* const ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, (int)__builtin_amdgcn_readfirstlane(bytes),
+                                           0x00020000);
+}
+constexpr uint32_t kOffDrop = 0x80000000u;  // past every range built here (bytes < 2^31)
+
+typedef unsigned int u32x2_v __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4_v __attribute__((ext_vector_type(4)));
+
+// 4 consecutive elements at byte offset `off` of the buffer (dropped when off
+// is past its range).
+template <typename T>
+__device__ __forceinline__ void buffer_store4(__amdgpu_buffer_rsrc_t r, uint32_t off,
+                                              const float (&v)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    const u32x4_v x = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                       __float_as_uint(v[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(x, r, (int)off, 0, 0);
+  } else {
+    const u32x2_v x = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(x, r, (int)off, 0, 0);
+  }
+}
+
 // Wait until every outstanding LDS and scalar-memory load of this wave has
 // returned (s_waitcnt lgkmcnt(0)) and keep the scheduler from moving
 // instructions across this point.  Orders "consume block k" before "issue
