@@ -255,6 +255,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   // groups issue the same memory operations)
   const T* __restrict__ row3 = (kHasZ && grp1) ? yup + (rb + a_chc) * L : row1;
   const bool softplus = p.softplus != 0;
+  const uint32_t okm = a_ok ? 0xffffffffu : 0u;
   float accD = 0.0f, accB = 0.0f;
 
   // Prefetch of a tile's inputs.  Every load is unconditional from a
@@ -270,7 +271,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   constexpr int kBCStates = 2 * kWaves * kSG;  // states covered by the dispatch bucket
   static_assert(2 * kBCStates * kTileB == kSG * kThreads, "kSG B/C elements per thread");
   __shared__ float sBlk[kWaves * kSG][kT4][16];  // [pair][block][(step, state, B|C)]
-  float bcn[kSG];
+  T bcn[kSG];  // as loaded: converting at the load would make the compiler wait there
   const int chc = min(ch, Dm - 1);
   auto issue = [&](int tile) {
     const int t = tile * kTileB + a_col;
@@ -284,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       const int e = g * kThreads + tid;
       const int n = min(n0 + (e / kTileB) % kBCStates, N - 1);
       const int t = min(tile * kTileB + e % kTileB, L - 1);
-      bcn[g] = Elem<T>::load1((e / (kTileB * kBCStates) ? Craw : Braw) + (size_t)n * L + t);
+      bcn[g] = ((e / (kTileB * kBCStates)) ? Craw : Braw)[(size_t)n * L + t];
     }
 #pragma unroll
     for (int g = 0; g < kSG; ++g)
@@ -308,18 +309,28 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     float v1[4], v2[4];
     decode4(n1, v1);
     decode4(n2, v2);
+    // Masks (channel past the last one, step outside the valid window) are
+    // bitwise ANDs rather than selects, and the softplus switch selects its
+    // result: either way the compiler keeps the four elements in one block
+    // instead of branching around the transcendental work of masked lanes.
+    uint32_t keep[4] = {okm, okm, okm, okm};
+    if (!(t0 >= vlo && t0 + kTileB <= vhi)) {  // tiles wholly inside the window skip this
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tt = t0 + a_col + j;
+        keep[j] = (a_ok && tt >= vlo && tt < vhi) ? 0xffffffffu : 0u;
+      }
+    }
     if (!grp1) {  // u = v1, delta_raw = v2
       float de[4], du[4], sg[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float x = v2[j] + Bias;
-        float dt = x, g = 1.0f;
-        if (softplus) softplus_and_grad_t20(x, dt, g);
-        const int tt = t0 + a_col + j;
-        const bool valid = a_ok && tt >= vlo && tt < vhi;
-        de[j] = valid ? dt : 0.0f;
+        float sp, g;
+        softplus_and_grad_t20(x, sp, g);
+        de[j] = __uint_as_float(__float_as_uint(softplus ? sp : x) & keep[j]);
+        sg[j] = __uint_as_float(__float_as_uint(softplus ? g : 1.0f) & keep[j]);
         du[j] = de[j] * v1[j];
-        sg[j] = valid ? g : 0.0f;
       }
       sDelta[a_q][a_sw] = make_float4(de[0], de[1], de[2], de[3]);
       sDu[a_q][a_sw] = make_float4(du[0], du[1], du[2], du[3]);
@@ -330,9 +341,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       if constexpr (kHasZ) decode4(n3, v3);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int tt = t0 + a_col + j;
-        const bool valid = a_ok && tt >= vlo && tt < vhi;
-        const float dym = valid ? v1[j] : 0.0f;
+        const float dym = __uint_as_float(__float_as_uint(v1[j]) & keep[j]);
         if constexpr (kHasZ) {
           const float sz = sigmoidf_fast(v2[j]);
           dov[j] = dym * (v2[j] * sz);
@@ -348,7 +357,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
     for (int g = 0; g < kSG; ++g) {
       const int e = g * kThreads + tid;
       const int j = e % kTileB, n = (e / kTileB) % kBCStates, kind = e / (kTileB * kBCStates);
-      sBlk[n >> 1][j >> 2][(j & 3) * 4 + (n & 1) * 2 + kind] = n0 + n < N ? bcn[g] : 0.0f;
+      sBlk[n >> 1][j >> 2][(j & 3) * 4 + (n & 1) * 2 + kind] = n0 + n < N ? to_f32(bcn[g]) : 0.0f;
     }
 #pragma unroll
     for (int g = 0; g < kSG; ++g)

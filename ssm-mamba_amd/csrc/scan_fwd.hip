@@ -543,13 +543,13 @@ static_assert(kWsTile == kChunk, "a tile is one saved chunk");
 static_assert(kWsProd * 4 == kWsTile, "one producer wave per 4-step column");
 static_assert(2 * kWsCons * kWsTile == 64 * kWsProd, "one B/C value pair per producer lane");
 
-// LDS slot swizzle of the role-split kernel: column q of channel row r sits at
-// row index r ^ ws_swz(q).  The producers' four lanes of a row access the
-// four columns together, which would otherwise fall in the same banks (the
-// columns are 1 KiB apart); with it every 8 and every 16 consecutive lanes of
-// a 128-bit access touch distinct 16-byte bank groups.  The consumers access
-// whole columns, a permutation of 64 consecutive float4s.
-__device__ __forceinline__ constexpr int ws_swz(int q) { return 2 * q + 8 * (q & 1); }
+// LDS column length of the role-split kernel, in float4s: 64 channel rows
+// and 2 of padding, so consecutive columns start 1056 B apart (32 B past a
+// multiple of the 128 B bank cycle).  The producers' 8-lane groups of a
+// 128-bit access (rows r, r+1 x columns 0..3) then touch 8 distinct 16-byte
+// bank groups, and the consumers' whole-column accesses are 64 consecutive
+// float4s from one base register (the column is an immediate offset).
+constexpr int kWsRow = kBlockCh + 2;
 
 // One tile's raw loads of a producer lane, kept as loaded bits: converting
 // at the load would make the compiler wait for it right there.
@@ -559,10 +559,6 @@ struct WsRows {
   T B, C;
 };
 
-__device__ __forceinline__ float to_f32(float x) { return x; }
-__device__ __forceinline__ float to_f32(__hip_bfloat16 x) {
-  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, x) << 16);
-}
 
 template <typename T, int kZ, bool kAligned>
 __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
@@ -577,10 +573,10 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   constexpr bool kSaveY = kZ == 2;
   constexpr int kT4 = kWsTile / 4;
 
-  __shared__ float4 sDl[kWsStage][kT4][kBlockCh];          // delta, [buffer][column][channel]
-  __shared__ float4 sDu[kWsStage][kT4][kBlockCh];          // delta * u
+  // [buffer][delta | delta * u][column][channel row]
+  __shared__ float4 sSt[kWsStage][2][kT4][kWsRow];
   __shared__ float4 sBC[kWsStage][kWsCons][kWsTile];       // (B0, C0, B1, C1) per pair and step
-  __shared__ float4 sY[2][kWsCons][kT4][kBlockCh];         // per-wave partial sums of C*h
+  __shared__ float4 sY[2][kWsCons][kT4][kWsRow];           // per-wave partial sums of C*h
 
   const int lane = threadIdx.x & 63;
   const int w = wave_id_uniform();
@@ -615,19 +611,24 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     const bool save = h_chunks != nullptr;
     const size_t hsD = (size_t)p.hs * Dm;  // floats between the saved rows of two states
     const size_t cstride = (size_t)N * hsD;  // floats between the saves of two chunks
-    float* const hc = save ? h_chunks + ((size_t)b * p.nchunks + Tbeg / kChunk) * cstride +
-                                 (size_t)(2 * w) * hsD + ch
-                           : nullptr;
+    // the saves go through a buffer range over the wave's two state rows of
+    // the chunk: lanes past the last channel, and a second state past N,
+    // get offsets outside it (the launch keeps 2 * hsD * 4 bytes < 2^31)
+    float* const hc0 = save ? h_chunks + ((size_t)b * p.nchunks + Tbeg / kChunk) * cstride +
+                                  (size_t)(2 * w) * hsD
+                            : nullptr;
     const bool ok0 = ch_ok && 2 * w < N, ok1 = ch_ok && 2 * w + 1 < N;
-    float* const dummyf = static_cast<float*>(dummy);
+    const uint32_t hoff0 = ok0 ? (uint32_t)ch * 4u : kOffDrop;
+    const uint32_t hoff1 = ok1 ? (uint32_t)(hsD + ch) * 4u : kOffDrop;
 
     // block 0 of a tile: read at the end of the previous tile
     BC2 bcb[2];
     float4 dlb[2], dub[2];
     auto read_block = [&](int buf, int k, BC2& bc, float4& dl4, float4& du4) {
       lds_bc_block(sBC[buf][w], 4 * k, bc);
-      dl4 = sDl[buf][k][lane ^ ws_swz(k)];
-      du4 = sDu[buf][k][lane ^ ws_swz(k)];
+      const float4* __restrict__ st = &sSt[buf][0][0][lane];
+      dl4 = st[k * kWsRow];
+      du4 = st[(kT4 + k) * kWsRow];
     };
     // as many barriers as the producers: 1 + 4 * ceil(ntiles / 4)
     const int nbar = 1 + 4 * ((ntiles + 3) / 4);
@@ -637,7 +638,7 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       if (i >= ntiles) continue;
       if (i == 0) read_block(0, 0, bcb[0], dlb[0], dub[0]);
       const int nbuf = buf == kWsStage - 1 ? 0 : buf + 1;
-      float4* __restrict__ cY = sY[i & 1][w][0];
+      float4* __restrict__ cY = &sY[i & 1][w][0][lane];
       // block k+1's LDS reads are issued before block k is computed; after
       // the last block, the next tile's first block (staged one iteration
       // ago, so complete since this tile's barrier)
@@ -648,15 +649,15 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
         else read_block(nbuf, 0, bcb[c ^ 1], dlb[c ^ 1], dub[c ^ 1]);
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         fwd_block(dlb[c], dub[c], bcb[c], A2, h, y);
-        cY[k * kBlockCh + (lane ^ ws_swz(k))] = make_float4(y[0], y[1], y[2], y[3]);
+        cY[k * kWsRow] = make_float4(y[0], y[1], y[2], y[3]);
       }
       // kT4 is even: the next tile's block 0 sits in buffer 0 again
       static_assert(kT4 % 2 == 0, "block 0 of every tile in register set 0");
       if (save) {
         // layout (batch, nchunks, nstate, dim): one contiguous 256 B run per state
-        float* const q = hc + (size_t)i * cstride;
-        *(ok0 ? q : dummyf) = h[0];
-        *(ok1 ? q + hsD : dummyf) = h[1];
+        const auto hr = raw_rsrc(hc0 + (size_t)i * cstride, (uint32_t)(2 * hsD * sizeof(float)));
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h[0]), hr, (int)hoff0, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h[1]), hr, (int)hoff1, 0, 0);
       }
       buf = nbuf;
     }
@@ -673,7 +674,6 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   const int pt = (w - kWsCons) * 64 + lane;
   const int row = pt / kT4;
   const int q = pt % kT4;
-  const int sw = row ^ ws_swz(q);  // LDS slot of this row in column q
   const int pch = d0 + row;
   const bool pch_ok = pch < Dm;
   const float Dv = (pch_ok && Dp) ? Dp[pch] : 0.0f;
@@ -748,8 +748,8 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) du[j] = de[j] * uv[j];
-    sDl[sb][q][sw] = make_float4(de[0], de[1], de[2], de[3]);
-    sDu[sb][q][sw] = make_float4(du[0], du[1], du[2], du[3]);
+    sSt[sb][0][q][row] = make_float4(de[0], de[1], de[2], de[3]);
+    sSt[sb][1][q][row] = make_float4(du[0], du[1], du[2], du[3]);
     reinterpret_cast<float2*>(&sBC[sb][bc_G][bc_step])[bc_half] =
         bc_ok ? make_float2(to_f32(r.B), to_f32(r.C)) : make_float2(0.0f, 0.0f);
   };
@@ -767,7 +767,7 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   // same iteration, added after it) in a fixed order, D*u, the gate, stores
   auto finish_read = [&](int i, float4 (&v)[kWsCons]) {
 #pragma unroll
-    for (int ww = 0; ww < kWsCons; ++ww) v[ww] = sY[i & 1][ww][q][sw];
+    for (int ww = 0; ww < kWsCons; ++ww) v[ww] = sY[i & 1][ww][q][row];
   };
   auto finish = [&](int i, const float4 (&v)[kWsCons], const float (&sk)[4],
                     const float (&gt)[4]) {
@@ -1171,10 +1171,12 @@ hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t
   return hipGetLastError();
 }
 
-// The role-split forward serves N <= 16 when a wave's 16 rows of output fit
-// a buffer range (16 * L * elem < 2^31); the general kernel serves the rest.
+// The role-split forward serves N <= 16 when its buffer ranges fit 2^31
+// bytes (a wave's 16 rows of output, 16 * L * elem, and a wave's two saved
+// state rows, 2 * hs * dim * 4); the general kernel serves the rest.
 static bool ws_forward(const ScanParams& p, size_t elem) {
-  return p.nstate <= 16 && (size_t)(kBlockCh / kWsProd) * p.seqlen * elem < (1u << 31);
+  return p.nstate <= 16 && (size_t)(kBlockCh / kWsProd) * p.seqlen * elem < (1u << 31) &&
+         (size_t)2 * p.hs * p.dim * sizeof(float) < (1u << 31);
 }
 
 template <typename T, int kSG, int kZ, bool kAligned>

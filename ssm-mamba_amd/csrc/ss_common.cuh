@@ -21,6 +21,12 @@ constexpr float kLn2 = 0.6931471805599453f;
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// one stored element to fp32
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(__hip_bfloat16 x) {
+  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, x) << 16);
+}
+
 typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
 typedef float f32x2_v __attribute__((ext_vector_type(2)));
 
