@@ -541,6 +541,368 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   }
 }
 
+// ---------------------------------------------------------------- backward, N <= 16
+
+// Role-split backward for up to 16 states, the counterpart of the forward's
+// role split.  A workgroup of 12 waves covers one batch row b x 64 channels
+// and walks its segment's 16-step tiles from the end:
+//   consumer waves 0..7   lane = channel, wave w = states 2w and 2w+1: take
+//                         the state the forward saved before the tile,
+//                         recompute the tile's 16 states and decays, run the
+//                         reverse recurrence, leave the per-position sums
+//                         over the wave's states (sum_n G B, sum_n A G a h) in
+//                         the wave's LDS slices, and write the dB / dC terms
+//                         summed over the 64 channels;
+//   producer waves 8..11  lane -> (channel row, 4-step column): stage the next
+//                         tile (delta and softplus'(x) once per element,
+//                         delta * u, the masked and gated dout, B and C) and
+//                         write its dz; finish the previous tile (the eight
+//                         slices of each sum added in a fixed order, du,
+//                         ddelta, the dD and dbias accumulators).
+// One barrier per tile; the staging buffers and the slices alternate between
+// two LDS buffers by tile parity (159,744 bytes in all).  The arithmetic and
+// its order are those of scan_bwd_kernel; the outputs agree bit for bit with
+// that kernel's except where the compiler contracts a multiply and an add
+// differently (the dbias accumulator).  Three waves per SIMD need at most 168
+// VGPRs: the producers keep u as loaded and softplus'(x) for a tile's finish
+// and read delta and dout back from the staging buffer before overwriting it.
+constexpr int kBwsRing = 2;  // producer register ring of raw rows, in tiles (a tile takes microseconds)
+
+// LDS slot of column q of channel row r in the role-split backward: r ^
+// bws_swz(q).  The producers' 8-lane groups of a 128-bit access (rows r, r+1
+// x columns 0..3) then touch 8 distinct 16-byte bank groups; the consumers'
+// whole-column accesses are permutations of 64 consecutive float4s.
+__device__ __forceinline__ constexpr int bws_swz(int q) { return 2 * q + 8 * (q & 1); }
+
+template <typename T>
+struct BwsRows {  // one tile's raw loads of a producer lane, as loaded
+  typename Raw4<T>::type u, d, dy, z, y;
+  T B, C;
+};
+
+template <typename T, bool kHasZ, bool kAligned>
+__global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
+    const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
+    const float* __restrict__ Ap, const T* __restrict__ Bp, const T* __restrict__ Cp,
+    const float* __restrict__ Dp, const float* __restrict__ biasp,
+    const float* __restrict__ h_init, const int64_t* __restrict__ length,
+    const T* __restrict__ zp, const T* __restrict__ yup, const float* __restrict__ h_chunks,
+    const T* __restrict__ dyp, const float* __restrict__ dh_last, T* __restrict__ dup,
+    T* __restrict__ ddp, T* __restrict__ dzp, float* __restrict__ dh_init,
+    float* __restrict__ ws_bc, float* __restrict__ ws_A, float* __restrict__ ws_D,
+    float* __restrict__ ws_bias, void* __restrict__ dummy, const float* __restrict__ seg_g,
+    const float* __restrict__ seg_dt) {
+  constexpr int kT4 = kTileB / 4;  // 4-step columns per tile
+  static_assert(kTileB == kChunk, "one saved state per backward tile");
+  static_assert(kWsProd * 64 == kBlockCh * kT4, "one producer lane per (row, column)");
+  static_assert(2 * 2 * kWsCons * kTileB == 2 * 64 * kWsProd, "two B/C elements per producer lane");
+
+  __shared__ float4 sSt[2][3][kT4][kBlockCh];     // [parity][delta | delta*u | dout][column][row]
+  __shared__ float sBlk[2][kWsCons][kT4][16];     // [parity][pair][block][(step, state, B|C)]
+  __shared__ float4 sGB[2][kWsCons][kT4][kBlockCh];  // per-wave sum_n G B
+  __shared__ float4 sDD[2][kWsCons][kT4][kBlockCh];  // per-wave sum_n A G a h_{t-1}
+
+  const int lane = threadIdx.x & 63;
+  const int w = wave_id_uniform();
+  const int b = blockIdx.y;
+  const int blk = blockIdx.x;
+  const int d0 = blk * kBlockCh;
+  const int L = p.seqlen, Dm = p.dim, N = p.nstate;
+  const int seg = blockIdx.z;
+  const int ntiles_all = (L + kTileB - 1) / kTileB;
+  const int tile_beg = seg * (p.seg_len / kTileB);
+  const int tile_end = min(ntiles_all, tile_beg + p.seg_len / kTileB);
+  const int nt = tile_end - tile_beg;  // tiles of this segment, walked from the end
+  const int nbar = 1 + 4 * ((nt + 3) / 4);  // barriers of both roles
+  const size_t srow = (size_t)seg * p.batch + b;
+  const size_t rb = (size_t)b * Dm;
+
+  if (w < kWsCons) {
+    // ------------------------------------------------ consumer: the recurrences
+    const int ch = d0 + lane;
+    const bool ch_ok = ch < Dm;
+    const int chc = min(ch, Dm - 1);
+    const size_t nBC = (size_t)p.batch * N * L;
+    float* const dummyf = static_cast<float*>(dummy);
+    float gam[2], dA[2], Av[2], A2[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int n = 2 * w + s;
+      const bool ok = ch_ok && n < N;
+      dA[s] = 0.0f;
+      Av[s] = ok ? Ap[(size_t)ch * N + n] : 0.0f;
+      A2[s] = Av[s] * kLog2e;
+      // carry in from the later segments, last first:
+      // gamma <- gamma_seg + exp(A sum dt) gamma (their summaries, zero carry-in)
+      float q = (ok && dh_last) ? dh_last[(rb + ch) * N + n] : 0.0f;
+      for (int sp = p.nseg - 1; ok && sp > seg; --sp) {
+        const size_t sb = (size_t)(sp - 1) * p.batch + b;
+        q = fmaf(fast_exp2(A2[s] * seg_dt[sb * Dm + ch]), q, seg_g[(sb * N + n) * Dm + ch]);
+      }
+      gam[s] = q;
+    }
+    // the state the forward saved before tile t (h_init, or zero, before tile 0)
+    auto saved_state = [&](int tile, float (&r)[2]) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int nc = min(2 * w + s, N - 1);
+        const float* src =
+            tile > 0 ? h_chunks + (((size_t)b * p.nchunks + (tile - 1)) * N + nc) * p.hs * (size_t)Dm + chc
+                     : (h_init ? h_init + (rb + chc) * N + nc : h_chunks);
+        r[s] = *src;
+      }
+    };
+    float hcn[2];
+    saved_state(tile_end - 1, hcn);
+    const int vi = lane >> 2;  // the value of lane l after the reduction: index l >> 2
+    const int rkind = vi >> 3, rs = (vi >> 2) & 1, rj = vi & 3;
+    const int rn = 2 * w + rs;
+    float* const wsb = ws_bc + ((size_t)rkind * p.nblk + blk) * nBC + ((size_t)b * N + rn) * L;
+    const bool hc_ok0 = ch_ok && 2 * w < N, hc_ok1 = ch_ok && 2 * w + 1 < N;
+
+    for (int i = 0; i < nbar; ++i) {
+      __syncthreads();
+      if (i >= nt) continue;
+      const int tile = tile_end - 1 - i;
+      const int t0 = tile * kTileB;
+      const int buf = i & 1;
+      float hc[2];
+      hc[0] = (hc_ok0 && (tile > 0 || h_init)) ? hcn[0] : 0.0f;
+      hc[1] = (hc_ok1 && (tile > 0 || h_init)) ? hcn[1] : 0.0f;
+      saved_state(max(tile - 1, tile_beg), hcn);  // the next tile's (re-read at the last)
+
+      float a[2][kChunk], H[2][kChunk];
+      StepVals X, Y;
+      float bcg[kT4];  // block registers of the wave's pair: lane l holds value l & 15
+#pragma unroll
+      for (int jq = 0; jq < kT4; ++jq) bcg[jq] = sBlk[buf][w][jq][lane & 15];
+      auto put4 = [&](float4 (&slice)[kT4][kBlockCh], int q, const float (&v)[4]) {
+        slice[q][lane ^ bws_swz(q)] = make_float4(v[0], v[1], v[2], v[3]);
+      };
+      auto fwd = [&](int jq, const StepVals& sv) {
+        float y[4];  // unused here (the forward saved the output)
+        bwd_recompute_block(jq, sv, bcg[jq], A2, hc, a, H, y);
+      };
+      auto rev = [&](int jq, const StepVals& sv) {
+        float gB[4], gD[4], vals[16];
+        bwd_reverse_block(jq, sv, bcg[jq], Av, A2, hc, a, H, gam, dA, vals, gB, gD);
+        put4(sGB[buf][w], jq, gB);
+        put4(sDD[buf][w], jq, gD);
+        // sum over the 64 channels of this block
+        wave_reduce16(vals, lane);
+        const int t = t0 + 4 * jq + rj;
+        *((rn < N && t < L) ? wsb + t : dummyf) = vals[0];
+      };
+      auto ld = [&](int jq, StepVals& sv, bool with_dout) {
+        const int li = lane ^ bws_swz(jq);
+        sv.dl = sSt[buf][0][jq][li];
+        sv.du = sSt[buf][1][jq][li];
+        if (with_dout) sv.dout = sSt[buf][2][jq][li];
+      };
+      // fixed schedule F0 F1 F2 F3 R3 R2 R1 R0 (recompute, then reverse)
+      ld(0, X, false); fwd(0, X);
+      ld(1, Y, false); fwd(1, Y);
+      ld(2, X, false); fwd(2, X);
+      ld(3, Y, true);  fwd(3, Y);
+      rev(3, Y);
+      ld(2, X, true); rev(2, X);
+      ld(1, Y, true); rev(1, Y);
+      ld(0, X, true); rev(0, X);
+    }
+    // per-row partials
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int n = 2 * w + s;
+      if (ch_ok && n < N) {
+        ws_A[(srow * Dm + ch) * N + n] = dA[s];
+        if (dh_init && seg == 0) dh_init[(rb + ch) * N + n] = gam[s];
+      }
+    }
+    return;
+  }
+
+  // ------------------------------------------------ producer: staging and per-position gradients
+  const int pt = (w - kWsCons) * 64 + lane;
+  const int row = pt / kT4;
+  const int q = pt % kT4;
+  const int sw = row ^ bws_swz(q);
+  const int pch = d0 + row;
+  const bool pch_ok = pch < Dm;
+  const int chc = min(pch, Dm - 1);
+  const float Dv = (pch_ok && Dp) ? Dp[pch] : 0.0f;
+  const float Bias = (pch_ok && biasp) ? biasp[pch] : 0.0f;
+  const T* __restrict__ u_row = u + (rb + chc) * L;
+  const T* __restrict__ d_row = dl + (rb + chc) * L;
+  const T* __restrict__ dy_row = dyp + (rb + chc) * L;
+  const T* __restrict__ z_row = kHasZ ? zp + (rb + chc) * L : u_row;
+  const T* __restrict__ y_row = kHasZ ? yup + (rb + chc) * L : u_row;
+  int vlo, vhi;
+  valid_window(length, p.pad_right, b, L, vlo, vhi);
+  const bool softplus = p.softplus != 0;
+  const uint32_t okm = pch_ok ? 0xffffffffu : 0u;
+  // B/C staging: lane pt -> state n = (pt / 16) % 16 and step pt % 16 of B
+  // (first element) and of C (second)
+  const int bc_n = (pt / kTileB) % (2 * kWsCons);
+  const int bc_j = pt % kTileB;
+  const bool bc_ok = bc_n < N;
+  const size_t bc_row = (size_t)b * p.bc_bstride + (size_t)min(bc_n, N - 1) * L;
+  const T* __restrict__ B_row = Bp + bc_row;
+  const T* __restrict__ C_row = Cp + bc_row;
+  const int bc_slot = (bc_j & 3) * 4 + (bc_n & 1) * 2;  // B; C at + 1
+  // tile index of iteration i (clamped to the segment: tiles past it are
+  // staged from valid rows and never used)
+  auto tile_of = [&](int i) { return max(tile_end - 1 - i, tile_beg); };
+
+  auto issue = [&](BwsRows<T>& r, int i) {
+    const int t = tile_of(i) * kTileB + 4 * q;
+    r.u = load_raw4_nb<T, kAligned>(u_row, t, L, pch_ok);
+    r.d = load_raw4_nb<T, kAligned>(d_row, t, L, pch_ok);
+    r.dy = load_raw4_nb<T, kAligned>(dy_row, t, L, pch_ok);
+    if constexpr (kHasZ) {
+      r.z = load_raw4_nb<T, kAligned>(z_row, t, L, pch_ok);
+      r.y = load_raw4_nb<T, kAligned>(y_row, t, L, pch_ok);
+    } else {
+      r.z = r.y = typename Raw4<T>::type{};
+    }
+    const int tb = min(tile_of(i) * kTileB + bc_j, L - 1);
+    r.B = B_row[tb];
+    r.C = C_row[tb];
+  };
+
+  // What a tile's finish needs from its staging besides delta and dout (read
+  // back from the staging buffer before the next staging overwrites it): u as
+  // loaded and softplus'(x) (zero where masked).
+  struct Kept {
+    typename Raw4<T>::type u;
+    float sg[4];
+  };
+
+  // stage iteration i's tile into buffer i & 1 and write its dz
+  auto stage = [&](const BwsRows<T>& r, int i, Kept& k) {
+    const int tile = tile_of(i);
+    const int t0 = tile * kTileB;
+    const int t = t0 + 4 * q;
+    const int sb = i & 1;
+    float uv[4], dv[4], dyv[4];
+    decode4(r.u, uv);
+    decode4(r.d, dv);
+    decode4(r.dy, dyv);
+    uint32_t keep[4] = {okm, okm, okm, okm};
+    if (!(t0 >= vlo && t0 + kTileB <= vhi)) {  // tiles wholly inside the window skip this
+#pragma unroll
+      for (int j = 0; j < 4; ++j) keep[j] = (pch_ok && t + j >= vlo && t + j < vhi) ? ~0u : 0u;
+    }
+    float de[4], du[4], dov[4], dzo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x = dv[j] + Bias;
+      float sp, g;
+      softplus_and_grad_t20(x, sp, g);
+      de[j] = __uint_as_float(__float_as_uint(softplus ? sp : x) & keep[j]);
+      k.sg[j] = __uint_as_float(__float_as_uint(softplus ? g : 1.0f) & keep[j]);
+      du[j] = de[j] * uv[j];
+      const float dym = __uint_as_float(__float_as_uint(dyv[j]) & keep[j]);
+      if constexpr (kHasZ) {
+        float zv[4], yv[4];
+        decode4(r.z, zv);
+        decode4(r.y, yv);
+        const float sz = sigmoidf_fast(zv[j]);
+        dov[j] = dym * (zv[j] * sz);
+        dzo[j] = dym * yv[j] * (sz * fmaf(zv[j], 1.0f - sz, 1.0f));
+      } else {
+        dov[j] = dym;
+        dzo[j] = 0.0f;
+      }
+    }
+    k.u = r.u;
+    sSt[sb][0][q][sw] = make_float4(de[0], de[1], de[2], de[3]);
+    sSt[sb][1][q][sw] = make_float4(du[0], du[1], du[2], du[3]);
+    sSt[sb][2][q][sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
+    float* const blk_dst = &sBlk[sb][bc_n >> 1][bc_j >> 2][bc_slot];
+    blk_dst[0] = bc_ok ? to_f32(r.B) : 0.0f;
+    blk_dst[1] = bc_ok ? to_f32(r.C) : 0.0f;
+    // a tile past the segment (i >= nt) writes nothing
+    const bool st_ok = pch_ok && i < nt;
+    if constexpr (kHasZ) store4_nb<T, kAligned>(dzp + (rb + pch) * L, t, L, st_ok, dummy, dzo);
+  };
+
+  float accD = 0.0f, accB = 0.0f;
+  // finish iteration i's tile: slices of parity i & 1
+  auto finish = [&](int i, const Kept& k) {
+    const int tile = tile_of(i);
+    const int t = tile * kTileB + 4 * q;
+    const int sb = i & 1;
+    float4 gb = sGB[sb][0][q][sw], gd = sDD[sb][0][q][sw];
+#pragma unroll
+    for (int ww = 1; ww < kWsCons; ++ww) {
+      const float4 q1 = sGB[sb][ww][q][sw];
+      gb.x += q1.x; gb.y += q1.y; gb.z += q1.z; gb.w += q1.w;
+    }
+#pragma unroll
+    for (int ww = 1; ww < kWsCons; ++ww) {
+      const float4 q2 = sDD[sb][ww][q][sw];
+      gd.x += q2.x; gd.y += q2.y; gd.z += q2.z; gd.w += q2.w;
+    }
+    const float gbv[4] = {gb.x, gb.y, gb.z, gb.w};
+    const float gdv[4] = {gd.x, gd.y, gd.z, gd.w};
+    float de[4], dov[4], uu[4];
+    f4_to(sSt[sb][0][q][sw], de);
+    f4_to(sSt[sb][2][q][sw], dov);
+    decode4(k.u, uu);
+    float duo[4], ddo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      duo[j] = fmaf(Dv, dov[j], de[j] * gbv[j]);
+      ddo[j] = fmaf(uu[j], gbv[j], gdv[j]) * k.sg[j];  // sg is 0 at padded steps
+    }
+    const bool ok = i < nt;
+    if (ok) {  // no memory operations inside
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        accD = fmaf(dov[j], uu[j], accD);  // dov is 0 at padded steps
+        accB += ddo[j];
+      }
+    }
+    store4_nb<T, kAligned>(dup + (rb + pch) * L, t, L, ok && pch_ok, dummy, duo);
+    store4_nb<T, kAligned>(ddp + (rb + pch) * L, t, L, ok && pch_ok, dummy, ddo);
+  };
+
+  // Iteration i after barrier i: finish tile i-1 (its slices were written
+  // during iteration i-1), then stage tile i+1 into the buffer tile i-1 used.
+  // Raw rows travel in a ring of kBwsRing tiles (tile k's loads are issued
+  // when tile k - kBwsRing is staged); what a finish needs rides in a ring of
+  // 4 tiles (staged at iteration k - 1, finished at k + 1).  Iterations
+  // 1 .. 4m run in unrolled groups of four with no conditions around memory
+  // operations, so the compiler's waits for the ring's loads count exactly.
+  BwsRows<T> rows[kBwsRing];
+  Kept kept[4];
+#pragma unroll
+  for (int k2 = 0; k2 < kBwsRing; ++k2) issue(rows[k2], k2);
+  stage(rows[0], 0, kept[0]);
+  issue(rows[0], kBwsRing);
+  __syncthreads();  // iteration 0
+  stage(rows[1], 1, kept[1]);
+  issue(rows[1], kBwsRing + 1);
+  for (int i0 = 1; i0 < nbar; i0 += 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j;  // (i + 1) % 4 == (j + 2) % 4, (i - 1) % 4 == j
+      __syncthreads();
+      finish(i - 1, kept[j]);
+      stage(rows[(j + 2) % kBwsRing], i + 1, kept[(j + 2) & 3]);
+      issue(rows[(j + 2) % kBwsRing], i + 1 + kBwsRing);
+    }
+  }
+  // dD from dout * u, dbias from ddelta: the 4 lanes of a row are
+  // consecutive
+  const float sd = group_sum<kT4>(accD);
+  const float sbias = group_sum<kT4>(accB);
+  if (pch_ok && q == 0) {
+    ws_D[srow * Dm + pch] = sd;
+    ws_bias[srow * Dm + pch] = sbias;
+  }
+}
+
 // ---------------------------------------------------------------- state chunks
 
 // After the kPart backward: per (batch row b, channel d), the per-position
@@ -868,6 +1230,16 @@ static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t 
     if (e != hipSuccess) return e;
   }
   dim3 grid(p.nblk, p.batch, p.nseg * nsc);
+  if constexpr (kSG == 1 && !kPart) {
+    ProfScope prof("scan_bwd", st);
+    hipLaunchKernelGGL((scan_bwd_ws_kernel<T, kHasZ, kAligned>), grid, dim3(kWsThreads), 0, st,
+                       dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, (const T*)p.B,
+                       (const T*)p.C, p.D, p.bias, p.h_init, p.length, (const T*)p.z,
+                       (const T*)p.out_ungated, p.h_chunks_in, (const T*)p.dout, p.dh_last,
+                       (T*)p.du, (T*)p.ddelta, (T*)p.dz, p.dh_init, p.ws_bc, p.ws_A, p.ws_D,
+                       p.ws_bias, p.dummy, p.seg_h, p.seg_dt);
+    return hipGetLastError();
+  }
   {
     ProfScope prof("scan_bwd", st);
     hipLaunchKernelGGL((scan_bwd_kernel<T, kSG, kHasZ, kAligned, kPart>), grid, dim3(kThreads), 0,

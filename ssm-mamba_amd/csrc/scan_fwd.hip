@@ -534,9 +534,6 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
 // delta = 0 (identity steps), so the saved state of a partial last chunk is
 // the state at its last real step, and their outputs are never stored.
 constexpr int kWsTile = 16;   // steps per tile
-constexpr int kWsCons = 8;    // consumer waves
-constexpr int kWsProd = 4;    // producer waves
-constexpr int kWsThreads = 64 * (kWsCons + kWsProd);
 constexpr int kWsStage = 3;   // staging buffers (tiles i, i+1 and i+2)
 constexpr int kWsRing = 4;    // producer register ring of raw rows, in tiles
 static_assert(kWsTile == kChunk, "a tile is one saved chunk");

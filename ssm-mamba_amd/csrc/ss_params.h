@@ -21,6 +21,11 @@ constexpr int kTileB = 16;    // steps staged through LDS per backward tile
 constexpr int kBlockCh = 64;  // channels per workgroup (one per lane)
 constexpr int kWaves = 8;     // waves per workgroup; wave w owns state pairs G = g*8 + w
 constexpr int kThreads = 64 * kWaves;
+// role-split kernels (N <= 16): consumer waves run the recurrences, producer
+// waves stage tiles and finish per-position outputs
+constexpr int kWsCons = 8;    // consumer waves: state pair w
+constexpr int kWsProd = 4;    // producer waves: (channel row, 4-step column) per lane
+constexpr int kWsThreads = 64 * (kWsCons + kWsProd);
 
 // Scalar shape/flag block passed to the scan kernels (pointers travel as
 // separate __restrict__ kernel arguments).
