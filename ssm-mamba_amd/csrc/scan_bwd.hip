@@ -752,6 +752,16 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
   // tile index of iteration i (clamped to the segment: tiles past it are
   // staged from valid rows and never used)
   auto tile_of = [&](int i) { return max(tile_end - 1 - i, tile_beg); };
+  // Output buffers of this wave's 16 channel rows (aligned path; the launch
+  // keeps 16 * L * sizeof(T) < 2^31): a masked lane, a step past L or a tile
+  // past the segment gets an offset outside the range and the store is dropped.
+  const int wrow0 = d0 + (w - kWsCons) * (kBlockCh / kWsProd);
+  const uint32_t wbytes =
+      (uint32_t)(max(0, min(kBlockCh / kWsProd, Dm - wrow0)) * (size_t)L * sizeof(T));
+  const auto du_rsrc = raw_rsrc(dup + ((size_t)rb + wrow0) * L, wbytes);
+  const auto dd_rsrc = raw_rsrc(ddp + ((size_t)rb + wrow0) * L, wbytes);
+  const auto dz_rsrc = raw_rsrc(kHasZ ? dzp + ((size_t)rb + wrow0) * L : dup, kHasZ ? wbytes : 0u);
+  const uint32_t row_off = (uint32_t)((row % (kBlockCh / kWsProd)) * (size_t)L * sizeof(T));
 
   auto issue = [&](BwsRows<T>& r, int i) {
     const int t = tile_of(i) * kTileB + 4 * q;
@@ -823,7 +833,13 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
     blk_dst[1] = bc_ok ? to_f32(r.C) : 0.0f;
     // a tile past the segment (i >= nt) writes nothing
     const bool st_ok = pch_ok && i < nt;
-    if constexpr (kHasZ) store4_nb<T, kAligned>(dzp + (rb + pch) * L, t, L, st_ok, dummy, dzo);
+    if constexpr (kHasZ) {
+      if constexpr (kAligned)
+        buffer_store4<T>(dz_rsrc, (i < nt && t < L) ? row_off + (uint32_t)t * sizeof(T) : kOffDrop,
+                         dzo);
+      else
+        store4_nb<T, kAligned>(dzp + (rb + pch) * L, t, L, st_ok, dummy, dzo);
+    }
   };
 
   float accD = 0.0f, accB = 0.0f;
@@ -863,8 +879,14 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
         accB += ddo[j];
       }
     }
-    store4_nb<T, kAligned>(dup + (rb + pch) * L, t, L, ok && pch_ok, dummy, duo);
-    store4_nb<T, kAligned>(ddp + (rb + pch) * L, t, L, ok && pch_ok, dummy, ddo);
+    if constexpr (kAligned) {
+      const uint32_t off = (ok && t < L) ? row_off + (uint32_t)t * sizeof(T) : kOffDrop;
+      buffer_store4<T>(du_rsrc, off, duo);
+      buffer_store4<T>(dd_rsrc, off, ddo);
+    } else {
+      store4_nb<T, kAligned>(dup + (rb + pch) * L, t, L, ok && pch_ok, dummy, duo);
+      store4_nb<T, kAligned>(ddp + (rb + pch) * L, t, L, ok && pch_ok, dummy, ddo);
+    }
   };
 
   // Iteration i after barrier i: finish tile i-1 (its slices were written
@@ -1230,7 +1252,9 @@ static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t 
     if (e != hipSuccess) return e;
   }
   dim3 grid(p.nblk, p.batch, p.nseg * nsc);
-  if constexpr (kSG == 1 && !kPart) {
+  // the role-split kernel's output buffer ranges (a wave's 16 rows) must fit
+  // 2^31 bytes
+  if (kSG == 1 && !kPart && (size_t)(kBlockCh / kWsProd) * p.seqlen * sizeof(T) < (1u << 31)) {
     ProfScope prof("scan_bwd", st);
     hipLaunchKernelGGL((scan_bwd_ws_kernel<T, kHasZ, kAligned>), grid, dim3(kWsThreads), 0, st,
                        dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, (const T*)p.B,
