@@ -297,6 +297,60 @@ int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank
                         const void* dt_bias, const void* log_A, const void* D, const void* xc,
                         const void* xz, int64_t ld_xz, float* state, void* y, void* stream);
 
+/*
+ * The token step of a whole stack of Mamba blocks in one launch: for each of
+ * nlayers layers in turn, x <- x + Mamba.step(rmsnorm(x)) (Block.step,
+ * modules/block.py:78-90, over the layers as models/causal_lm.py:92-93
+ * loops): the work of ssm_decode_in_proj_conv (folded x-projection),
+ * ssm_decode_ssm_step and the residual ssm_decode_gemv, with the
+ * out-projection's dot products summed in K-slices and the state update's
+ * sums split over thread pairs (each a fixed order: the results are
+ * deterministic and agree with those calls to fp32 rounding, not bit for
+ * bit).  No counterpart call in the reference.
+ *
+ * One persistent grid runs the three phases of every layer; its workgroups
+ * pass activations to each other through the workspace, each waiting for the
+ * data it reads, so every workgroup must be resident at once
+ * (SSM_ERR_UNSUPPORTED otherwise, before anything runs): do not run other
+ * work on the device at the same time.  Shapes: nstate = 16, the in- and
+ * out-projections in one pass each (model_dim <= 1024 and dim <= 2048 for
+ * bf16, half that for fp32) and at most 8 x-projection partial blocks per
+ * state-update thread (SSM_ERR_UNSUPPORTED otherwise).
+ *
+ * layer_table: device memory, nlayers rows of SSM_LAYER_NPTR pointers in the
+ * order of the enum below (NULL allowed for the biases, dt_bias and D; the
+ * others 16-byte aligned, the state fp32).  Shapes: in_proj_weight (2*dim,
+ * model_dim), norm_weight (model_dim), conv_weight (dim, width), x_proj_weight
+ * (rank + 2*nstate, dim), dt_proj_weight (dim, rank), log_A (dim, nstate),
+ * out_proj_weight (model_dim, dim), conv_window (batch, dim, width-1), state
+ * (batch, dim, nstate).  x, out: (batch, model_dim); out may be x.
+ * rank a multiple of 16 bytes of elements, at most 16 such;
+ * ssm_decode_xproj_blocks(dim, rank + 2*nstate) > 0; 2 <= width <= 4.
+ *
+ * workspace: at least ssm_decode_layers_workspace(...) bytes (it grows with
+ * nlayers: each layer has its own hand-off buffers), 256-byte aligned,
+ * zero-filled before its first use and then left to the launches (it holds a
+ * launch counter); one workspace per stream of launches.  Every wait is
+ * bounded: should one ever time out, the launch and every later launch on
+ * the workspace do nothing further until ssm_decode_layers_status reports it
+ * (SSM_ERR_HIP) and zero-fills the workspace.
+ */
+enum {
+  SSM_LAYER_IN_PROJ_W = 0, SSM_LAYER_IN_PROJ_B, SSM_LAYER_NORM_W, SSM_LAYER_CONV_W,
+  SSM_LAYER_CONV_B, SSM_LAYER_X_PROJ_W, SSM_LAYER_DT_PROJ_W, SSM_LAYER_DT_BIAS, SSM_LAYER_LOG_A,
+  SSM_LAYER_D, SSM_LAYER_OUT_PROJ_W, SSM_LAYER_OUT_PROJ_B, SSM_LAYER_CONV_WINDOW, SSM_LAYER_STATE,
+  SSM_LAYER_NPTR
+};
+int64_t ssm_decode_layers_workspace(int64_t batch, int64_t nlayers, int64_t model_dim,
+                                    int64_t dim, int64_t params_dim, int dtype);
+int ssm_decode_layers(int64_t batch, int64_t nlayers, int64_t model_dim, int64_t dim, int64_t nstate,
+                      int64_t rank, int64_t width, int dtype, const void* layer_table, const void* x,
+                      void* out, float norm_eps, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+/* Synchronises the stream; SSM_OK, or SSM_ERR_HIP after a wait timed out
+ * (the workspace is zero-filled then). */
+int ssm_decode_layers_status(void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

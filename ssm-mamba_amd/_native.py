@@ -97,13 +97,20 @@ SIGNATURES = {
         _p, _p, _i64,                          # xc, xz, ld_xz
         _p, _p, _p,                            # state, y, stream
     ]),
+    "ssm_decode_layers_workspace": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32]),
+    "ssm_decode_layers": (_i32, [
+        _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32,  # batch, nlayers, model_dim, dim, nstate, rank, width, dtype
+        _p, _p, _p, ctypes.c_float,            # layer_table, x, out, norm_eps
+        _p, _i64, _p,                          # workspace, workspace_bytes, stream
+    ]),
+    "ssm_decode_layers_status": (_i32, [_p, _i64, _p]),
     "ssm_rms_norm_cm": (_i32, [
         _i64, _i64, _i64, _i32,                # batch, channels, seqlen, dtype
         _p, _p, ctypes.c_float, _p, _p,        # x, weight, eps, out, stream
     ]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 def lib() -> ctypes.CDLL:

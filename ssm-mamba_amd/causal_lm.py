@@ -435,8 +435,14 @@ class CausalLM(nn.Module):
     def step(self, input_ids: torch.Tensor) -> torch.Tensor:
         """input_ids (batch,) -> logits (batch, vocab), advancing every cache."""
         x = self.embedding(input_ids)
-        for layer in self.layers:
-            x = layer.step(x)
+        if _dec.layers_supported(self.layers, x):
+            # every layer's step in one launch
+            x = _dec.layers_step(self, self.layers, x)
+            if not torch.cuda.is_current_stream_capturing():
+                _dec.layers_check(self)
+        else:
+            for layer in self.layers:
+                x = layer.step(x)
         if _dec.gemv_supported(self.lm_head.weight, x, self.norm.weight):
             return _dec.gemv(self.lm_head.weight, x, norm_weight=self.norm.weight,
                              eps=self.norm.eps)
@@ -588,4 +594,5 @@ class GreedyDecoder:
                 return self.tokens[:, :self.max_new].clone()
             n = min(check_every, self.max_new - done)
             self.replay(n)
+            _dec.layers_check(self.model)
             done += n

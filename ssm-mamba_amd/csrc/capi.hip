@@ -38,6 +38,14 @@ hipError_t launch_decode_ssm_step(int bf16, const void* p, int nout, int nparts,
                                   const void* Wdt, const void* dtb, const void* logA, const void* D,
                                   const void* xc, const void* xz, int ld, float* state, void* y,
                                   int B, int dim, int nstate, bool vecR, hipStream_t st);
+int64_t decode_layers_workspace(int B, int nlayers, int K, int dim, int nout, int bf16);
+const char* decode_layers_unsupported(int K, int dim, int nout, int bf16);
+int64_t decode_layers_error_offset();
+int decode_layers_grid(int B, int K, int dim);
+int decode_layers_max_width();
+hipError_t launch_decode_layers(int bf16, const void* table, int nlayers, int B, int K, int dim,
+                                int width, int R, int nout, float eps, const void* x, void* out,
+                                void* ws, hipStream_t st);
 hipError_t launch_rms_norm_cm(int bf16, const void* x, const void* w, float eps, void* out, int B,
                               int C, int L, bool pair, hipStream_t st);
 hipError_t launch_causal_conv1d_fwd(int batch, int dim, int L, int K, int dtype_bf16,
@@ -235,7 +243,7 @@ extern "C" {
 
 const char* ssm_last_error(void) { return g_err.c_str(); }
 
-int ssm_abi_version(void) { return 6; }
+int ssm_abi_version(void) { return 7; }
 
 int ssm_profile_begin(void) {
   g_err.clear();
@@ -590,6 +598,86 @@ int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank
                                                 state, y, (int)batch, (int)dim, (int)nstate, vecR,
                                                 static_cast<hipStream_t>(stream)),
                     "decode_ssm_step launch");
+}
+
+int64_t ssm_decode_layers_workspace(int64_t batch, int64_t nlayers, int64_t model_dim, int64_t dim,
+                                    int64_t params_dim, int dtype) {
+  if (check_decode(batch, dtype) != SSM_OK || nlayers < 1 || nlayers > 65536 || model_dim < 1 ||
+      model_dim > INT_MAX / 16 || ssm::decode_xproj_blocks(dim, params_dim) == 0)
+    return 0;
+  return ssm::decode_layers_workspace((int)batch, (int)nlayers, (int)model_dim, (int)dim,
+                                      (int)params_dim, dtype == SSM_BF16);
+}
+
+int ssm_decode_layers(int64_t batch, int64_t nlayers, int64_t model_dim, int64_t dim, int64_t nstate,
+                      int64_t rank, int64_t width, int dtype, const void* layer_table, const void* x,
+                      void* out, float norm_eps, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
+  int rc = check_decode(batch, dtype);
+  if (rc != SSM_OK) return rc;
+  if (!layer_table || !x || !out || !workspace)
+    return fail(SSM_ERR_INVALID, "layer_table, x, out and workspace must be non-NULL");
+  if (nlayers < 1 || nlayers > 65536)
+    return fail(SSM_ERR_INVALID, "decode_layers needs 1 <= nlayers <= 65536 (got %lld)", (long long)nlayers);
+  if (nstate != 16)
+    return fail(SSM_ERR_UNSUPPORTED, "decode_layers supports nstate 16 (got %lld)", (long long)nstate);
+  const int e = elems16(dtype);
+  if (model_dim < e || model_dim % e || model_dim > INT_MAX / 16)
+    return fail(SSM_ERR_UNSUPPORTED, "decode_layers needs model_dim a positive multiple of %d", e);
+  if (rank < 1 || rank % e || rank > 8 * e)
+    return fail(SSM_ERR_UNSUPPORTED, "decode_layers needs rank a multiple of %d and at most %d (got %lld)",
+                e, 8 * e, (long long)rank);
+  const int64_t nout = rank + 2 * nstate;
+  if (dim > (1 << 24) || ssm::decode_xproj_blocks(dim, nout) == 0)
+    return fail(SSM_ERR_UNSUPPORTED,
+                "decode_layers needs the folded x-projection: ssm_decode_xproj_blocks(dim, rank + 2 * nstate) > 0");
+  if (width < 2 || width > ssm::decode_layers_max_width())
+    return fail(SSM_ERR_UNSUPPORTED, "decode_layers conv width must be in [2, %d] (got %lld)",
+                ssm::decode_layers_max_width(), (long long)width);
+  if (const char* why = ssm::decode_layers_unsupported((int)model_dim, (int)dim, (int)nout,
+                                                       dtype == SSM_BF16))
+    return fail(SSM_ERR_UNSUPPORTED, "decode_layers: %s (model_dim %lld, dim %lld, params_dim %lld)",
+                why, (long long)model_dim, (long long)dim, (long long)nout);
+  if (!aligned16(x) || !aligned16(out) || (reinterpret_cast<uintptr_t>(workspace) & 255) ||
+      (reinterpret_cast<uintptr_t>(layer_table) & 7))
+    return fail(SSM_ERR_UNSUPPORTED,
+                "decode_layers needs 16-byte aligned x and out, a 256-byte aligned workspace and an 8-byte aligned layer_table");
+  const int64_t need = ssm::decode_layers_workspace((int)batch, (int)nlayers, (int)model_dim,
+                                                    (int)dim, (int)nout, dtype == SSM_BF16);
+  if (workspace_bytes < need)
+    return fail(SSM_ERR_INVALID, "decode_layers workspace is %lld bytes, needs %lld",
+                (long long)workspace_bytes, (long long)need);
+  const hipError_t he = ssm::launch_decode_layers(dtype == SSM_BF16, layer_table, (int)nlayers,
+                                                  (int)batch, (int)model_dim, (int)dim, (int)width,
+                                                  (int)rank, (int)nout, norm_eps, x, out, workspace,
+                                                  static_cast<hipStream_t>(stream));
+  if (he == hipErrorCooperativeLaunchTooLarge)
+    return fail(SSM_ERR_UNSUPPORTED,
+                "decode_layers needs all %d workgroups resident at once, more than this device holds",
+                ssm::decode_layers_grid((int)batch, (int)model_dim, (int)dim));
+  return hip_status(he, "decode_layers launch");
+}
+
+int ssm_decode_layers_status(void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!workspace || workspace_bytes < ssm::decode_layers_error_offset() + 4)
+    return fail(SSM_ERR_INVALID, "workspace must be non-NULL and hold at least the sync area");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  unsigned err = 0;
+  // the error word of the sync area at the start of the workspace
+  const char* word = static_cast<const char*>(workspace) + ssm::decode_layers_error_offset();
+  if (int rc = hip_status(hipMemcpyAsync(&err, word, sizeof(err), hipMemcpyDeviceToHost, st),
+                          "decode_layers status copy"))
+    return rc;
+  if (int rc = hip_status(hipStreamSynchronize(st), "decode_layers status sync")) return rc;
+  if (!err) return SSM_OK;
+  if (int rc = hip_status(hipMemsetAsync(workspace, 0, (size_t)workspace_bytes, st),
+                          "decode_layers workspace reset"))
+    return rc;
+  if (int rc = hip_status(hipStreamSynchronize(st), "decode_layers workspace reset")) return rc;
+  return fail(SSM_ERR_HIP,
+              "decode_layers: a wait for another workgroup's data timed out (not every workgroup "
+              "was resident); the outputs of the launches since the last status check are "
+              "invalid, and the workspace is cleared");
 }
 
 int ssm_rms_norm_cm(int64_t batch, int64_t channels, int64_t seqlen, int dtype, const void* x,

@@ -1,7 +1,8 @@
 """Host side of the fused decode-step kernels (``ssm_decode_*`` in
 include/ssm_mamba.h): one Mamba block step per token in three launches (four
 when the x-projection cannot be folded) instead of the reference's per-op
-sequence (``modules/block.py:80-86``, ``modules/mamba.py:189-243``), plus the
+sequence (``modules/block.py:80-86``, ``modules/mamba.py:189-243``), or the
+steps of every layer of a model in one launch (``layers_step``), plus the
 LM-head GEMV with the final RMSNorm (``models/causal_lm.py:93-104``).
 
 These are inference kernels (no autograd).  ``block_step_supported`` says
@@ -26,6 +27,9 @@ ENABLED = True
 # Fold the x-projection into the in-projection and state-update kernels where
 # ssm_decode_xproj_blocks allows; False keeps it a GEMV of its own.
 FOLD_XPROJ = True
+# CausalLM.step runs all of its layers in one launch (ssm_decode_layers) where
+# layers_supported allows; False keeps three launches per layer.
+LAYER_CHAIN = True
 
 
 def _elems16(dtype: torch.dtype) -> int:
@@ -172,3 +176,121 @@ def block_step(ssm, x: torch.Tensor, norm_weight: Optional[torch.Tensor] = None,
     y = ssm_step(params, ssm.delta_rank, ssm.delta_proj.weight, ssm.delta_proj.bias, ssm.log_A,
                  ssm.D, xc, xz, ssm._ssm_hiddens)
     return gemv(ssm.out_proj.weight, y, bias=ssm.out_proj.bias, residual=x if residual else None)
+
+
+# ---- the layer chain: every layer's step in one launch ------------------------
+
+_CHAIN_STATE = 16
+_CHAIN_MAX_WIDTH = 4
+_CHAIN_MAX_BATCH = 4
+
+
+def _layer_tensors(block):
+    """The SSM_LAYER_* row of one Block, in the header's order."""
+    ssm = block.ssm
+    return [ssm.input_proj.weight, ssm.input_proj.bias, block.norm.weight, ssm.conv.weight,
+            ssm.conv.bias, ssm.ssm_param_proj.weight, ssm.delta_proj.weight, ssm.delta_proj.bias,
+            ssm.log_A, ssm.D, ssm.out_proj.weight, ssm.out_proj.bias, ssm._conv_context,
+            ssm._ssm_hiddens]
+
+
+def layers_supported(layers, x: torch.Tensor) -> bool:
+    """Whether ``layers_step`` can run the Blocks ``layers`` on the token batch
+    x: every layer qualifies for the fused step, all share one shape and norm
+    eps, the state size is 16 and the x-projection folds."""
+    if not (ENABLED and LAYER_CHAIN and FOLD_XPROJ) or torch.is_grad_enabled() or len(layers) == 0:
+        return False
+    # up to 4 rows: the 8-row variants of the kernel spill registers
+    if x.dim() != 2 or x.dtype not in _DTYPES or x.shape[0] > _CHAIN_MAX_BATCH:
+        return False
+    s0 = layers[0].ssm
+    shape = (s0.inner_dim, s0.state_dim, s0.delta_rank, s0.conv_kernel)
+    eps = layers[0].norm.eps
+    if s0.state_dim != _CHAIN_STATE or not 2 <= s0.conv_kernel <= _CHAIN_MAX_WIDTH:
+        return False
+    e = _elems16(x.dtype)
+    if s0.delta_rank % e or s0.delta_rank > 8 * e:
+        return False
+    # each projection in one pass: d_model up to 128 and d_inner up to 256
+    # 16-byte chunks of elements
+    if x.shape[1] > 128 * e or s0.inner_dim > 256 * e:
+        return False
+    if not xproj_blocks(s0.inner_dim, s0.delta_rank + 2 * s0.state_dim):
+        return False
+    for blk in layers:
+        ssm = blk.ssm
+        if (ssm.inner_dim, ssm.state_dim, ssm.delta_rank, ssm.conv_kernel) != shape \
+                or blk.norm.eps != eps or blk.norm.weight is None:
+            return False
+        if not block_step_supported(ssm, x, blk.norm.weight):
+            return False
+        if ssm.conv.weight.shape[1] != 1:
+            return False
+    return True
+
+
+class LayerChain:
+    """The device-side layer table and the workspace of ``ssm_decode_layers``
+    for one stack of Blocks and one (device, batch, dtype).  The table holds
+    the layers' parameter and cache addresses; it is rebuilt when any of them
+    changes (a HIP graph that captured a launch keeps the old table alive and
+    must be re-captured then, as for any other buffer it bakes in)."""
+
+    def __init__(self, layers, x: torch.Tensor):
+        s0 = layers[0].ssm
+        self.batch, self.model_dim = x.shape
+        self.dim, self.rank, self.width = s0.inner_dim, s0.delta_rank, s0.conv_kernel
+        self.dtype, self.device = x.dtype, x.device
+        self.eps = float(layers[0].norm.eps)
+        nbytes = int(N.lib().ssm_decode_layers_workspace(
+            self.batch, len(layers), self.model_dim, self.dim, self.rank + 2 * _CHAIN_STATE,
+            _DTYPES[x.dtype]))
+        if nbytes <= 0:
+            raise RuntimeError("ssm_decode_layers_workspace rejected the shape")
+        # zero-filled before the first launch (a launch counter and the
+        # layers' hand-off buffers, whose flags must not match a launch yet)
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=x.device)
+        self.ptrs = None
+        self.table = None
+
+    def update(self, layers) -> None:
+        ptrs = [0 if t is None else t.data_ptr() for blk in layers for t in _layer_tensors(blk)]
+        if ptrs != self.ptrs:
+            self.table = torch.tensor(ptrs, dtype=torch.int64).to(self.device)
+            self.ptrs = ptrs
+
+    def step(self, layers, x: torch.Tensor) -> torch.Tensor:
+        self.update(layers)
+        out = torch.empty_like(x)
+        with torch.cuda.device(x.device):
+            N.check(N.lib().ssm_decode_layers(
+                self.batch, len(layers), self.model_dim, self.dim, _CHAIN_STATE, self.rank,
+                self.width, _DTYPES[x.dtype], self.table.data_ptr(), x.data_ptr(), out.data_ptr(),
+                self.eps, self.workspace.data_ptr(), self.workspace.numel(), _stream(x.device)))
+        return out
+
+    def check(self) -> None:
+        """Synchronise and raise if a grid barrier of an earlier launch timed
+        out (the outputs since the last check are then invalid)."""
+        with torch.cuda.device(self.device):
+            N.check(N.lib().ssm_decode_layers_status(self.workspace.data_ptr(),
+                                                     self.workspace.numel(),
+                                                     _stream(self.device)))
+
+
+def layers_step(owner, layers, x: torch.Tensor) -> torch.Tensor:
+    """x after Block.step of every layer in ``layers`` (one launch); the
+    layers' caches advance in place.  ``owner`` keeps the LayerChain objects
+    (one per device, batch and dtype)."""
+    chains = owner.__dict__.setdefault("_layer_chains", {})
+    key = (x.device, x.shape[0], x.dtype)
+    chain = chains.get(key)
+    if chain is None:
+        chain = chains[key] = LayerChain(layers, x)
+    return chain.step(layers, x)
+
+
+def layers_check(owner) -> None:
+    """Raise if any layer-chain launch of ``owner`` hit a barrier time-out."""
+    for chain in owner.__dict__.get("_layer_chains", {}).values():
+        chain.check()

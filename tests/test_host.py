@@ -227,3 +227,35 @@ def test_toplevel_scan_module_validation(mutate, msg):
     with pytest.raises(RuntimeError, match=msg):
         ss.backward(a["u"], a["A"], a["B"], a["C"], a["D"], a["delta"], a["delta_bias"], h, None,
                     a["u"] if a["u"].dim() == 3 else torch.zeros(2, 4, 8), None)
+
+
+def test_layer_chain_arguments_are_checked():
+    """ssm_decode_layers validates its shapes and workspace before any launch;
+    placeholder addresses stand in for the device buffers (no GPU needed)."""
+    from ssm_mamba_amd import _native as N
+    lib = N.lib()
+    P = 4096  # never dereferenced: every call below fails its argument checks
+    ws = lib.ssm_decode_layers_workspace(4, 48, 1024, 2048, 96, N.SSM_BF16)
+    # the sync area (3 lines of 256 B), then per layer 8-byte units of 2 bf16
+    # (x: 4 x 1024; xc, z, y: 4 x 2048) or 1 fp32 (partials: 128 blocks of 4 x 96)
+    per_layer = (4 * 1024 // 2 + 3 * 4 * 2048 // 2 + 128 * 4 * 96) * 8
+    assert ws == 3 * 256 + 48 * per_layer
+    assert lib.ssm_decode_layers_workspace(4, 48, 1024, 2047, 96, N.SSM_BF16) == 0
+    assert lib.ssm_decode_layers_workspace(4, 0, 1024, 2048, 96, N.SSM_BF16) == 0
+    args = lambda **kw: [kw.get(k, v) for k, v in dict(
+        batch=4, nlayers=48, model_dim=1024, dim=2048, nstate=16, rank=64, width=4,
+        dtype=N.SSM_BF16, table=P, x=P, out=P, eps=1e-5, ws=P * 64, ws_bytes=ws,
+        stream=None).items()]
+    call = lambda **kw: lib.ssm_decode_layers(*args(**kw))
+    assert call(nstate=8) == 2 and b"nstate 16" in lib.ssm_last_error()
+    assert call(rank=60) == 2 and b"rank" in lib.ssm_last_error()
+    assert call(dim=2040) == 2 and b"folded x-projection" in lib.ssm_last_error()
+    assert call(batch=9) == 2
+    assert call(nlayers=0) == 1
+    assert call(width=5) == 2 and b"width" in lib.ssm_last_error()
+    assert call(ws_bytes=ws - 1) == 1 and b"workspace" in lib.ssm_last_error()
+    assert call(model_dim=2048, ws_bytes=1 << 30) == 2 and b"single pass" in lib.ssm_last_error()
+    assert call(dtype=N.SSM_F32, rank=64, ws_bytes=1 << 30) == 2 and b"at most 32" in lib.ssm_last_error()
+    assert call(dtype=N.SSM_F32, rank=32, ws_bytes=1 << 30) == 2 and b"single pass" in lib.ssm_last_error()
+    assert call(ws=P * 64 + 16) == 2 and b"256-byte" in lib.ssm_last_error()
+    assert call(table=None) == 1
