@@ -351,6 +351,24 @@ int ssm_decode_layers(int64_t batch, int64_t nlayers, int64_t model_dim, int64_t
  * (the workspace is zero-filled then). */
 int ssm_decode_layers_status(void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Greedy pick of the decode loop: token[b] = argmax_v probs[b, v] over the
+ * softmax output (batch, vocab) -- the argmax of models/causal_lm.py:117-120,
+ * the first maximum, NaN ranking above every number as in torch.argmax --
+ * and, with tokens non-NULL, the loop's bookkeeping in the same launch:
+ * tokens[b * tokens_ld + min(*pos, tokens_cols - 1)] = token[b], then
+ * *pos += 1 (pos nullable: column 0, no increment).  token, tokens, pos are
+ * int64.  Rows of a multiple of 16 bytes, 16-byte aligned.  workspace:
+ * ssm_decode_pick_workspace(batch) bytes, zero-filled before the first call
+ * (a counter each call leaves at zero); calls that share it must not overlap.
+ * No counterpart call in the reference (its loop does these as torch ops,
+ * models/causal_lm.py:111-129).
+ */
+int64_t ssm_decode_pick_workspace(int64_t batch);
+int ssm_decode_pick(int64_t batch, int64_t vocab, int dtype, const void* probs, int64_t* token,
+                    int64_t* tokens, int64_t tokens_ld, int64_t tokens_cols, int64_t* pos,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -104,6 +104,12 @@ SIGNATURES = {
         _p, _i64, _p,                          # workspace, workspace_bytes, stream
     ]),
     "ssm_decode_layers_status": (_i32, [_p, _i64, _p]),
+    "ssm_decode_pick_workspace": (_i64, [_i64]),
+    "ssm_decode_pick": (_i32, [
+        _i64, _i64, _i32, _p, _p,              # batch, vocab, dtype, probs, token
+        _p, _i64, _i64, _p,                    # tokens, tokens_ld, tokens_cols, pos
+        _p, _i64, _p,                          # workspace, workspace_bytes, stream
+    ]),
     "ssm_rms_norm_cm": (_i32, [
         _i64, _i64, _i64, _i32,                # batch, channels, seqlen, dtype
         _p, _p, ctypes.c_float, _p, _p,        # x, weight, eps, out, stream

@@ -528,7 +528,14 @@ class GreedyDecoder:
 
     def _body(self) -> None:
         logits = self.model.step(self.token)
-        nxt = _greedy_pick(logits, self.temperature)
+        if self.temperature != 1.0:
+            logits = logits / self.temperature
+        probs = torch.softmax(logits, dim=-1)
+        if _dec.pick_supported(probs):
+            # argmax, token, tokens[:, pos] and pos += 1 in one launch
+            _dec.pick(probs, self.token, self.tokens, self.pos)
+            return
+        nxt = probs.argmax(dim=-1)
         self.token.copy_(nxt)
         self.tokens.index_copy_(1, self.pos.clamp(max=self.tokens.shape[1] - 1), nxt[:, None])
         self.pos.add_(1)

@@ -41,6 +41,10 @@ hipError_t launch_decode_ssm_step(int bf16, const void* p, int nout, int nparts,
 int64_t decode_layers_workspace(int B, int nlayers, int K, int dim, int nout, int bf16);
 const char* decode_layers_unsupported(int K, int dim, int nout, int bf16);
 int64_t decode_layers_error_offset();
+int64_t decode_pick_workspace(int B);
+hipError_t launch_decode_pick(int bf16, const void* p, int B, int V, int64_t* token,
+                              int64_t* tokens, int64_t ld, int64_t cols, int64_t* pos, void* ws,
+                              hipStream_t st);
 int decode_layers_grid(int B, int K, int dim);
 int decode_layers_max_width();
 hipError_t launch_decode_layers(int bf16, const void* table, int nlayers, int B, int K, int dim,
@@ -656,6 +660,32 @@ int ssm_decode_layers(int64_t batch, int64_t nlayers, int64_t model_dim, int64_t
                 "decode_layers needs all %d workgroups resident at once, more than this device holds",
                 ssm::decode_layers_grid((int)batch, (int)model_dim, (int)dim));
   return hip_status(he, "decode_layers launch");
+}
+
+int64_t ssm_decode_pick_workspace(int64_t batch) {
+  return batch < 1 || batch > ssm::decode_max_batch() ? 0 : ssm::decode_pick_workspace((int)batch);
+}
+
+int ssm_decode_pick(int64_t batch, int64_t vocab, int dtype, const void* probs, int64_t* token,
+                    int64_t* tokens, int64_t tokens_ld, int64_t tokens_cols, int64_t* pos,
+                    void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = check_decode(batch, dtype);
+  if (rc != SSM_OK) return rc;
+  if (!probs || !token || !workspace) return fail(SSM_ERR_INVALID, "probs, token and workspace must be non-NULL");
+  if (workspace_bytes < ssm::decode_pick_workspace((int)batch))
+    return fail(SSM_ERR_INVALID, "decode_pick workspace is %lld bytes, needs %lld",
+                (long long)workspace_bytes, (long long)ssm::decode_pick_workspace((int)batch));
+  if (vocab < 1 || vocab > INT_MAX / 2)
+    return fail(SSM_ERR_INVALID, "decode_pick needs 1 <= vocab < 2^30 (got %lld)", (long long)vocab);
+  if (tokens && (tokens_cols < 1 || tokens_ld < tokens_cols))
+    return fail(SSM_ERR_INVALID, "decode_pick needs tokens_cols >= 1 and tokens_ld >= tokens_cols");
+  if (!aligned16(probs) || (vocab * (dtype == SSM_BF16 ? 2 : 4)) % 16)
+    return fail(SSM_ERR_UNSUPPORTED, "decode_pick needs 16-byte aligned rows (vocab %lld)",
+                (long long)vocab);
+  return hip_status(ssm::launch_decode_pick(dtype == SSM_BF16, probs, (int)batch, (int)vocab, token,
+                                            tokens, tokens_ld, tokens ? tokens_cols : 1, pos,
+                                            workspace, static_cast<hipStream_t>(stream)),
+                    "decode_pick launch");
 }
 
 int ssm_decode_layers_status(void* workspace, int64_t workspace_bytes, void* stream) {

@@ -1151,6 +1151,116 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
   }
 }
 
+// ---------------------------------------------------------------------------
+// Greedy pick of the decode loop: token[b] = argmax_v p[b, v], the first
+// maximum (NaN ranks above every number, as in torch.argmax) -- the argmax of
+// models/causal_lm.py:117-120 applied to the softmax output -- and the loop's
+// bookkeeping: tokens[b, min(pos, cols - 1)] = token[b], then pos += 1.
+//
+// kPickParts workgroups per row each find the best (value, index) of a slice
+// and store it at device scope; the last workgroup to finish (a device-scope
+// counter, which it clears again) combines the slices and does the
+// bookkeeping.  (value, index) pairs are totally ordered (indexes differ), so
+// the result does not depend on the order of the combination.
+constexpr int kPickThreads = 256;
+constexpr int kPickParts = 32;
+
+// (v, i) ranks before (w, j)
+__device__ __forceinline__ bool pick_beats(float v, int i, float w, int j) {
+  const bool vn = v != v, wn = w != w;
+  if (vn != wn) return vn;
+  if (!vn && v != w) return v > w;
+  return i < j;
+}
+
+__device__ __forceinline__ void pick_reduce_wave(float& v, int& i) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(v, m, 64);
+    const int oi = __shfl_xor(i, m, 64);
+    if (pick_beats(ov, oi, v, i)) { v = ov; i = oi; }
+  }
+}
+
+// ws: [0] the counter, then from word 64 the slices' (value bits, index)
+template <typename T>
+__global__ __launch_bounds__(kPickThreads) void pick_kernel(const T* __restrict__ p, int B, int V,
+                                                            int64_t* __restrict__ token,
+                                                            int64_t* __restrict__ tokens,
+                                                            int64_t ld, int64_t cols,
+                                                            int64_t* __restrict__ pos,
+                                                            unsigned* __restrict__ ws) {
+  constexpr int E = Chunk<T>::E;
+  constexpr int kIn = 4;  // chunks per thread in flight
+  using Raw = typename Chunk<T>::Raw;
+  __shared__ float s_v[kPickThreads / 64];
+  __shared__ int s_i[kPickThreads / 64];
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = blockIdx.x / kPickParts, part = blockIdx.x % kPickParts;
+  const int nc = V / E;  // rows are whole chunks
+  const int c_lo = part * nc / kPickParts, c_hi = (part + 1) * nc / kPickParts;
+  const T* __restrict__ row = p + (size_t)b * V;
+  float bv = -INFINITY;
+  int bi = V;  // ranks after every real index
+  for (int c0 = c_lo; c0 < c_hi; c0 += kPickThreads * kIn) {
+    Raw r[kIn];  // all of the round's loads first (clamped addresses, used when in range)
+#pragma unroll
+    for (int j = 0; j < kIn; ++j)
+      r[j] = ldchunk(row + (size_t)min(c0 + j * kPickThreads + (int)threadIdx.x, nc - 1) * E);
+#pragma unroll
+    for (int j = 0; j < kIn; ++j) {
+      const int c = c0 + j * kPickThreads + threadIdx.x;
+      if (c < c_hi) {
+        float f[E];
+        Chunk<T>::cvt(r[j], f);
+#pragma unroll
+        for (int k = 0; k < E; ++k)
+          if (pick_beats(f[k], c * E + k, bv, bi)) { bv = f[k]; bi = c * E + k; }
+      }
+    }
+  }
+  pick_reduce_wave(bv, bi);
+  if (lane == 0) { s_v[wave] = bv; s_i[wave] = bi; }
+  __syncthreads();
+  const auto r = dev_rsrc(ws, (size_t)(64 + 2 * B * kPickParts) * 4);
+  if (threadIdx.x == 0) {
+    float v = s_v[0];
+    int i = s_i[0];
+    for (int w = 1; w < kPickThreads / 64; ++w)
+      if (pick_beats(s_v[w], s_i[w], v, i)) { v = s_v[w]; i = s_i[w]; }
+    const u32x2_v pr = {__float_as_uint(v), (uint32_t)i};
+    __builtin_amdgcn_raw_buffer_store_b64(pr, r, (int)((64 + 2 * blockIdx.x) * 4), 0, kSC1);
+    __builtin_amdgcn_s_waitcnt(0);  // the slice is stored before it is counted
+    s_last = dev_add_u32(ws, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // the last workgroup: wave w combines rows w, w + 4, ... (no barrier inside)
+  const int64_t ps = pos ? *pos : 0;
+  const int64_t col = ps < cols - 1 ? ps : cols - 1;
+  for (int rb = wave; rb < B; rb += kPickThreads / 64) {
+    float v = -INFINITY;
+    int i = V;
+    if (lane < kPickParts) {
+      const u32x2_v pr =
+          __builtin_amdgcn_raw_buffer_load_b64(r, (int)((64 + 2 * (rb * kPickParts + lane)) * 4), 0, kSC1);
+      v = __uint_as_float(pr[0]);
+      i = (int)pr[1];
+    }
+    pick_reduce_wave(v, i);
+    if (lane == 0) {
+      token[rb] = i;
+      if (tokens) tokens[(size_t)rb * ld + col] = i;
+    }
+  }
+  __syncthreads();  // every lane has read pos
+  if (threadIdx.x == 0) {
+    if (pos) *pos = ps + 1;
+    dev_store_u32(ws, 0u);  // the counter, for the next launch
+  }
+}
+
 template <typename T, int kMB, int kRows>
 hipError_t launch_gemv_r(const GemvArgs& a, bool norm, bool conv, hipStream_t st) {
   const int rows_per_block = (kDecThreads / 64) * kRows;
@@ -1391,6 +1501,23 @@ const char* decode_layers_unsupported(int K, int dim, int nout, int bf16) {
 }
 
 int64_t decode_layers_error_offset() { return (int64_t)kSyncErr * sizeof(unsigned); }
+
+int64_t decode_pick_workspace(int B) { return (int64_t)(64 + 2 * B * kPickParts) * 4; }
+
+hipError_t launch_decode_pick(int bf16, const void* p, int B, int V, int64_t* token,
+                              int64_t* tokens, int64_t ld, int64_t cols, int64_t* pos, void* ws,
+                              hipStream_t st) {
+  ProfScope prof("decode_pick", st);
+  const dim3 grid(B * kPickParts);
+  unsigned* w = static_cast<unsigned*>(ws);
+  if (bf16)
+    hipLaunchKernelGGL(pick_kernel<__hip_bfloat16>, grid, dim3(kPickThreads), 0, st,
+                       static_cast<const __hip_bfloat16*>(p), B, V, token, tokens, ld, cols, pos, w);
+  else
+    hipLaunchKernelGGL(pick_kernel<float>, grid, dim3(kPickThreads), 0, st,
+                       static_cast<const float*>(p), B, V, token, tokens, ld, cols, pos, w);
+  return hipGetLastError();
+}
 
 int decode_layers_grid(int B, int K, int dim) { return layers_grid(B, K, dim); }
 

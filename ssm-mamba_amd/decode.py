@@ -290,6 +290,42 @@ def layers_step(owner, layers, x: torch.Tensor) -> torch.Tensor:
     return chain.step(layers, x)
 
 
+_PICK_WS = {}
+
+
+def pick_supported(probs: torch.Tensor) -> bool:
+    return (ENABLED and probs.is_cuda and probs.dim() == 2 and probs.dtype in _DTYPES
+            and 1 <= probs.shape[0] <= MAX_BATCH and probs.is_contiguous() and _aligned(probs)
+            and probs.shape[1] * probs.element_size() % 16 == 0)
+
+
+def pick(probs: torch.Tensor, token: torch.Tensor, tokens: Optional[torch.Tensor] = None,
+         pos: Optional[torch.Tensor] = None) -> None:
+    """token[:] = probs.argmax(-1) (first maximum, NaN highest, as torch), and
+    with tokens and pos: tokens[:, min(pos, cols - 1)] = token; pos += 1 --
+    one launch (int64 token (batch,), tokens (batch, cols), pos (1,))."""
+    batch, vocab = probs.shape
+    for t in (token, tokens, pos):
+        if t is not None and (t.dtype != torch.int64 or t.device != probs.device):
+            raise ValueError("pick: token, tokens and pos must be int64 on the probs' device")
+    if token.numel() != batch or not token.is_contiguous():
+        raise ValueError("pick: token must be a contiguous (batch,) tensor")
+    if tokens is not None and (tokens.shape[0] != batch or tokens.stride(1) != 1):
+        raise ValueError("pick: tokens must be (batch, cols) with unit column stride")
+    # the counter the last workgroup leaves at zero, kept per device (the
+    # graph a GreedyDecoder captures bakes its address in)
+    ws = _PICK_WS.get(probs.device)
+    need = int(N.lib().ssm_decode_pick_workspace(MAX_BATCH))
+    if ws is None:
+        ws = _PICK_WS[probs.device] = torch.zeros(need, dtype=torch.uint8, device=probs.device)
+    with torch.cuda.device(probs.device):
+        N.check(N.lib().ssm_decode_pick(
+            batch, vocab, _DTYPES[probs.dtype], probs.data_ptr(), token.data_ptr(), _ptr(tokens),
+            tokens.stride(0) if tokens is not None else 0,
+            tokens.shape[1] if tokens is not None else 0, _ptr(pos), ws.data_ptr(), ws.numel(),
+            _stream(probs.device)))
+
+
 def layers_check(owner) -> None:
     """Raise if any layer-chain launch of ``owner`` hit a barrier time-out."""
     for chain in owner.__dict__.get("_layer_chains", {}).values():

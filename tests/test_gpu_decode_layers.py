@@ -180,3 +180,39 @@ def test_chain_step_matches_oracle(cuda):
         bound = 1e-4 + 1e-3 * ref.abs()
         assert bool((err <= bound).all()), f"step {i}: max err {float(err.max()):.3g}"
     assert DEC.LAYER_CHAIN
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batch,vocab", [(1, 8), (4, 50280), (3, 1000), (8, 4096)])
+def test_pick_matches_torch_argmax(cuda, dtype, batch, vocab):
+    """The greedy pick against torch.argmax on softmax outputs, with ties
+    (equal maxima at several positions: the first wins) and NaNs (the first
+    NaN wins, as in torch), plus its bookkeeping: tokens[:, min(pos, cols-1)]
+    and pos + 1, the column clamped at the end."""
+    from ssm_mamba_amd import decode as DEC
+    g = torch.Generator().manual_seed(batch * vocab)
+    logits = torch.randn(batch, vocab, generator=g)
+    probs = torch.softmax(logits, dim=-1).to(dtype)
+    if batch > 1:
+        # row 1: the maximum also at later positions (a tie the first must win)
+        j = int(probs[1].float().argmax())
+        for k in (j + 3, vocab - 1):
+            if k < vocab:
+                probs[1, k] = probs[1, j]
+    if batch > 2:
+        probs[2, vocab // 3] = float("nan")
+        probs[2, vocab // 2] = float("nan")
+    probs = probs.to(cuda)
+    ref = probs.argmax(dim=-1)
+    cols = 5
+    token = torch.zeros(batch, dtype=torch.int64, device=cuda)
+    tokens = torch.full((batch, cols), -1, dtype=torch.int64, device=cuda)
+    pos = torch.tensor([3], dtype=torch.int64, device=cuda)
+    assert DEC.pick_supported(probs)
+    for step in range(3):
+        DEC.pick(probs, token, tokens, pos)
+    torch.cuda.synchronize()
+    assert torch.equal(token, ref), f"{token.tolist()} vs {ref.tolist()}"
+    assert int(pos) == 6
+    assert torch.equal(tokens[:, 3], ref) and torch.equal(tokens[:, 4], ref)
+    assert bool((tokens[:, :3] == -1).all())
