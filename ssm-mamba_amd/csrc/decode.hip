@@ -671,8 +671,8 @@ struct SsmArgs {
 //
 // As with GemvWork, the loads come in separate steps (the partials, the
 // operands that do not depend on p, and the activations xc and z).  The layer
-// chain (kChain) reads the partials, xc and z as LL units (all partials of a
-// thread in one round, the caller checks) and leaves y in an LDS tile.
+// chain reads xc and z as LL units, sums the partials itself into s_p and
+// calls compute<true>, which leaves y in an LDS tile.
 template <typename T, int kN, bool kVecR, bool kParts, int kSplit = 1, int kPL = kPartLoads,
           int kMaxRC = 16>
 struct SsmStep {
@@ -718,26 +718,6 @@ struct SsmStep {
 #pragma unroll
       for (int j = 0; j < kPL; ++j) pv[j] = part(a, min(w0 + j, a.nparts - 1));
     }
-  }
-
-  // the layer chain: this thread's partials (at most kPL blocks) from LL units,
-  // the float4 column of block w being units (w B + b) nout4 + 4 gi .. + 3
-  __device__ __forceinline__ bool load_parts_ll(const SsmArgs& a, const LLWait& w) {
-    const auto r = dev_rsrc(a.pp, (size_t)a.nparts * a.B * a.nout4 * 8);
-    uint32_t pairs[2 * kPL];
-#pragma unroll
-    for (int j = 0; j < kPL; ++j) {
-      const uint32_t u0 = (uint32_t)(((size_t)min(w0 + j, a.nparts - 1) * a.B + b) * a.nout4 + 4 * gi);
-      pairs[2 * j] = u0;
-      pairs[2 * j + 1] = u0 + 2;
-    }
-    u32x4_v v[2 * kPL];
-    const bool ok = ll_wait2<2 * kPL>(r, pairs, sg < S, w, v);
-#pragma unroll
-    for (int j = 0; j < kPL; ++j)
-      pv[j] = make_float4(__uint_as_float(v[2 * j][0]), __uint_as_float(v[2 * j][2]),
-                          __uint_as_float(v[2 * j + 1][0]), __uint_as_float(v[2 * j + 1][2]));
-    return ok;
   }
 
   // this thread's operands that do not depend on p (dt-projection chunks
@@ -790,12 +770,9 @@ struct SsmStep {
     return v;
   }
 
-  // s_p: [nout4] floats; s_red: [S][nout4 / 4] float4 (S * nout4 <= 4 kThreads);
-  // s_y (kChain): [256] floats, y of the workgroup's channels (0 past dim)
-  template <bool kChain>
-  __device__ __forceinline__ void finish(const SsmArgs& a, float* s_p, float4* s_red,
-                                         float* s_y = nullptr) {
-    const int nout = a.nout, nout4 = a.nout4, R = a.R;
+  // s_p: [nout4] floats; s_red: [S][nout4 / 4] float4 (S * nout4 <= 4 kThreads)
+  __device__ __forceinline__ void finish(const SsmArgs& a, float* s_p, float4* s_red) {
+    const int nout = a.nout, nout4 = a.nout4;
     if constexpr (kParts) {
       float4 pacc = make_float4(0.f, 0.f, 0.f, 0.f);
       if (sg < S) {
@@ -806,7 +783,7 @@ struct SsmStep {
               pacc.x += pv[j].x; pacc.y += pv[j].y; pacc.z += pv[j].z; pacc.w += pv[j].w;
             }
           }
-          if (kChain || wb + kPL >= w1) break;
+          if (wb + kPL >= w1) break;
 #pragma unroll
           for (int j = 0; j < kPL; ++j) pv[j] = part(a, min(wb + kPL + j, a.nparts - 1));
         }
@@ -824,6 +801,14 @@ struct SsmStep {
       for (int i = threadIdx.x; i < nout; i += kThreads) s_p[i] = Elem<T>::load1(p + (size_t)b * nout + i);
     }
     __syncthreads();
+    compute<false>(a, s_p);
+  }
+
+  // delta, state update and gate from params s_p (in LDS, complete); s_y
+  // (kChain): [256] floats, y of the workgroup's channels (0 past dim)
+  template <bool kChain>
+  __device__ __forceinline__ void compute(const SsmArgs& a, const float* s_p, float* s_y = nullptr) {
+    const int R = a.R;
     if (kChain && d >= a.dim && q == 0) s_y[threadIdx.x / kSplit] = 0.0f;
     if (d >= a.dim) return;
 
@@ -876,7 +861,7 @@ __global__ __launch_bounds__(kDecThreads) void ssm_step_kernel(const SsmArgs a) 
   st.load_parts(a);
   st.load_operands(a);
   st.load_act(a);
-  st.template finish<false>(a, s_p, reinterpret_cast<float4*>(s_p + a.nout4));
+  st.finish(a, s_p, reinterpret_cast<float4*>(s_p + a.nout4));
 }
 
 // ---------------------------------------------------------------------------
@@ -939,8 +924,9 @@ struct LayersArgs {
   char* ll;                 // LL buffers: layer l's at ll + l * ll_stride
   size_t ll_stride;
   // byte offsets in a layer's block: its input x (B, K / V units; written by
-  // the layer before), the partials (nparts, B, nout4), xc, z and y (B, dim / V)
-  uint32_t ll_x, ll_p, ll_xc, ll_z, ll_y;
+  // the layer before), the partials (nparts, B, nout4), their slice sums
+  // (B, nd, nout4), xc, z and y (B, dim / V)
+  uint32_t ll_x, ll_p, ll_q, ll_xc, ll_z, ll_y;
   unsigned* sync;           // generation, done counter and error word
   unsigned maxspin;
 };
@@ -1000,13 +986,12 @@ constexpr int kChainSplit = kChainThreads / kDecThreads;  // threads per channel
 constexpr int kChainKSplit = 2;                            // K-slices of the out-projection
 constexpr int kChainRows1 = kXBlock / kChainWaves;         // in-projection rows per wave
 constexpr int kChainTaps = 4;                              // conv width limit
-constexpr int kChainPartLoads = 8;                         // partial blocks per phase-2 thread
 constexpr int kChainRC = 8;                                // dt rank up to 8 16-byte chunks
 
 template <typename T, int kMB, int kN, int kRows3>
 struct Chain {
   using P1 = GemvWork<T, kMB, kChainRows1, true, kEpiConvX, kChainWaves, 1, 2, kChainTaps>;
-  using P2 = SsmStep<T, kN, true, true, kChainSplit, kChainPartLoads, kChainRC>;
+  using P2 = SsmStep<T, kN, true, true, kChainSplit, 1, kChainRC>;
   using P3 = GemvWork<T, kMB, kRows3, false, kEpiPlain, kChainWaves, kChainKSplit, 2>;
 };
 
@@ -1040,6 +1025,8 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
   if (flag == 0) return;
   const LLWait w{flag, a.maxspin, err};
   const size_t xbytes = (size_t)a.B * a.K / V * 8, cbytes = (size_t)a.B * a.dim / V * 8;
+  const size_t pbytes = (size_t)a.nparts * a.B * a.nout4 * 8;
+  const size_t qbytes = (size_t)a.B * nd * a.nout4 * 8;
 
   // Each phase's weights and operands go out just before the wait for its
   // input.  (Issuing them a phase earlier, to land during the previous phase's
@@ -1086,19 +1073,64 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
       }
     }
 
-    // phase 2: partial sums, dt projection, state update, gate
+    // phase 2: partial sums, dt projection, state update, gate.  The nd
+    // workgroups of a batch row first sum one nd-th of its partial blocks each
+    // (in block order) and publish those slice sums; each then adds the nd
+    // slice sums (in slice order): two small hand-offs instead of every
+    // workgroup reading all of its row's partial blocks.
     if (blk < n2) {
-      const int bb = blk / nd, d0 = (blk % nd) * kDecThreads;
+      const int bb = blk / nd, dblk = blk % nd, d0 = dblk * kDecThreads;
+      const int ng = a.nout4 / 4;
       P2 p2;
-      p2.begin(s2, blk % nd, bb);
+      p2.begin(s2, dblk, bb);
       p2.load_operands(s2);
-      const bool ok_p = p2.load_parts_ll(s2, w);
-      const bool ok_a = p2.load_act_ll(s2, w);
-      if (__syncthreads_or(!(ok_p && ok_a))) {
-        if (threadIdx.x == 0) dev_store_u32(err, 1u);
-        return;
+      const int w_lo = dblk * a.nparts / nd, nw = (dblk + 1) * a.nparts / nd - w_lo;
+      {
+        const int t = threadIdx.x, wl = t / ng, gi = t - wl * ng;
+        const uint32_t u0 = (uint32_t)(((w_lo + min(wl, nw - 1)) * a.B + bb) * a.nout4 + 4 * gi);
+        const uint32_t pairs[2] = {u0, u0 + 2};
+        u32x4_v v[2];
+        const bool ok = ll_wait2<2>(dev_rsrc(lb + a.ll_p, pbytes), pairs, wl < nw, w, v);
+        if (wl < nw)
+          s_red[t] = make_float4(__uint_as_float(v[0][0]), __uint_as_float(v[0][2]),
+                                 __uint_as_float(v[1][0]), __uint_as_float(v[1][2]));
+        if (__syncthreads_or(!ok)) {
+          if (threadIdx.x == 0) dev_store_u32(err, 1u);
+          return;
+        }
       }
-      p2.template finish<true>(s2, s_p, s_red, s_y);
+      if ((int)threadIdx.x < a.nout4) {
+        const int jc = threadIdx.x;
+        const float* r = reinterpret_cast<const float*>(s_red) + jc;
+        float t = 0.0f;
+        for (int wl = 0; wl < nw; ++wl) t += r[wl * a.nout4];
+        ll_put(dev_rsrc(lb + a.ll_q, qbytes), (uint32_t)((bb * nd + dblk) * a.nout4 + jc),
+               __float_as_uint(t), flag);
+      }
+      {
+        const int t = threadIdx.x, sl = t / ng, gi = t - sl * ng;
+        const uint32_t u0 = (uint32_t)((bb * nd + min(sl, nd - 1)) * a.nout4 + 4 * gi);
+        const uint32_t pairs[2] = {u0, u0 + 2};
+        u32x4_v v[2];
+        const bool ok_q = ll_wait2<2>(dev_rsrc(lb + a.ll_q, qbytes), pairs, sl < nd, w, v);
+        const bool ok_a = p2.load_act_ll(s2, w);
+        __syncthreads();  // every thread is done with the slice sums in s_red
+        if (sl < nd)
+          s_red[t] = make_float4(__uint_as_float(v[0][0]), __uint_as_float(v[0][2]),
+                                 __uint_as_float(v[1][0]), __uint_as_float(v[1][2]));
+        if (__syncthreads_or(!(ok_q && ok_a))) {
+          if (threadIdx.x == 0) dev_store_u32(err, 1u);
+          return;
+        }
+      }
+      if ((int)threadIdx.x < a.nout) {
+        const float* r = reinterpret_cast<const float*>(s_red) + threadIdx.x;
+        float t = 0.0f;
+        for (int sl = 0; sl < nd; ++sl) t += r[sl * a.nout4];
+        s_p[threadIdx.x] = round_to<T>(t);
+      }
+      __syncthreads();
+      p2.template compute<true>(s2, s_p, s_y);
       __syncthreads();
       constexpr int kU = kDecThreads / V;
       if ((int)threadIdx.x < kU && d0 + (int)threadIdx.x * V < a.dim) {
@@ -1412,9 +1444,10 @@ const char* layers_unsupported_t(int K, int dim, int nout) {
   if (K > C::P1::PK) return "model_dim exceeds the in-projection's single pass";
   if (dim > C::P3::PK) return "dim exceeds the out-projection's single pass";
   const int ng = ((nout + 3) & ~3) / 4;
-  const int S = kChainThreads / ng;
+  const int nd = (dim + kDecThreads - 1) / kDecThreads;
   const int nparts = dim / kXBlock;
-  if ((nparts + S - 1) / S > kChainPartLoads) return "too many x-projection partials per thread";
+  if (((nparts + nd - 1) / nd) * ng > kChainThreads)
+    return "too many x-projection partial blocks per state-update workgroup";
   return nullptr;
 }
 
@@ -1468,10 +1501,10 @@ hipError_t launch_decode_ssm_step(int bf16, const void* p, int nout, int nparts,
 
 // workspace of the layer chain: the sync area, then per layer a block of LL
 // buffers (8-byte units of 4 data bytes): the layer's input x, the partials,
-// xc, z and y, each 256-byte aligned
+// their slice sums, xc, z and y, each 256-byte aligned
 namespace {
 struct LayersWs {
-  size_t ll, stride, x, p, xc, z, y, total;
+  size_t ll, stride, x, p, q, xc, z, y, total;
 };
 
 LayersWs layers_ws(int B, int nlayers, int K, int dim, int nout, int elem) {
@@ -1482,6 +1515,7 @@ LayersWs layers_ws(int B, int nlayers, int K, int dim, int nout, int elem) {
   size_t o = 0;
   w.x = o; o += up((size_t)B * K / V * 8);
   w.p = o; o += up((size_t)(dim / kXBlock) * B * ((nout + 3) & ~3) * 8);
+  w.q = o; o += up((size_t)B * ((dim + kDecThreads - 1) / kDecThreads) * ((nout + 3) & ~3) * 8);
   w.xc = o; o += up((size_t)B * dim / V * 8);
   w.z = o; o += up((size_t)B * dim / V * 8);
   w.y = o; o += up((size_t)B * dim / V * 8);
@@ -1535,7 +1569,7 @@ hipError_t launch_decode_layers(int bf16, const void* table, int nlayers, int B,
   a.nout = nout; a.nout4 = (nout + 3) & ~3; a.nparts = dim / kXBlock; a.eps = eps;
   a.x_in = x; a.x_out = out;
   a.ll = base + w.ll; a.ll_stride = w.stride;
-  a.ll_x = (uint32_t)w.x; a.ll_p = (uint32_t)w.p; a.ll_xc = (uint32_t)w.xc;
+  a.ll_x = (uint32_t)w.x; a.ll_p = (uint32_t)w.p; a.ll_q = (uint32_t)w.q; a.ll_xc = (uint32_t)w.xc;
   a.ll_z = (uint32_t)w.z; a.ll_y = (uint32_t)w.y;
   a.sync = reinterpret_cast<unsigned*>(base);
   // about a second of polling at most (a poll is a device-memory round trip)
