@@ -293,8 +293,11 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
     step captured once in a HIP graph and replayed.  Returns tokens/s for both
     and the share of time in the scan / state-update kernels: for the prefill
     from the library's per-kernel HIP events (forward scan, its segment
-    summaries and the B/C prep), for the decode from a graph of the step's 48
-    state-update kernels alone on the same buffers."""
+    summaries and the B/C prep); for the decode, the 48 layers run as one
+    kernel (ssm_decode_layers, whose state update cannot be timed apart), so
+    the step reports that kernel's share from a graph of it alone, and for
+    reference a graph of 48 stand-alone state-update kernels on the same
+    buffers."""
     import torch
 
     from ssm_mamba_amd import _native as N
@@ -385,6 +388,28 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
         e1.record()
         torch.cuda.synchronize()
         upd_ms = e0.elapsed_time(e1)
+
+        # the step's layer chain alone (one launch for the 48 layers)
+        x0 = torch.randn(batch, cfg.model_dim, device=dev).bfloat16()
+        chain = DEC.layers_supported(model.layers, x0)
+        chain_ms = 0.0
+        if chain:
+            with torch.cuda.stream(side):
+                DEC.layers_step(model, model.layers, x0)
+            torch.cuda.current_stream(dev).wait_stream(side)
+            cg = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(cg):
+                DEC.layers_step(model, model.layers, x0)
+            cg.replay()
+            torch.cuda.synchronize()
+            e0, e1 = ev(), ev()
+            e0.record()
+            for _ in range(decode_steps):
+                cg.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            chain_ms = e0.elapsed_time(e1)
+            DEC.layers_check(model)
     res = {
         "config": "48 layers, d_model 1024, d_inner 2048, N 16, d_conv 4, dt_rank 64, vocab 50280, "
                   "bf16 weights (random init), eval; prefill 4 x 2048 (pad id 0 -> lengths), then "
@@ -397,8 +422,10 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
         "prefill_scan_ms": round(scan_ms, 3),
         "decode_ms_per_step": round(dec_ms / decode_steps, 4),
         "decode_tokens_per_s": round(batch * decode_steps / (dec_ms * 1e-3), 1),
-        "decode_update_share": round(upd_ms / dec_ms, 4),
-        "decode_update_us_per_step": round(1e3 * upd_ms / decode_steps, 2),
+        "decode_layer_chain": bool(chain),
+        "decode_layer_chain_share": round(chain_ms / dec_ms, 4),
+        "decode_layer_chain_us_per_step": round(1e3 * chain_ms / decode_steps, 2),
+        "decode_standalone_update_us_per_step": round(1e3 * upd_ms / decode_steps, 2),
         "decode_fused_kernels": bool(fused),
         "first_new_tokens": new_tokens[0, :8].tolist(),
     }

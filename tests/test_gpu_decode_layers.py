@@ -1,5 +1,6 @@
 """The layer chain (ssm_decode_layers: the decode step of every layer in one
-persistent launch with grid barriers between its phases) against the
+persistent launch, workgroups handing activations to each other through
+flagged buffer units instead of grid barriers) against the
 per-layer fused kernels (logits, SSM states and conv windows over several
 token steps; the chain sums the out-projection in K-slices and splits the
 state update over thread pairs, so the two agree to rounding), for fp32 and
@@ -116,8 +117,9 @@ def test_chain_config4_widths(cuda):
 
 def test_chain_graph_replays_match_eager(cuda):
     """The chain captured in a HIP graph: every replay equals the eager step
-    from the same caches (the barrier counters return to zero after each
-    launch, so replays start clean), and the status check stays clear."""
+    from the same caches (the done counter returns to zero and the
+    generation flag advances after each launch, so replays start clean),
+    and the status check stays clear."""
     from ssm_mamba_amd import decode as DEC
     m, cfg = make_lm(seed=60, vocab=89, model_dim=256, state_dim=16, layers=4)
     m = m.to(cuda, torch.bfloat16)
