@@ -577,7 +577,7 @@ __device__ __forceinline__ constexpr int bws_swz(int q) { return 2 * q + 8 * (q 
 template <typename T>
 struct BwsRows {  // one tile's raw loads of a producer lane, as loaded
   typename Raw4<T>::type u, d, dy, z, y;
-  T B, C;
+  uint32_t B, C;  // element bits
 };
 
 template <typename T, bool kHasZ, bool kAligned>
@@ -763,7 +763,40 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
   const auto dz_rsrc = raw_rsrc(kHasZ ? dzp + ((size_t)rb + wrow0) * L : dup, kHasZ ? wbytes : 0u);
   const uint32_t row_off = (uint32_t)((row % (kBlockCh / kWsProd)) * (size_t)L * sizeof(T));
 
+  // The aligned path's loads go through buffer ranges over the same 16 rows,
+  // and over the batch row's B and C rows, at 32-bit offsets (no 64-bit
+  // address arithmetic per tile).  The step is clamped into the row as on the
+  // pointer path; a row past the last channel reads zero.
+  const auto u_ld = raw_rsrc(const_cast<T*>(u) + ((size_t)rb + wrow0) * L, wbytes);
+  const auto d_ld = raw_rsrc(const_cast<T*>(dl) + ((size_t)rb + wrow0) * L, wbytes);
+  const auto dy_ld = raw_rsrc(const_cast<T*>(dyp) + ((size_t)rb + wrow0) * L, wbytes);
+  const auto z_ld = raw_rsrc(kHasZ ? const_cast<T*>(zp) + ((size_t)rb + wrow0) * L : const_cast<T*>(u),
+                             kHasZ ? wbytes : 0u);
+  const auto y_ld = raw_rsrc(kHasZ ? const_cast<T*>(yup) + ((size_t)rb + wrow0) * L : const_cast<T*>(u),
+                             kHasZ ? wbytes : 0u);
+  const uint32_t bc_bytes = (uint32_t)((size_t)N * L * sizeof(T));
+  const auto B_ld = raw_rsrc(const_cast<T*>(Bp) + (size_t)b * p.bc_bstride, bc_bytes);
+  const auto C_ld = raw_rsrc(const_cast<T*>(Cp) + (size_t)b * p.bc_bstride, bc_bytes);
+  const uint32_t bc_row_off = (uint32_t)((size_t)min(bc_n, N - 1) * L * sizeof(T));
+
   auto issue = [&](BwsRows<T>& r, int i) {
+    if constexpr (kAligned) {
+      const int t0 = tile_of(i) * kTileB;
+      const uint32_t off = row_off + (uint32_t)min(t0 + 4 * q, L - 4) * sizeof(T);
+      r.u = buffer_load_raw4<T>(u_ld, off);
+      r.d = buffer_load_raw4<T>(d_ld, off);
+      r.dy = buffer_load_raw4<T>(dy_ld, off);
+      if constexpr (kHasZ) {
+        r.z = buffer_load_raw4<T>(z_ld, off);
+        r.y = buffer_load_raw4<T>(y_ld, off);
+      } else {
+        r.z = r.y = typename Raw4<T>::type{};
+      }
+      const uint32_t boff = bc_row_off + (uint32_t)min(t0 + bc_j, L - 1) * sizeof(T);
+      r.B = buffer_load_bits1<T>(B_ld, boff);
+      r.C = buffer_load_bits1<T>(C_ld, boff);
+      return;
+    }
     const int t = tile_of(i) * kTileB + 4 * q;
     r.u = load_raw4_nb<T, kAligned>(u_row, t, L, pch_ok);
     r.d = load_raw4_nb<T, kAligned>(d_row, t, L, pch_ok);
@@ -775,8 +808,8 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
       r.z = r.y = typename Raw4<T>::type{};
     }
     const int tb = min(tile_of(i) * kTileB + bc_j, L - 1);
-    r.B = B_row[tb];
-    r.C = C_row[tb];
+    r.B = elem_bits(B_row[tb]);
+    r.C = elem_bits(C_row[tb]);
   };
 
   // What a tile's finish needs from its staging besides delta and dout (read
@@ -829,8 +862,8 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
     sSt[sb][1][q][sw] = make_float4(du[0], du[1], du[2], du[3]);
     sSt[sb][2][q][sw] = make_float4(dov[0], dov[1], dov[2], dov[3]);
     float* const blk_dst = &sBlk[sb][bc_n >> 1][bc_j >> 2][bc_slot];
-    blk_dst[0] = bc_ok ? to_f32(r.B) : 0.0f;
-    blk_dst[1] = bc_ok ? to_f32(r.C) : 0.0f;
+    blk_dst[0] = bc_ok ? bits_to_f32<T>(r.B) : 0.0f;
+    blk_dst[1] = bc_ok ? bits_to_f32<T>(r.C) : 0.0f;
     // a tile past the segment (i >= nt) writes nothing
     const bool st_ok = pch_ok && i < nt;
     if constexpr (kHasZ) {

@@ -553,7 +553,7 @@ constexpr int kWsRow = kBlockCh + 2;
 template <typename T>
 struct WsRows {
   typename Raw4<T>::type u, d, z;
-  T B, C;
+  uint32_t B, C;  // element bits
 };
 
 
@@ -698,15 +698,45 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
 
   // raw rows of tile i (clamped to the last tile; the loads of tiles past it
   // are never used)
+  // This wave's 16 channel rows (the launch guarantees 16 * L * sizeof(T) <
+  // 2^31, so the byte offsets fit): the aligned path loads and stores through
+  // buffer ranges over them, and loads B and C through ranges over the batch
+  // row's state rows, at 32-bit offsets (no 64-bit address arithmetic per
+  // tile).  The step is clamped into the row as on the pointer path; a row
+  // past the last channel reads zero.
+  const int wrow0 = d0 + (w - kWsCons) * (kBlockCh / kWsProd);
+  const uint32_t wbytes =
+      (uint32_t)(max(0, min(kBlockCh / kWsProd, Dm - wrow0)) * (size_t)L * sizeof(T));
+  const uint32_t row_off = (uint32_t)((row % (kBlockCh / kWsProd)) * (size_t)L * sizeof(T));
+  const auto u_ld = raw_rsrc(const_cast<T*>(u) + ((size_t)rb + wrow0) * L, wbytes);
+  const auto d_ld = raw_rsrc(const_cast<T*>(dl) + ((size_t)rb + wrow0) * L, wbytes);
+  const auto z_ld = raw_rsrc(kHasZ ? const_cast<T*>(zp) + ((size_t)rb + wrow0) * L : const_cast<T*>(u),
+                             kHasZ ? wbytes : 0u);
+  const uint32_t bc_bytes = (uint32_t)((size_t)N * L * sizeof(T));
+  const auto B_ld = raw_rsrc(const_cast<T*>(Bp) + (size_t)b * p.bc_bstride, bc_bytes);
+  const auto C_ld = raw_rsrc(const_cast<T*>(Cp) + (size_t)b * p.bc_bstride, bc_bytes);
+  const uint32_t bc_row_off = (uint32_t)((size_t)min(bc_n, N - 1) * L * sizeof(T));
+
   auto issue = [&](WsRows<T>& r, int i) {
     const int t0 = min(Tbeg + i * kWsTile, last_t0);
-    r.u = load_raw4_nb<T, kAligned>(u_row, t0 + 4 * q, L, pch_ok);
-    r.d = load_raw4_nb<T, kAligned>(d_row, t0 + 4 * q, L, pch_ok);
-    if constexpr (kHasZ) r.z = load_raw4_nb<T, kAligned>(z_row, t0 + 4 * q, L, pch_ok);
-    else r.z = typename Raw4<T>::type{};
-    const int tb = min(t0 + bc_step, L - 1);
-    r.B = B_row[tb];
-    r.C = C_row[tb];
+    if constexpr (kAligned) {
+      const uint32_t off = row_off + (uint32_t)min(t0 + 4 * q, L - 4) * sizeof(T);
+      r.u = buffer_load_raw4<T>(u_ld, off);
+      r.d = buffer_load_raw4<T>(d_ld, off);
+      if constexpr (kHasZ) r.z = buffer_load_raw4<T>(z_ld, off);
+      else r.z = typename Raw4<T>::type{};
+      const uint32_t boff = bc_row_off + (uint32_t)min(t0 + bc_step, L - 1) * sizeof(T);
+      r.B = buffer_load_bits1<T>(B_ld, boff);
+      r.C = buffer_load_bits1<T>(C_ld, boff);
+    } else {
+      r.u = load_raw4_nb<T, kAligned>(u_row, t0 + 4 * q, L, pch_ok);
+      r.d = load_raw4_nb<T, kAligned>(d_row, t0 + 4 * q, L, pch_ok);
+      if constexpr (kHasZ) r.z = load_raw4_nb<T, kAligned>(z_row, t0 + 4 * q, L, pch_ok);
+      else r.z = typename Raw4<T>::type{};
+      const int tb = min(t0 + bc_step, L - 1);
+      r.B = elem_bits(B_row[tb]);
+      r.C = elem_bits(C_row[tb]);
+    }
   };
 
   // stage tile i into buffer sb: delta (softplus once per element, zero
@@ -748,17 +778,11 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     sSt[sb][0][q][row] = make_float4(de[0], de[1], de[2], de[3]);
     sSt[sb][1][q][row] = make_float4(du[0], du[1], du[2], du[3]);
     reinterpret_cast<float2*>(&sBC[sb][bc_G][bc_step])[bc_half] =
-        bc_ok ? make_float2(to_f32(r.B), to_f32(r.C)) : make_float2(0.0f, 0.0f);
+        bc_ok ? make_float2(bits_to_f32<T>(r.B), bits_to_f32<T>(r.C)) : make_float2(0.0f, 0.0f);
   };
 
-  // Output buffers of this wave's 16 channel rows (the launch guarantees
-  // 16 * L * sizeof(T) < 2^31, so the byte offsets fit).
-  const int wrow0 = d0 + (w - kWsCons) * (kBlockCh / kWsProd);
-  const uint32_t wbytes =
-      (uint32_t)(max(0, min(kBlockCh / kWsProd, Dm - wrow0)) * (size_t)L * sizeof(T));
   const auto out_rsrc = raw_rsrc(out + ((size_t)rb + wrow0) * L, wbytes);
   const auto yu_rsrc = raw_rsrc(kSaveY ? yu + ((size_t)rb + wrow0) * L : out, kSaveY ? wbytes : 0u);
-  const uint32_t row_off = (uint32_t)((row % (kBlockCh / kWsProd)) * (size_t)L * sizeof(T));
 
   // finish tile i: the eight slices (read before the staging work of the
   // same iteration, added after it) in a fixed order, D*u, the gate, stores

@@ -189,6 +189,44 @@ constexpr uint32_t kOffDrop = 0x80000000u;  // past every range built here (byte
 typedef unsigned int u32x2_v __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4_v __attribute__((ext_vector_type(4)));
 
+// 4 consecutive elements at byte offset `off` of the buffer, as loaded; zero
+// when off is past its range.
+template <typename T>
+__device__ __forceinline__ typename Raw4<T>::type buffer_load_raw4(__amdgpu_buffer_rsrc_t r,
+                                                                   uint32_t off) {
+  if constexpr (sizeof(T) == 4) {
+    const u32x4_v v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return uint4{v.x, v.y, v.z, v.w};
+  } else {
+    const u32x2_v v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    return uint2{v.x, v.y};
+  }
+}
+
+// The bits of one element at byte offset `off` (zero past the range).
+template <typename T>
+__device__ __forceinline__ uint32_t buffer_load_bits1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(T) == 4) return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+  else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
+// The bits of one element as held in memory, and those bits as a float.
+template <typename T>
+__device__ __forceinline__ uint32_t elem_bits(T x) {
+  if constexpr (sizeof(T) == 4) {
+    return __float_as_uint(x);
+  } else {
+    unsigned short s;
+    __builtin_memcpy(&s, &x, sizeof(s));
+    return s;
+  }
+}
+template <typename T>
+__device__ __forceinline__ float bits_to_f32(uint32_t v) {
+  if constexpr (sizeof(T) == 4) return __uint_as_float(v);
+  else return __uint_as_float(v << 16);
+}
+
 // 4 consecutive elements at byte offset `off` of the buffer (dropped when off
 // is past its range).
 template <typename T>
