@@ -15,8 +15,9 @@
 // workgroup of the x half writes the fp32 partial W_x[:, its channels] @ xc,
 // and every ssm_step workgroup adds the partials of its batch row in a fixed
 // order (kEpiConvX / kParts below); or, for a whole stack of layers, in one
-// persistent launch that runs those three kernels' workgroups as phases
-// separated by grid barriers (decode_layers_kernel).
+// persistent launch that runs those three kernels' workgroups as phases, the
+// workgroups handing activations to each other through flagged 8-byte units
+// instead of grid barriers (decode_layers_kernel).
 //
 // and the LM head as gemv_kernel with the final norm.  Batch is small (one
 // token per sequence), so every kernel is a weight stream: a wave owns a few
@@ -1077,9 +1078,15 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
     // workgroups of a batch row first sum one nd-th of its partial blocks each
     // (in block order) and publish those slice sums; each then adds the nd
     // slice sums (in slice order): two small hand-offs instead of every
-    // workgroup reading all of its row's partial blocks.
-    if (blk < n2) {
-      const int bb = blk / nd, dblk = blk % nd, d0 = dblk * kDecThreads;
+    // workgroup reading all of its row's partial blocks.  Phase 2 runs on the
+    // workgroups of phase 1's z half (from z2 on) where there are enough of
+    // them: they finish phase 1 earlier (no conv step or x-projection
+    // partials), so their phase-2 operand loads are in before the partials
+    // arrive and the wait for the partials is not held up behind them.
+    const int z2 = max(0, min(a.dim / kXBlock, (int)gridDim.x - n2));
+    if (blk - z2 >= 0 && blk - z2 < n2) {
+      const int blk2 = blk - z2;
+      const int bb = blk2 / nd, dblk = blk2 % nd, d0 = dblk * kDecThreads;
       const int ng = a.nout4 / 4;
       P2 p2;
       p2.begin(s2, dblk, bb);
