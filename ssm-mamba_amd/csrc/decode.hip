@@ -280,6 +280,7 @@ struct GemvWork {
   float e_cw[kNG][kMaxTaps], e_win[kNG][kMaxTaps - 1];
   Raw xw[kXC];                        // the W_x slice of output j = threadIdx.x
   Raw wr[kRows][kPass];               // weights of the current pass
+  float xs_keep[kNG];                 // kChain conv epilogue: the window's new last column
   Raw nwr[kNorm ? kPass : 1];         // norm weights of the current pass
   float acc[kRows][kMB];
   float ssq[kMB];
@@ -368,6 +369,25 @@ struct GemvWork {
 
   // this lane's weight chunks of the pass at column kb (and the norm weight
   // of its columns, clamped past K where the chunk is not used)
+  // After finish<true> with the conv epilogue: the conv window roll (drop the
+  // oldest column, append x).  The layer chain calls it after the phase's
+  // hand-off stores, which the other workgroups wait for; the window is read
+  // again only at the next token step.
+  __device__ __forceinline__ void store_window(const GemvArgs& a) {
+    if constexpr (kEpi != kEpiPlain) {
+#pragma unroll
+      for (int g = 0; g < kNG; ++g) {
+        if (!e_ok[g] || e_row[g] >= a.dim) continue;
+        const int wd = a.width;
+        T* __restrict__ win = static_cast<T*>(a.ctx) + ((size_t)e_b[g] * a.dim + e_row[g]) * (wd - 1);
+#pragma unroll
+        for (int j = 0; j + 1 < kMaxTaps - 1; ++j)
+          if (j + 1 < wd - 1) Elem<T>::store1(win + j, e_win[g][j + 1]);
+        Elem<T>::store1(win + wd - 2, xs_keep[g]);
+      }
+    }
+  }
+
   __device__ __forceinline__ void load_pass(const GemvArgs& a, int kb) {
     const T* __restrict__ W = static_cast<const T*>(a.W);
     const int O = a.O, K = a.K;
@@ -594,11 +614,15 @@ struct GemvWork {
           const float xcv = round_to<T>(silu_f(cv));
           if constexpr (!kChain) Elem<T>::store1(static_cast<T*>(a.xc) + (size_t)bl * a.dim + row, xcv);
           if constexpr (kXP) sm.xc[bl][row - xblk0] = xcv;
-          T* __restrict__ win = static_cast<T*>(a.ctx) + ((size_t)bl * a.dim + row) * (wd - 1);
+          if constexpr (kChain) {
+            xs_keep[g] = xs;  // see store_window
+          } else {
+            T* __restrict__ win = static_cast<T*>(a.ctx) + ((size_t)bl * a.dim + row) * (wd - 1);
 #pragma unroll
-          for (int j = 0; j + 1 < kMaxTaps - 1; ++j)
-            if (j + 1 < wd - 1) Elem<T>::store1(win + j, e_win[g][j + 1]);
-          Elem<T>::store1(win + wd - 2, xs);
+            for (int j = 0; j + 1 < kMaxTaps - 1; ++j)
+              if (j + 1 < wd - 1) Elem<T>::store1(win + j, e_win[g][j + 1]);
+            Elem<T>::store1(win + wd - 2, xs);
+          }
         }
       }
     }
@@ -673,7 +697,8 @@ struct SsmArgs {
 // As with GemvWork, the loads come in separate steps (the partials, the
 // operands that do not depend on p, and the activations xc and z).  The layer
 // chain reads xc and z as LL units, sums the partials itself into s_p and
-// calls compute<true>, which leaves y in an LDS tile.
+// calls compute<true>, which leaves y in an LDS tile and keeps the new state
+// in registers until store_state.
 template <typename T, int kN, bool kVecR, bool kParts, int kSplit = 1, int kPL = kPartLoads,
           int kMaxRC = 16>
 struct SsmStep {
@@ -844,13 +869,24 @@ struct SsmStep {
         hn[i] = fmaf(av, hn[i], du * s_p[R + n]);
         out = fmaf(s_p[R + kN + n], hn[i], out);
       }
-      *reinterpret_cast<float4*>(h + 4 * g) = make_float4(hn[0], hn[1], hn[2], hn[3]);
+      if constexpr (kChain) hv[g] = make_float4(hn[0], hn[1], hn[2], hn[3]);  // see store_state
+      else *reinterpret_cast<float4*>(h + 4 * g) = make_float4(hn[0], hn[1], hn[2], hn[3]);
     }
     out = split_sum(out);
     if (q != 0) return;
     out = fmaf(a.Dv ? dv_v : 0.0f, u, out);
     if constexpr (kChain) s_y[threadIdx.x / kSplit] = out * silu_f(z);
     else Elem<T>::store1(static_cast<T*>(a.y) + (size_t)b * a.dim + d, out * silu_f(z));
+  }
+
+  // After compute<true>: write the updated state back.  The layer chain calls
+  // it after the y hand-off stores, which the other workgroups wait for; the
+  // state is read again only at the next token step.
+  __device__ __forceinline__ void store_state(const SsmArgs& a) {
+    if (d >= a.dim) return;
+    float* __restrict__ h = a.state + ((size_t)b * a.dim + dc) * kN + q * kNS;
+#pragma unroll
+    for (int g = 0; g < kNS / 4; ++g) *reinterpret_cast<float4*>(h + 4 * g) = hv[g];
   }
 };
 
@@ -1072,6 +1108,9 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
                (uint32_t)((bb * a.dim + c0) / V + uu),
                LLVal<T>::pack(src[uu * V], src[(uu * V + 1) % kXBlock]), flag);
       }
+      // the conv cache after the hand-off stores (stores issue in order, so
+      // cache writes issued first would hold up the units others wait for)
+      p1.store_window(g1);
     }
 
     // phase 2: partial sums, dt projection, state update, gate.  The nd
@@ -1145,6 +1184,7 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
         ll_put(dev_rsrc(lb + a.ll_y, cbytes), (uint32_t)((bb * a.dim + d0) / V + threadIdx.x),
                LLVal<T>::pack(s_y[i], s_y[(i + 1) % kDecThreads]), flag);
       }
+      p2.store_state(s2);  // the SSM state after the y hand-off stores
     }
 
     // phase 3: out-projection + residual -> the next layer's input
