@@ -1015,8 +1015,8 @@ __device__ __forceinline__ GemvArgs out_proj_args(const LayersArgs& a, const Lay
 
 // Phase shapes of the layer chain: 8 waves per workgroup (two per SIMD, so
 // each phase's instruction latency is shared out), two rows per wave for the
-// in-projection, two K-slices of one or two rows per wave for the
-// out-projection, two threads per channel for the state update.
+// in-projection, two K-slices of two rows per wave for the out-projection,
+// two threads per channel for the state update.
 constexpr int kChainWaves = 8;
 constexpr int kChainThreads = 64 * kChainWaves;
 constexpr int kChainSplit = kChainThreads / kDecThreads;  // threads per channel in phase 2
@@ -1424,15 +1424,17 @@ hipError_t launch_ssm_step_t(const SsmArgs& a, int nstate, bool vecR, hipStream_
   }
 }
 
-// out-projection rows per wave of the layer chain: one up to K = 1024 rows
-// (256 workgroups of kChainWaves / kChainKSplit = 4 row waves), two past that
-inline int chain_rows3(int K) { return K <= 1024 ? 1 : 2; }
+// out-projection rows per wave of the layer chain.  Two rows (8 per
+// workgroup) rather than one: every out-projection workgroup reads all of y,
+// so half as many of them halve that hand-off's reads (at config 4, 4 MB
+// instead of 8 MB per layer), and the workgroups past them skip the phase.
+constexpr int kChainRows3 = 2;
 
 // workgroups the layer chain runs with: the largest of its three phases
 int layers_grid(int B, int K, int dim) {
   const int n1 = (2 * dim + kXBlock - 1) / kXBlock;
   const int n2 = ((dim + kDecThreads - 1) / kDecThreads) * B;
-  const int rows = (kChainWaves / kChainKSplit) * chain_rows3(K);
+  const int rows = (kChainWaves / kChainKSplit) * kChainRows3;
   const int n3 = (K + rows - 1) / rows;
   return std::max(n1, std::max(n2, n3));
 }
@@ -1470,8 +1472,7 @@ hipError_t launch_layers_k(const LayersArgs& a, hipStream_t st) {
 
 template <typename T, int kMB>
 hipError_t launch_layers_b(const LayersArgs& a, hipStream_t st) {
-  if (chain_rows3(a.K) == 1) return launch_layers_k<T, kMB, 16, 1>(a, st);
-  return launch_layers_k<T, kMB, 16, 2>(a, st);
+  return launch_layers_k<T, kMB, 16, kChainRows3>(a, st);
 }
 
 template <typename T>
