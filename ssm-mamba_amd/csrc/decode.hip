@@ -683,7 +683,7 @@ struct SsmArgs {
 //   y = (sum_n C h' + D xc) * silu(z),   C = p[b, R+N:R+2N], z = xz[b, dim + d]
 // (modules/mamba.py:216-240 with selective_update/kernel.cu:39-71; the T
 // roundings mirror the reference's intermediate T tensors).  A workgroup of
-// kThreads = 256 kSplit threads covers 256 channels of one batch row.  With
+// kThreads = kChan kSplit threads covers kChan channels of one batch row.  With
 // kSplit > 1 the threads of a channel (adjacent lanes) split the dt dot
 // product by chunks and the output sum by states, and combine both with
 // butterfly adds (a fixed order).
@@ -700,10 +700,10 @@ struct SsmArgs {
 // calls compute<true>, which leaves y in an LDS tile and keeps the new state
 // in registers until store_state.
 template <typename T, int kN, bool kVecR, bool kParts, int kSplit = 1, int kPL = kPartLoads,
-          int kMaxRC = 16>
+          int kMaxRC = 16, int kChan = kDecThreads>
 struct SsmStep {
   static constexpr int E = Chunk<T>::E;
-  static constexpr int kThreads = kDecThreads * kSplit;
+  static constexpr int kThreads = kChan * kSplit;
   static constexpr int kNS = kN / kSplit;               // states per thread
   static_assert(kNS % 4 == 0 && (kSplit & (kSplit - 1)) == 0, "whole float4 state groups per thread");
   // dt-projection chunks per row: R <= kMaxRC E
@@ -720,7 +720,7 @@ struct SsmStep {
   __device__ __forceinline__ void begin(const SsmArgs& a, int dblk, int brow) {
     b = brow;
     q = threadIdx.x % kSplit;
-    d = dblk * kDecThreads + threadIdx.x / kSplit;
+    d = dblk * kChan + threadIdx.x / kSplit;
     dc = min(d, a.dim - 1);
     ng = a.nout4 >> 2;
     S = kParts ? kThreads / ng : 1;
@@ -916,8 +916,9 @@ __global__ __launch_bounds__(kDecThreads) void ssm_step_kernel(const SsmArgs a) 
 // phase 1 (workgroup i < n1): in-projection rows [16 i, 16 i + 16), norm,
 //          conv step and the x-projection partial of the x half: xc (x half)
 //          or z (z half) and the partials out as LL units;
-// phase 2 (i < n2):        the state update of 256 channels of one batch row
-//          from the partials, xc and z: y out as LL units;
+// phase 2 (n2 workgroups from the z half on): the state update of 128
+//          channels of one batch row from the partials, xc and z: y out as LL
+//          units;
 // phase 3 (i < n3):        out-projection rows + residual from y: the next
 //          layer's input out as LL units (the last layer's to x_out).
 //
@@ -1016,10 +1017,13 @@ __device__ __forceinline__ GemvArgs out_proj_args(const LayersArgs& a, const Lay
 // Phase shapes of the layer chain: 8 waves per workgroup (two per SIMD, so
 // each phase's instruction latency is shared out), two rows per wave for the
 // in-projection, two K-slices of two rows per wave for the out-projection,
-// two threads per channel for the state update.
+// four threads per channel (4 of the 16 states each) for the state update, so
+// that 128 channels per workgroup spread it over twice as many workgroups as
+// 256 would (at config 4, 64 instead of 32).
 constexpr int kChainWaves = 8;
 constexpr int kChainThreads = 64 * kChainWaves;
-constexpr int kChainSplit = kChainThreads / kDecThreads;  // threads per channel in phase 2
+constexpr int kChainChan = 128;                           // channels per phase-2 workgroup
+constexpr int kChainSplit = kChainThreads / kChainChan;   // threads per channel in phase 2
 constexpr int kChainKSplit = 2;                            // K-slices of the out-projection
 constexpr int kChainRows1 = kXBlock / kChainWaves;         // in-projection rows per wave
 constexpr int kChainTaps = 4;                              // conv width limit
@@ -1028,7 +1032,7 @@ constexpr int kChainRC = 8;                                // dt rank up to 8 16
 template <typename T, int kMB, int kN, int kRows3>
 struct Chain {
   using P1 = GemvWork<T, kMB, kChainRows1, true, kEpiConvX, kChainWaves, 1, 2, kChainTaps>;
-  using P2 = SsmStep<T, kN, true, true, kChainSplit, 1, kChainRC>;
+  using P2 = SsmStep<T, kN, true, true, kChainSplit, 1, kChainRC, kChainChan>;
   using P3 = GemvWork<T, kMB, kRows3, false, kEpiPlain, kChainWaves, kChainKSplit, 2>;
 };
 
@@ -1044,11 +1048,11 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
   } gsm;
   __shared__ __align__(16) float s_p[kMaxXOut];
   __shared__ float4 s_red[kChainThreads];
-  __shared__ float s_y[kDecThreads];
+  __shared__ float s_y[kChainChan];
   __shared__ unsigned s_flag;
   const int blk = blockIdx.x;
   const int n1 = (2 * a.dim + kXBlock - 1) / kXBlock;
-  const int nd = (a.dim + kDecThreads - 1) / kDecThreads;
+  const int nd = (a.dim + kChainChan - 1) / kChainChan;
   const int n2 = nd * a.B;
   const int n3 = (a.K + P3::kXB - 1) / P3::kXB;
   // workgroups past a GEMV phase's blocks load the last block's operands (read
@@ -1125,7 +1129,7 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
     const int z2 = max(0, min(a.dim / kXBlock, (int)gridDim.x - n2));
     if (blk - z2 >= 0 && blk - z2 < n2) {
       const int blk2 = blk - z2;
-      const int bb = blk2 / nd, dblk = blk2 % nd, d0 = dblk * kDecThreads;
+      const int bb = blk2 / nd, dblk = blk2 % nd, d0 = dblk * kChainChan;
       const int ng = a.nout4 / 4;
       P2 p2;
       p2.begin(s2, dblk, bb);
@@ -1178,11 +1182,11 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
       __syncthreads();
       p2.template compute<true>(s2, s_p, s_y);
       __syncthreads();
-      constexpr int kU = kDecThreads / V;
+      constexpr int kU = kChainChan / V;
       if ((int)threadIdx.x < kU && d0 + (int)threadIdx.x * V < a.dim) {
         const int i = threadIdx.x * V;
         ll_put(dev_rsrc(lb + a.ll_y, cbytes), (uint32_t)((bb * a.dim + d0) / V + threadIdx.x),
-               LLVal<T>::pack(s_y[i], s_y[(i + 1) % kDecThreads]), flag);
+               LLVal<T>::pack(s_y[i], s_y[(i + 1) % kChainChan]), flag);
       }
       p2.store_state(s2);  // the SSM state after the y hand-off stores
     }
@@ -1433,7 +1437,7 @@ constexpr int kChainRows3 = 2;
 // workgroups the layer chain runs with: the largest of its three phases
 int layers_grid(int B, int K, int dim) {
   const int n1 = (2 * dim + kXBlock - 1) / kXBlock;
-  const int n2 = ((dim + kDecThreads - 1) / kDecThreads) * B;
+  const int n2 = ((dim + kChainChan - 1) / kChainChan) * B;
   const int rows = (kChainWaves / kChainKSplit) * kChainRows3;
   const int n3 = (K + rows - 1) / rows;
   return std::max(n1, std::max(n2, n3));
@@ -1492,7 +1496,7 @@ const char* layers_unsupported_t(int K, int dim, int nout) {
   if (K > C::P1::PK) return "model_dim exceeds the in-projection's single pass";
   if (dim > C::P3::PK) return "dim exceeds the out-projection's single pass";
   const int ng = ((nout + 3) & ~3) / 4;
-  const int nd = (dim + kDecThreads - 1) / kDecThreads;
+  const int nd = (dim + kChainChan - 1) / kChainChan;
   const int nparts = dim / kXBlock;
   if (((nparts + nd - 1) / nd) * ng > kChainThreads)
     return "too many x-projection partial blocks per state-update workgroup";
@@ -1563,7 +1567,7 @@ LayersWs layers_ws(int B, int nlayers, int K, int dim, int nout, int elem) {
   size_t o = 0;
   w.x = o; o += up((size_t)B * K / V * 8);
   w.p = o; o += up((size_t)(dim / kXBlock) * B * ((nout + 3) & ~3) * 8);
-  w.q = o; o += up((size_t)B * ((dim + kDecThreads - 1) / kDecThreads) * ((nout + 3) & ~3) * 8);
+  w.q = o; o += up((size_t)B * ((dim + kChainChan - 1) / kChainChan) * ((nout + 3) & ~3) * 8);
   w.xc = o; o += up((size_t)B * dim / V * 8);
   w.z = o; o += up((size_t)B * dim / V * 8);
   w.y = o; o += up((size_t)B * dim / V * 8);

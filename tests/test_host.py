@@ -238,8 +238,9 @@ def test_layer_chain_arguments_are_checked():
     ws = lib.ssm_decode_layers_workspace(4, 48, 1024, 2048, 96, N.SSM_BF16)
     # the sync area (3 lines of 256 B), then per layer 8-byte units of 2 bf16
     # (x: 4 x 1024; xc, z, y: 4 x 2048) or 1 fp32 (partials: 128 blocks of
-    # 4 x 96; their slice sums: 4 rows x 8 slices x 96)
-    per_layer = (4 * 1024 // 2 + 3 * 4 * 2048 // 2 + 128 * 4 * 96 + 4 * 8 * 96) * 8
+    # 4 x 96; their slice sums: 4 rows x 16 slices x 96, one slice per
+    # state-update workgroup of 128 channels)
+    per_layer = (4 * 1024 // 2 + 3 * 4 * 2048 // 2 + 128 * 4 * 96 + 4 * 16 * 96) * 8
     assert ws == 3 * 256 + 48 * per_layer
     assert lib.ssm_decode_layers_workspace(4, 48, 1024, 2047, 96, N.SSM_BF16) == 0
     assert lib.ssm_decode_layers_workspace(4, 0, 1024, 2048, 96, N.SSM_BF16) == 0
