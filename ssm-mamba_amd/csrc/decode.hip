@@ -705,7 +705,10 @@ struct SsmStep {
   static constexpr int E = Chunk<T>::E;
   static constexpr int kThreads = kChan * kSplit;
   static constexpr int kNS = kN / kSplit;               // states per thread
-  static_assert(kNS % 4 == 0 && (kSplit & (kSplit - 1)) == 0, "whole float4 state groups per thread");
+  static_assert((kNS % 4 == 0 || kNS == 2) && (kSplit & (kSplit - 1)) == 0,
+                "whole float4 (or one float2) state groups per thread");
+  static constexpr int kSV = kNS < 4 ? kNS : 4;  // states per vector load / store
+  using SV = typename std::conditional<kSV == 4, float4, float2>::type;
   // dt-projection chunks per row: R <= kMaxRC E
   static constexpr int kRC = kMaxRC / kSplit;           // of them held by one thread
   using Raw = typename Chunk<T>::Raw;
@@ -713,7 +716,7 @@ struct SsmStep {
   int b, d, dc, q, ng, S, sg, gi, w0, w1;
   float4 pv[kParts ? kPL : 1];
   Raw wv[kVecR ? kRC : 1];
-  float4 hv[kNS / 4];
+  float hs[kNS];  // this thread's states
   float la[kNS];
   float bias_v, dv_v, u, z;
 
@@ -761,7 +764,10 @@ struct SsmStep {
     }
     const float* __restrict__ h = a.state + ((size_t)b * a.dim + dc) * kN + q * kNS;
 #pragma unroll
-    for (int g = 0; g < kNS / 4; ++g) hv[g] = *reinterpret_cast<const float4*>(h + 4 * g);
+    for (int g = 0; g < kNS / kSV; ++g) {
+      const SV v = *reinterpret_cast<const SV*>(h + kSV * g);
+      __builtin_memcpy(&hs[kSV * g], &v, sizeof(v));
+    }
 #pragma unroll
     for (int n = 0; n < kNS; ++n) la[n] = Elem<T>::load1(logA + (size_t)dc * kN + q * kNS + n);
     // absent dt_bias / D read a valid stand-in (log_A) and are dropped at use:
@@ -860,17 +866,19 @@ struct SsmStep {
     float out = 0.0f;
     float* __restrict__ h = a.state + ((size_t)b * a.dim + dc) * kN + q * kNS;
 #pragma unroll
-    for (int g = 0; g < kNS / 4; ++g) {
-      float hn[4] = {hv[g].x, hv[g].y, hv[g].z, hv[g].w};
+    for (int g = 0; g < kNS / kSV; ++g) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int nl = 4 * g + i, n = q * kNS + nl;
+      for (int i = 0; i < kSV; ++i) {
+        const int nl = kSV * g + i, n = q * kNS + nl;
         const float av = fast_exp2(-dt * fast_exp2(la[nl] * kLog2e) * kLog2e);  // exp(dt * A), A = -exp(log_A)
-        hn[i] = fmaf(av, hn[i], du * s_p[R + n]);
-        out = fmaf(s_p[R + kN + n], hn[i], out);
+        hs[nl] = fmaf(av, hs[nl], du * s_p[R + n]);
+        out = fmaf(s_p[R + kN + n], hs[nl], out);
       }
-      if constexpr (kChain) hv[g] = make_float4(hn[0], hn[1], hn[2], hn[3]);  // see store_state
-      else *reinterpret_cast<float4*>(h + 4 * g) = make_float4(hn[0], hn[1], hn[2], hn[3]);
+      if constexpr (!kChain) {  // kChain: see store_state
+        SV v;
+        __builtin_memcpy(&v, &hs[kSV * g], sizeof(v));
+        *reinterpret_cast<SV*>(h + kSV * g) = v;
+      }
     }
     out = split_sum(out);
     if (q != 0) return;
@@ -886,7 +894,11 @@ struct SsmStep {
     if (d >= a.dim) return;
     float* __restrict__ h = a.state + ((size_t)b * a.dim + dc) * kN + q * kNS;
 #pragma unroll
-    for (int g = 0; g < kNS / 4; ++g) *reinterpret_cast<float4*>(h + 4 * g) = hv[g];
+    for (int g = 0; g < kNS / kSV; ++g) {
+      SV v;
+      __builtin_memcpy(&v, &hs[kSV * g], sizeof(v));
+      *reinterpret_cast<SV*>(h + kSV * g) = v;
+    }
   }
 };
 
@@ -1117,11 +1129,11 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
       p1.store_window(g1);
     }
 
-    // phase 2: partial sums, dt projection, state update, gate.  The nd
-    // workgroups of a batch row first sum one nd-th of its partial blocks each
-    // (in block order) and publish those slice sums; each then adds the nd
-    // slice sums (in slice order): two small hand-offs instead of every
-    // workgroup reading all of its row's partial blocks.  Phase 2 runs on the
+    // phase 2: partial sums, dt projection, state update, gate.  The first
+    // ns of the nd workgroups of a batch row each sum one ns-th of its partial
+    // blocks (in block order) and publish those slice sums; each of the nd then
+    // adds the ns slice sums (in slice order): two small hand-offs instead of
+    // every workgroup reading all of its row's partial blocks.  Phase 2 runs on the
     // workgroups of phase 1's z half (from z2 on) where there are enough of
     // them: they finish phase 1 earlier (no conv step or x-projection
     // partials), so their phase-2 operand loads are in before the partials
@@ -1134,38 +1146,43 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
       P2 p2;
       p2.begin(s2, dblk, bb);
       p2.load_operands(s2);
-      const int w_lo = dblk * a.nparts / nd, nw = (dblk + 1) * a.nparts / nd - w_lo;
-      {
-        const int t = threadIdx.x, wl = t / ng, gi = t - wl * ng;
-        const uint32_t u0 = (uint32_t)(((w_lo + min(wl, nw - 1)) * a.B + bb) * a.nout4 + 4 * gi);
-        const uint32_t pairs[2] = {u0, u0 + 2};
-        u32x4_v v[2];
-        const bool ok = ll_wait2<2>(dev_rsrc(lb + a.ll_p, pbytes), pairs, wl < nw, w, v);
-        if (wl < nw)
-          s_red[t] = make_float4(__uint_as_float(v[0][0]), __uint_as_float(v[0][2]),
-                                 __uint_as_float(v[1][0]), __uint_as_float(v[1][2]));
-        if (__syncthreads_or(!ok)) {
-          if (threadIdx.x == 0) dev_store_u32(err, 1u);
-          return;
+      // ns slices of the partial blocks, one per workgroup dblk < ns (every
+      // workgroup then reads all ns slice sums in one round: ns ng <= threads)
+      const int ns = min(nd, kChainThreads / ng);
+      if (dblk < ns) {
+        const int w_lo = dblk * a.nparts / ns, nw = (dblk + 1) * a.nparts / ns - w_lo;
+        {
+          const int t = threadIdx.x, wl = t / ng, gi = t - wl * ng;
+          const uint32_t u0 = (uint32_t)(((w_lo + min(wl, nw - 1)) * a.B + bb) * a.nout4 + 4 * gi);
+          const uint32_t pairs[2] = {u0, u0 + 2};
+          u32x4_v v[2];
+          const bool ok = ll_wait2<2>(dev_rsrc(lb + a.ll_p, pbytes), pairs, wl < nw, w, v);
+          if (wl < nw)
+            s_red[t] = make_float4(__uint_as_float(v[0][0]), __uint_as_float(v[0][2]),
+                                   __uint_as_float(v[1][0]), __uint_as_float(v[1][2]));
+          if (__syncthreads_or(!ok)) {
+            if (threadIdx.x == 0) dev_store_u32(err, 1u);
+            return;
+          }
         }
-      }
-      if ((int)threadIdx.x < a.nout4) {
-        const int jc = threadIdx.x;
-        const float* r = reinterpret_cast<const float*>(s_red) + jc;
-        float t = 0.0f;
-        for (int wl = 0; wl < nw; ++wl) t += r[wl * a.nout4];
-        ll_put(dev_rsrc(lb + a.ll_q, qbytes), (uint32_t)((bb * nd + dblk) * a.nout4 + jc),
-               __float_as_uint(t), flag);
+        if ((int)threadIdx.x < a.nout4) {
+          const int jc = threadIdx.x;
+          const float* r = reinterpret_cast<const float*>(s_red) + jc;
+          float t = 0.0f;
+          for (int wl = 0; wl < nw; ++wl) t += r[wl * a.nout4];
+          ll_put(dev_rsrc(lb + a.ll_q, qbytes), (uint32_t)((bb * nd + dblk) * a.nout4 + jc),
+                 __float_as_uint(t), flag);
+        }
       }
       {
         const int t = threadIdx.x, sl = t / ng, gi = t - sl * ng;
-        const uint32_t u0 = (uint32_t)((bb * nd + min(sl, nd - 1)) * a.nout4 + 4 * gi);
+        const uint32_t u0 = (uint32_t)((bb * nd + min(sl, ns - 1)) * a.nout4 + 4 * gi);
         const uint32_t pairs[2] = {u0, u0 + 2};
         u32x4_v v[2];
-        const bool ok_q = ll_wait2<2>(dev_rsrc(lb + a.ll_q, qbytes), pairs, sl < nd, w, v);
+        const bool ok_q = ll_wait2<2>(dev_rsrc(lb + a.ll_q, qbytes), pairs, sl < ns, w, v);
         const bool ok_a = p2.load_act_ll(s2, w);
         __syncthreads();  // every thread is done with the slice sums in s_red
-        if (sl < nd)
+        if (sl < ns)
           s_red[t] = make_float4(__uint_as_float(v[0][0]), __uint_as_float(v[0][2]),
                                  __uint_as_float(v[1][0]), __uint_as_float(v[1][2]));
         if (__syncthreads_or(!(ok_q && ok_a))) {
@@ -1176,7 +1193,7 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
       if ((int)threadIdx.x < a.nout) {
         const float* r = reinterpret_cast<const float*>(s_red) + threadIdx.x;
         float t = 0.0f;
-        for (int sl = 0; sl < nd; ++sl) t += r[sl * a.nout4];
+        for (int sl = 0; sl < ns; ++sl) t += r[sl * a.nout4];
         s_p[threadIdx.x] = round_to<T>(t);
       }
       __syncthreads();
@@ -1497,8 +1514,9 @@ const char* layers_unsupported_t(int K, int dim, int nout) {
   if (dim > C::P3::PK) return "dim exceeds the out-projection's single pass";
   const int ng = ((nout + 3) & ~3) / 4;
   const int nd = (dim + kChainChan - 1) / kChainChan;
+  const int ns = std::min(nd, kChainThreads / ng);
   const int nparts = dim / kXBlock;
-  if (((nparts + nd - 1) / nd) * ng > kChainThreads)
+  if (ns < 1 || ((nparts + ns - 1) / ns) * ng > kChainThreads)
     return "too many x-projection partial blocks per state-update workgroup";
   return nullptr;
 }
