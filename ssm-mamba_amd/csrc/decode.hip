@@ -503,18 +503,22 @@ struct GemvWork {
 #pragma unroll
             for (int i = 0; i < E; ++i) wf[r][i] *= 1.0f + nv[i];
         }
+        // every batch row's activations first (rows past B repeat row B - 1,
+        // whose sums are never used): no branch per row, so the LDS reads are
+        // all in flight together instead of one round trip per row
+        Raw xr[kMB];
+#pragma unroll
+        for (int b = 0; b < kMB; ++b) xr[b] = *reinterpret_cast<const Raw*>(&sm.sx[min(b, B - 1)][kl]);
 #pragma unroll
         for (int b = 0; b < kMB; ++b) {
-          if (b < B) {
-            float v[E];
-            Chunk<T>::cvt(*reinterpret_cast<const Raw*>(&sm.sx[b][kl]), v);
+          float v[E];
+          Chunk<T>::cvt(xr[b], v);
 #pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-              float s = acc[r][b];
+          for (int r = 0; r < kRows; ++r) {
+            float s = acc[r][b];
 #pragma unroll
-              for (int i = 0; i < E; ++i) s = fmaf(wf[r][i], v[i], s);
-              acc[r][b] = s;
-            }
+            for (int i = 0; i < E; ++i) s = fmaf(wf[r][i], v[i], s);
+            acc[r][b] = s;
           }
         }
       }
@@ -632,14 +636,21 @@ struct GemvWork {
         const int blk = xblk0 / kXBlock;
         const size_t p0 = (size_t)blk * B * a.nout4 + threadIdx.x;
         const auto prs = dev_rsrc(a.part, (size_t)(a.dim / kXBlock) * B * a.nout4 * 8);
+        // all rows' sums first (rows past B repeat row B - 1), then the stores
+        float ps[kMB];
+#pragma unroll
+        for (int b = 0; b < kMB; ++b) {
+          const int bc = min(b, B - 1);
+          float s = 0.0f;
+#pragma unroll
+          for (int c = 0; c < kXBlock; ++c) s = fmaf(xwf[c], sm.xc[bc][c], s);
+          ps[b] = s;
+        }
 #pragma unroll
         for (int b = 0; b < kMB; ++b) {
           if (b < B) {
-            float s = 0.0f;
-#pragma unroll
-            for (int c = 0; c < kXBlock; ++c) s = fmaf(xwf[c], sm.xc[b][c], s);
-            if constexpr (kChain) ll_put(prs, (uint32_t)(p0 + (size_t)b * a.nout4), __float_as_uint(s), a.flag);
-            else a.part[p0 + (size_t)b * a.nout4] = s;
+            if constexpr (kChain) ll_put(prs, (uint32_t)(p0 + (size_t)b * a.nout4), __float_as_uint(ps[b]), a.flag);
+            else a.part[p0 + (size_t)b * a.nout4] = ps[b];
           }
         }
       }
