@@ -806,10 +806,14 @@ struct SsmStep {
     return ok_u && ok_z;
   }
 
-  // sum of v over the kSplit adjacent lanes of a channel (butterfly)
+  // sum of v over the kSplit adjacent lanes of a channel (butterfly).  Within
+  // a quad the partners are DPP quad permutations (no LDS round trip, as a
+  // shuffle would take); a + b = b + a, so every lane gets the same sum.
   __device__ __forceinline__ float split_sum(float v) const {
+    if constexpr (kSplit >= 2) v += dpp_mov<kDppQuadXor1>(v);
+    if constexpr (kSplit >= 4) v += dpp_mov<kDppQuadXor2>(v);
 #pragma unroll
-    for (int m = 1; m < kSplit; m <<= 1) v += __shfl_xor(v, m, 64);
+    for (int m = 4; m < kSplit; m <<= 1) v += __shfl_xor(v, m, 64);
     return v;
   }
 
@@ -1180,7 +1184,14 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
           const int jc = threadIdx.x;
           const float* r = reinterpret_cast<const float*>(s_red) + jc;
           float t = 0.0f;
-          for (int wl = 0; wl < nw; ++wl) t += r[wl * a.nout4];
+          for (int w0 = 0; w0 < nw; w0 += 4) {  // 4 reads in flight, then the adds in order
+            float rv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rv[i] = r[min(w0 + i, nw - 1) * a.nout4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (w0 + i < nw) t += rv[i];
+          }
           ll_put(dev_rsrc(lb + a.ll_q, qbytes), (uint32_t)((bb * nd + dblk) * a.nout4 + jc),
                  __float_as_uint(t), flag);
         }
@@ -1204,7 +1215,14 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
       if ((int)threadIdx.x < a.nout) {
         const float* r = reinterpret_cast<const float*>(s_red) + threadIdx.x;
         float t = 0.0f;
-        for (int sl = 0; sl < ns; ++sl) t += r[sl * a.nout4];
+        for (int s0 = 0; s0 < ns; s0 += 4) {  // 4 reads in flight, then the adds in order
+          float rv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) rv[i] = r[min(s0 + i, ns - 1) * a.nout4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (s0 + i < ns) t += rv[i];
+        }
         s_p[threadIdx.x] = round_to<T>(t);
       }
       __syncthreads();
