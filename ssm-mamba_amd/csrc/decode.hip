@@ -730,6 +730,7 @@ struct SsmStep {
   float hs[kNS];  // this thread's states
   float la[kNS];
   float bias_v, dv_v, u, z;
+  u32x2_v act_u, act_z;  // the chain's xc and z units as first read
 
   __device__ __forceinline__ void begin(const SsmArgs& a, int dblk, int brow) {
     b = brow;
@@ -793,14 +794,25 @@ struct SsmStep {
   }
 
   // the layer chain: xc and z of this thread's channel from LL units (B, dim / V)
-  // at a.xc and a.xz
+  // at a.xc and a.xz.  issue_act_ll reads both units once, ahead of the wait
+  // for the partial sums: they are written in the in-projection phase, before
+  // the partials' slice sums exist, so they are normally there, and their
+  // round trip runs under that wait instead of after it.  load_act_ll then
+  // polls again only for a unit whose flag was not yet set.
+  __device__ __forceinline__ void issue_act_ll(const SsmArgs& a) {
+    constexpr int V = LLVal<T>::V;
+    const uint32_t i = (uint32_t)(b * a.dim + dc);
+    const size_t bytes = (size_t)a.B * a.dim / V * 8;
+    act_u = ll_get1(dev_rsrc(a.xc, bytes), i / V);
+    act_z = ll_get1(dev_rsrc(a.xz, bytes), i / V);
+  }
   __device__ __forceinline__ bool load_act_ll(const SsmArgs& a, const LLWait& w) {
     constexpr int V = LLVal<T>::V;
     const uint32_t i = (uint32_t)(b * a.dim + dc);
     const size_t bytes = (size_t)a.B * a.dim / V * 8;
-    u32x2_v vu, vz;
-    const bool ok_u = ll_wait1(dev_rsrc(a.xc, bytes), i / V, w, vu);
-    const bool ok_z = ll_wait1(dev_rsrc(a.xz, bytes), i / V, w, vz);
+    u32x2_v vu = act_u, vz = act_z;
+    const bool ok_u = vu[1] == w.flag || ll_wait1(dev_rsrc(a.xc, bytes), i / V, w, vu);
+    const bool ok_z = vz[1] == w.flag || ll_wait1(dev_rsrc(a.xz, bytes), i / V, w, vz);
     u = LLVal<T>::get(vu[0], i % V);
     z = LLVal<T>::get(vz[0], i % V);
     return ok_u && ok_z;
@@ -1204,6 +1216,7 @@ __global__ __launch_bounds__(kChainThreads) void decode_layers_kernel(const Laye
         const uint32_t u0 = (uint32_t)((bb * nd + min(sl, ns - 1)) * a.nout4 + 4 * gi);
         const uint32_t pairs[2] = {u0, u0 + 2};
         u32x4_v v[2];
+        p2.issue_act_ll(s2);
         const bool ok_q = ll_wait2<2>(dev_rsrc(lb + a.ll_q, qbytes), pairs, sl < ns, w, v);
         const bool ok_a = p2.load_act_ll(s2, w);
         __syncthreads();  // every thread is done with the slice sums in s_red
