@@ -976,8 +976,9 @@ __global__ __launch_bounds__(kDecThreads) void ssm_step_kernel(const SsmArgs a) 
 // barrier), the chain took 0.99 ms per token at config 4 against 0.92 ms for
 // the per-layer kernels: the barriers were half of each layer's 20.6 us.  With
 // the LL hand-off, the phase placement and store order described at the
-// phases below, and LDS operands read before the arithmetic, it takes 0.70 ms
-// (14.6 us per layer, about 9 us of it hand-offs).
+// phases below, LDS operands read before the arithmetic and the state
+// update's activations read ahead of its wait, it takes 0.68 ms (14.2 us per
+// layer, about 8.5 us of it hand-offs).
 struct LayerPtrs {
   const void* w_in;     // (2 dim, K)
   const void* b_in;     // (2 dim) nullable
