@@ -99,6 +99,18 @@ __device__ __forceinline__ void fwd_block(const float4 dl4, const float4 du4, co
   }
 }
 
+// The same block without outputs (the segment summaries).
+__device__ __forceinline__ void fwd_block_state(const float4 dl4, const float4 du4, const BC2& v,
+                                                const float (&A2)[2], float (&h)[2]) {
+  const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+  const float duv[4] = {du4.x, du4.y, du4.z, du4.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) h[s] = fmaf(fast_exp2(dlv[j] * A2[s]), h[s], duv[j] * v.B(j, s));
+  }
+}
+
 // Every pointer is its own __restrict__ argument: with that no-alias
 // information the compiler can prove the output stores never clobber the
 // prepped B/C block, which is what lets its wave-uniform reads be scalar loads.
@@ -557,7 +569,17 @@ struct WsRows {
 };
 
 
-template <typename T, int kZ, bool kAligned>
+// kSum: the segment summaries instead of the scan (what scan_fwd_segsum_kernel
+// computes, with the same bits): blockIdx.z is sub-segment j of seg_len /
+// sub_k steps, the state starts from zero, the consumers run the recurrence
+// without outputs or saves and leave the final state in seg_h, and the
+// producers stage delta, delta*u and B/C only and sum the step sizes into
+// seg_dt.  A producer lane keeps two sums, one over the even and one over the
+// odd 16-step tiles of its 4-step column, and the four lanes of a channel row
+// combine them as the summary kernel's eight lanes of 32-step tiles do
+// (((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)) over its columns c), so
+// both kernels add the same numbers in the same order.
+template <typename T, int kZ, bool kAligned, bool kSum>
 __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
     const float* __restrict__ Ap, const T* __restrict__ Bp, const T* __restrict__ Cp,
@@ -565,7 +587,8 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     const float* __restrict__ h_init, const int64_t* __restrict__ length,
     const T* __restrict__ zp, T* __restrict__ out, T* __restrict__ yu,
     float* __restrict__ h_chunks, float* __restrict__ h_last, void* __restrict__ dummy,
-    const float* __restrict__ seg_h, const float* __restrict__ seg_dt) {
+    float* __restrict__ seg_h, float* __restrict__ seg_dt) {
+  static_assert(!kSum || kZ == 0, "the summaries read no gate");
   constexpr bool kHasZ = kZ != 0;
   constexpr bool kSaveY = kZ == 2;
   constexpr int kT4 = kWsTile / 4;
@@ -581,10 +604,12 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   const int d0 = blockIdx.x * kBlockCh;
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
   const int seg = blockIdx.z;
-  const int Tbeg = seg * p.seg_len;  // a multiple of kWsTile
-  const int Lend = min(L, Tbeg + p.seg_len);
+  const int span = kSum ? p.seg_len / p.sub_k : p.seg_len;  // a multiple of 2 kWsTile
+  const int Tbeg = seg * span;
+  const int Lend = min(L, Tbeg + span);
   const int ntiles = (Lend - Tbeg + kWsTile - 1) / kWsTile;
   const size_t rb = (size_t)b * Dm;
+  const size_t sb = (size_t)seg * p.batch + b;  // summary row (kSum)
 
   if (w < kWsCons) {
     // ------------------------------------------------ consumer: the recurrence
@@ -596,16 +621,16 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       const int n = 2 * w + s;
       const bool ok = ch_ok && n < N;
       A2[s] = ok ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
-      float hv = (ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
+      float hv = (!kSum && ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
       // carry in through the earlier sub-segments' affine maps, in order
-      for (int sp = 0; ok && sp < seg * p.sub_k; ++sp) {
+      for (int sp = 0; !kSum && ok && sp < seg * p.sub_k; ++sp) {
         const size_t sb = (size_t)sp * p.batch + b;
         const float decay = fast_exp2(A2[s] * seg_dt[sb * Dm + ch]);
         hv = fmaf(decay, hv, seg_h[(sb * N + n) * Dm + ch]);
       }
       h[s] = hv;
     }
-    const bool save = h_chunks != nullptr;
+    const bool save = !kSum && h_chunks != nullptr;
     const size_t hsD = (size_t)p.hs * Dm;  // floats between the saved rows of two states
     const size_t cstride = (size_t)N * hsD;  // floats between the saves of two chunks
     // the saves go through a buffer range over the wave's two state rows of
@@ -644,9 +669,13 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
         const int c = k & 1;
         if (k + 1 < kT4) read_block(buf, k + 1, bcb[c ^ 1], dlb[c ^ 1], dub[c ^ 1]);
         else read_block(nbuf, 0, bcb[c ^ 1], dlb[c ^ 1], dub[c ^ 1]);
-        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        fwd_block(dlb[c], dub[c], bcb[c], A2, h, y);
-        cY[k * kWsRow] = make_float4(y[0], y[1], y[2], y[3]);
+        if constexpr (kSum) {
+          fwd_block_state(dlb[c], dub[c], bcb[c], A2, h);
+        } else {
+          float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          fwd_block(dlb[c], dub[c], bcb[c], A2, h, y);
+          cY[k * kWsRow] = make_float4(y[0], y[1], y[2], y[3]);
+        }
       }
       // kT4 is even: the next tile's block 0 sits in buffer 0 again
       static_assert(kT4 % 2 == 0, "block 0 of every tile in register set 0");
@@ -658,7 +687,10 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       }
       buf = nbuf;
     }
-    if (!save && h_last && Lend == L) {
+    if constexpr (kSum) {
+      if (ok0) seg_h[(sb * N + 2 * w) * Dm + ch] = h[0];
+      if (ok1) seg_h[(sb * N + 2 * w + 1) * Dm + ch] = h[1];
+    } else if (!save && h_last && Lend == L) {
       if (ok0) h_last[(rb + ch) * N + 2 * w] = h[0];
       if (ok1) h_last[(rb + ch) * N + 2 * w + 1] = h[1];
     }
@@ -742,7 +774,8 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   // stage tile i into buffer sb: delta (softplus once per element, zero
   // outside the valid window), delta * u, B and C; D*u and silu(z) are kept
   // for its finish
-  auto stage = [&](const WsRows<T>& r, int i, int sb, float (&sk)[4], float (&gt)[4]) {
+  float dts[2] = {0.0f, 0.0f};  // kSum: step sizes of the even and odd tiles
+  auto stage = [&](const WsRows<T>& r, int i, int sbuf, float (&sk)[4], float (&gt)[4], int par) {
     const int t_tile = Tbeg + i * kWsTile;
     const int t = t_tile + 4 * q;
     float uv[4], dv[4], de[4], du[4];
@@ -775,9 +808,13 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) du[j] = de[j] * uv[j];
-    sSt[sb][0][q][row] = make_float4(de[0], de[1], de[2], de[3]);
-    sSt[sb][1][q][row] = make_float4(du[0], du[1], du[2], du[3]);
-    reinterpret_cast<float2*>(&sBC[sb][bc_G][bc_step])[bc_half] =
+    if constexpr (kSum) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dts[par] += de[j];
+    }
+    sSt[sbuf][0][q][row] = make_float4(de[0], de[1], de[2], de[3]);
+    sSt[sbuf][1][q][row] = make_float4(du[0], du[1], du[2], du[3]);
+    reinterpret_cast<float2*>(&sBC[sbuf][bc_G][bc_step])[bc_half] =
         bc_ok ? make_float2(bits_to_f32<T>(r.B), bits_to_f32<T>(r.C)) : make_float2(0.0f, 0.0f);
   };
 
@@ -838,12 +875,12 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   float4 v[kWsCons];
 #pragma unroll
   for (int k = 0; k < kWsRing; ++k) issue(rows[k], k);
-  stage(rows[0], 0, 0, sk[0], gt[0]);
+  stage(rows[0], 0, 0, sk[0], gt[0], 0);
   issue(rows[0], kWsRing);
-  stage(rows[1], 1, 1, sk[1], gt[1]);
+  stage(rows[1], 1, 1, sk[1], gt[1], 1);
   issue(rows[1], kWsRing + 1);
   __syncthreads();  // iteration 0
-  stage(rows[2], 2, 2, sk[2], gt[2]);
+  stage(rows[2], 2, 2, sk[2], gt[2], 0);
   issue(rows[2], kWsRing + 2);
   int sbuf = 0;  // staging buffer of tile i + 2
   for (int i0 = 1; i0 <= ntiles; i0 += 4) {
@@ -851,12 +888,22 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     for (int j = 0; j < 4; ++j) {
       const int i = i0 + j;  // (i + 2) % 4 == (j + 3) % 4, (i - 1) % 4 == j
       __syncthreads();
-      finish_read(i - 1, v);
-      stage(rows[(j + 3) % kWsRing], i + 2, sbuf, sk[(j + 3) & 3], gt[(j + 3) & 3]);
+      if constexpr (!kSum) finish_read(i - 1, v);
+      // i0 % 4 == 1, so tile i + 2 has the parity of j + 3
+      stage(rows[(j + 3) % kWsRing], i + 2, sbuf, sk[(j + 3) & 3], gt[(j + 3) & 3], (j + 3) & 1);
       issue(rows[(j + 3) % kWsRing], i + 2 + kWsRing);
-      finish(i - 1, v, sk[j], gt[j]);
+      if constexpr (!kSum) finish(i - 1, v, sk[j], gt[j]);
       sbuf = sbuf == kWsStage - 1 ? 0 : sbuf + 1;
     }
+  }
+  if constexpr (kSum) {
+    // the four lanes of a channel row are 4 consecutive lanes (q = lane % 4)
+#pragma unroll
+    for (int m = 1; m < kT4; m <<= 1) {
+      dts[0] += __shfl_xor(dts[0], m, 64);
+      dts[1] += __shfl_xor(dts[1], m, 64);
+    }
+    if (q == 0 && pch_ok) seg_dt[sb * Dm + pch] = dts[0] + dts[1];
   }
 }
 
@@ -1202,19 +1249,28 @@ static bool ws_forward(const ScanParams& p, size_t elem) {
 
 template <typename T, int kSG, int kZ, bool kAligned>
 static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t st) {
+  const bool ws = ws_forward(p, sizeof(T));
   if (p.nseg > 1) {
     ProfScope prof("scan_fwd_segsum", st);
-    hipLaunchKernelGGL((scan_fwd_segsum_kernel<T, kSG, kAligned>),
-                       dim3(p.nblk, p.batch, (p.nseg - 1) * p.sub_k), dim3(kThreads), 0, st,
-                       dims_of(p),
-                       (const T*)p.u, (const T*)p.delta, p.A, bc, p.bias, p.length, p.seg_h,
-                       p.seg_dt);
+    if (ws)
+      hipLaunchKernelGGL((scan_fwd_ws_kernel<T, 0, kAligned, true>),
+                         dim3(p.nblk, p.batch, (p.nseg - 1) * p.sub_k), dim3(kWsThreads), 0, st,
+                         dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, (const T*)p.B,
+                         (const T*)p.C, p.D, p.bias, p.h_init, p.length, (const T*)nullptr,
+                         (T*)p.out, (T*)nullptr, (float*)nullptr, (float*)nullptr, p.dummy,
+                         p.seg_h, p.seg_dt);
+    else
+      hipLaunchKernelGGL((scan_fwd_segsum_kernel<T, kSG, kAligned>),
+                         dim3(p.nblk, p.batch, (p.nseg - 1) * p.sub_k), dim3(kThreads), 0, st,
+                         dims_of(p),
+                         (const T*)p.u, (const T*)p.delta, p.A, bc, p.bias, p.length, p.seg_h,
+                         p.seg_dt);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   ProfScope prof("scan_fwd", st);
-  if (ws_forward(p, sizeof(T))) {
-    hipLaunchKernelGGL((scan_fwd_ws_kernel<T, kZ, kAligned>), dim3(p.nblk, p.batch, p.nseg),
+  if (ws) {
+    hipLaunchKernelGGL((scan_fwd_ws_kernel<T, kZ, kAligned, false>), dim3(p.nblk, p.batch, p.nseg),
                        dim3(kWsThreads), 0, st, dims_of(p), (const T*)p.u, (const T*)p.delta, p.A,
                        (const T*)p.B, (const T*)p.C, p.D, p.bias, p.h_init, p.length,
                        (const T*)p.z, (T*)p.out, (T*)p.out_ungated, p.h_chunks, p.h_last, p.dummy,
@@ -1249,15 +1305,17 @@ static hipError_t launch_fwd2(const ScanParams& p, const float* bc, bool aligned
   return launch_fwd3<T, 16>(p, bc, aligned, st);
 }
 
-// The prepped B/C layout serves the segment summaries and state counts past
-// 16; the main kernel reads B and C directly otherwise.
-bool fwd_needs_bc_prep(const ScanParams& p) { return p.nseg > 1 || p.nstate > 16; }
+// The prepped B/C layout serves state counts past 16 and the general
+// kernel's segment summaries; the role-split kernels read B and C directly.
+static bool fwd_needs_bc_prep(const ScanParams& p, size_t elem) {
+  return p.nstate > 16 || (p.nseg > 1 && !ws_forward(p, elem));
+}
 
 // bc must hold bc_prep_floats() floats; it is filled here before the scan
 // when a kernel reads the prepped layout.
 hipError_t launch_scan_fwd(const ScanParams& p, int dtype, bool aligned, float* bc,
                            hipStream_t st) {
-  if (fwd_needs_bc_prep(p)) {
+  if (fwd_needs_bc_prep(p, dtype == 1 ? 2 : 4)) {
     hipError_t e = launch_bc_prep(p, dtype, bc, st);
     if (e != hipSuccess) return e;
   }
