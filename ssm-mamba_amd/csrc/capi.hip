@@ -22,7 +22,7 @@ size_t bc_prep_floats(int batch, int nstate, int seqlen);
 size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen);
 void fwd_segments(int batch, int nblk, int seqlen, int& nseg, int& seg_len);
 size_t fwd_seg_floats(int batch, int dim, int nstate, int seqlen);
-int fwd_summary_split(int batch, int nblk, int nseg);
+int fwd_summary_split(int batch, int nblk, int nseg, int seg_len);
 int conv1d_max_width();
 int decode_max_batch();
 int decode_xproj_blocks(int64_t dim, int64_t nout);
@@ -357,7 +357,7 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   char* ws = static_cast<char*>(workspace) +
              round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
   ssm::fwd_segments((int)batch, p.nblk, (int)seqlen, p.nseg, p.seg_len);
-  p.sub_k = ssm::fwd_summary_split((int)batch, p.nblk, p.nseg);
+  p.sub_k = ssm::fwd_summary_split((int)batch, p.nblk, p.nseg, p.seg_len);
   p.seg_h = reinterpret_cast<float*>(ws);
   p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * p.sub_k * batch * nstate * dim;
   ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));

@@ -1202,16 +1202,20 @@ void fwd_segments(int batch, int nblk, int seqlen, int& nseg, int& seg_len) {
   nseg = (seqlen + seg_len - 1) / seg_len;
 }
 
-// Forward summaries per segment: the summary kernel covers segments
-// 0 .. nseg - 2 only, so with few segments it may leave CUs idle; splitting
-// each segment's summary into 2 or 4 sub-segments (of a whole number of
-// 32-step tiles) restores about one workgroup per CU.
-int fwd_summary_split(int batch, int nblk, int nseg) {
-  constexpr int kTargetWG = 256;
+// Forward summaries per segment: the summaries cover segments 0 .. nseg - 2
+// only, so with few segments they may leave CUs idle; each segment's summary
+// is split into 1, 2 or 4 sub-segments (each a whole number of 32-step
+// tiles): as many as keep to one workgroup per CU, and twice that where it still
+// leaves CUs idle and the sub-segments stay at least kMinSub steps long (a
+// summary workgroup holds at most 37 KB of LDS, so a CU runs two; shorter
+// sub-segments cost more in pipeline start-up than the extra workgroups gain).
+int fwd_summary_split(int batch, int nblk, int nseg, int seg_len) {
+  constexpr int kTargetWG = 256, kMinSub = 512;
   if (nseg <= 1) return 1;
   const long wg = (long)(nseg - 1) * batch * nblk;
   int k = 1;
   while (k < 4 && wg * 2 * k <= kTargetWG) k *= 2;
+  if (k < 4 && wg * k < kTargetWG && seg_len / (2 * k) >= kMinSub) k *= 2;
   return k;
 }
 
@@ -1219,7 +1223,7 @@ size_t fwd_seg_floats(int batch, int dim, int nstate, int seqlen) {
   int nseg, seg_len;
   const int nblk = (dim + kBlockCh - 1) / kBlockCh;
   fwd_segments(batch, nblk, seqlen, nseg, seg_len);
-  const int k = fwd_summary_split(batch, nblk, nseg);
+  const int k = fwd_summary_split(batch, nblk, nseg, seg_len);
   return (size_t)(nseg - 1) * k * batch * dim * (nstate + 1);
 }
 
