@@ -624,9 +624,9 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       float hv = (!kSum && ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
       // carry in through the earlier sub-segments' affine maps, in order
       for (int sp = 0; !kSum && ok && sp < seg * p.sub_k; ++sp) {
-        const size_t sb = (size_t)sp * p.batch + b;
-        const float decay = fast_exp2(A2[s] * seg_dt[sb * Dm + ch]);
-        hv = fmaf(decay, hv, seg_h[(sb * N + n) * Dm + ch]);
+        const size_t spb = (size_t)sp * p.batch + b;
+        const float decay = fast_exp2(A2[s] * seg_dt[spb * Dm + ch]);
+        hv = fmaf(decay, hv, seg_h[(spb * N + n) * Dm + ch]);
       }
       h[s] = hv;
     }
@@ -771,9 +771,10 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     }
   };
 
-  // stage tile i into buffer sb: delta (softplus once per element, zero
+  // stage tile i into buffer sbuf: delta (softplus once per element, zero
   // outside the valid window), delta * u, B and C; D*u and silu(z) are kept
-  // for its finish
+  // for its finish; with kSum, delta is also added to the sum of tile parity
+  // par (i % 2)
   float dts[2] = {0.0f, 0.0f};  // kSum: step sizes of the even and odd tiles
   auto stage = [&](const WsRows<T>& r, int i, int sbuf, float (&sk)[4], float (&gt)[4], int par) {
     const int t_tile = Tbeg + i * kWsTile;
