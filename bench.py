@@ -79,8 +79,18 @@ def scan_bytes(batch, dim, seqlen, nstate, s_in, has_z=True):
     return fwd, bwd
 
 
-def time_scan(ss, N, x, steps, warmup, fwd_only=False):
-    """Returns (ms per step from events around the loop, {kernel: avg ms})."""
+def time_scan(ss, N, x, steps, warmup, fwd_only=False, clock_warmup_ms=0.0, info=None):
+    """Returns (ms per step from events around the loop, {kernel: avg ms}).
+
+    clock_warmup_ms: before the `warmup` steps, run untimed steps back to
+    back until that much wall time has passed.  The engine clock of an idle
+    GPU takes about 40 ms of continuous work to reach its steady state (a
+    per-step trace of the first 600 steps of a process: 2.6 ms/step over the
+    first 5, 0.64 over steps 10-25, 0.56 from step 50 on; after 1 s idle the
+    first 20 steps run 15% slow again), so a short --warmup alone times the
+    ramp.  The steps it took are written to info["clock_warmup_steps"]."""
+    import time
+
     import torch
 
     def step():
@@ -92,6 +102,17 @@ def time_scan(ss, N, x, steps, warmup, fwd_only=False):
             ss.backward(x["u"], x["A"], x["B"], x["C"], x["D"], x["delta"], x["bias"], h, None,
                         x["dout"], None, z=x["z"], out_ungated=y)
 
+    n_clock = 0
+    if clock_warmup_ms > 0:
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < clock_warmup_ms:
+            for _ in range(8):
+                step()
+            n_clock += 8
+            torch.cuda.synchronize()
+    if info is not None:
+        info["clock_warmup_steps"] = n_clock
+        info["clock_warmup_ms"] = clock_warmup_ms
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -286,9 +307,11 @@ def decode_eager(su, dev, steps):
 def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
     """Config 4, end to end: the causal LM of ssm_mamba_amd.causal_lm at 48
     layers, d_model 1024 (d_inner 2048, N 16, conv 4, dt_rank 64), vocab 50280,
-    bf16 weights with random init, eval mode.  Prefill = one forward over 4 x
-    2048 random token ids (id 0 is the pad id, so rows may be shorter and take
-    the left-padding length path), caching the decode state; decode = exactly
+    bf16 weights with random init, eval mode.  Prefill = generate's prefill over
+    4 x 2048 random token ids (id 0 is the pad id, so rows may be shorter and
+    take the left-padding length path): every layer over the prompt, caching
+    the decode state, and the final norm and LM head at position lengths - 1
+    of each row (the full-logits forward is reported beside it); decode = exactly
     `decode_steps` greedy steps (48 layers + norm + LM head + pick each), the
     step captured once in a HIP graph and replayed.  Returns tokens/s for both
     and the share of time in the scan / state-update kernels: for the prefill
@@ -321,17 +344,23 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
         dec.prefill(ids, lengths)
         dec.replay(2)
         torch.cuda.synchronize()
-        pre = []
-        for _ in range(reps):
-            e0, e1 = ev(), ev()
-            e0.record()
-            model(ids, lengths, use_cache=True)
-            e1.record()
-            torch.cuda.synchronize()
-            pre.append(e0.elapsed_time(e1))
-        pre_ms = sorted(pre)[len(pre) // 2]
+        def median_ms(fn):
+            times = []
+            for _ in range(reps):
+                e0, e1 = ev(), ev()
+                e0.record()
+                fn()
+                e1.record()
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1))
+            return sorted(times)[len(times) // 2]
+
+        # generate's prefill: the LM head only at each row's last position
+        pre_ms = median_ms(lambda: model.forward_last(ids, lengths, use_cache=True))
+        # forward with the logits of every position, for reference
+        full_ms = median_ms(lambda: model(ids, lengths, use_cache=True))
         N.profile_begin()
-        model(ids, lengths, use_cache=True)
+        model.forward_last(ids, lengths, use_cache=True)
         prof = N.profile_end()
         scan_ms = sum(v[1] for k, v in prof.items() if k in ("scan_fwd", "scan_fwd_segsum", "bc_prep"))
 
@@ -417,6 +446,8 @@ def time_e2e(dev, decode_steps: int = 128, reps: int = 3):
         "params": n_params,
         "prompt_lengths": lengths.tolist(),
         "prefill_ms": round(pre_ms, 3),
+        "prefill_note": "generate's prefill: the LM head at each row's position lengths - 1 only",
+        "prefill_all_logits_ms": round(full_ms, 3),
         "prefill_tokens_per_s": round(batch * seqlen / (pre_ms * 1e-3), 1),
         "prefill_scan_share": round(scan_ms / pre_ms, 4),
         "prefill_scan_ms": round(scan_ms, 3),
@@ -518,10 +549,13 @@ def _cpu_model() -> str:
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    # the GPU clocks take about 50 steps (40 ms) to settle after the first
-    # launches; the timed steps then measure the steady state
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=50)
+    # the engine clock takes about 40 ms of continuous work to settle (see
+    # time_scan); this untimed warm-up runs ahead of --warmup and is reported
+    # in the JSON line as "clock_warmup"
+    ap.add_argument("--clock-warmup-ms", type=float, default=200.0,
+                    help="untimed config-1 steps run back to back for this long before --warmup")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-extra", action="store_true", help="only the config-1 step")
@@ -565,7 +599,9 @@ def main():
         print("profile run done", flush=True)
         return
     fwd_b, bwd_b = scan_bytes(batch, dim, seqlen, nstate, 2)
-    ms, kern = time_scan(ss, N, x, args.steps, args.warmup)
+    cw = {}
+    ms, kern = time_scan(ss, N, x, args.steps, args.warmup, clock_warmup_ms=args.clock_warmup_ms,
+                         info=cw)
     gbs = (fwd_b + bwd_b) / (ms * 1e-3) / 1e9
     t_fwd, t_bwd = kern.get("scan_fwd", 0.0), kern.get("scan_bwd", 0.0)
     if t_bwd >= t_fwd:
@@ -581,6 +617,9 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_warmup": {"steps": cw["clock_warmup_steps"], "ms": cw["clock_warmup_ms"],
+                         "note": "untimed steps run back to back ahead of --warmup until the "
+                                 "engine clock settles (about 40 ms of work from idle)"},
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -622,13 +661,13 @@ def main():
                          "cold_GBs": round(44_937_216 / (flushed * 1e-6) / 1e9, 1)}
         res["host_overhead"] = time_host_overhead(dev)
         x0 = inputs(2, 1536, 512, 16, torch.float32, dev, seed=0)
-        ms0, k0 = time_scan(ss, N, x0, 20, 3, fwd_only=True)
+        ms0, k0 = time_scan(ss, N, x0, 20, 3, fwd_only=True, clock_warmup_ms=50.0)
         f0, _ = scan_bytes(2, 1536, 512, 16, 4)
         res["config0_fwd"] = {"ms": round(k0["scan_fwd"], 4),
                               "GBs": round(f0 / (k0["scan_fwd"] * 1e-3) / 1e9, 1)}
         del x0
         x3 = inputs(1, 2560, 16384, 16, torch.float32, dev, seed=3, delta_shift=2.0)
-        ms3, k3 = time_scan(ss, N, x3, 3, 1)
+        ms3, k3 = time_scan(ss, N, x3, 10, 2, clock_warmup_ms=50.0)
         f3, b3 = scan_bytes(1, 2560, 16384, 16, 4)
         res["config3_fwd_bwd"] = {"ms_per_step": round(ms3, 4),
                                   "GBs": round((f3 + b3) / (ms3 * 1e-3) / 1e9, 1),

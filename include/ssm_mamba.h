@@ -18,12 +18,19 @@
  * ddelta_bias (dim); h_init/h_last/dh_last/dh_init (batch, dim, nstate);
  * h_chunks (batch, ssm_scan_nchunks(seqlen), nstate, dim): the state after
  * each SSM_CHUNK steps, channel-contiguous (h_chunks[:, -1] transposed is the
- * final state); or, with h_pairs = 1, (batch, ssm_scan_nchunks(seqlen),
- * 2 * nstate, dim) holding for each state n the product of the decays
- * exp(delta_t A) from step 0 to the chunk end in row 2n and the state in row
- * 2n + 1 -- the reference's (prod a, h) chunk carry
- * (csrc/selective_scan/forward_kernel.cu:225-228) with its
- * (batch, dim, nchunks, 2 * nstate) index order as a strided view;
+ * final state); or, with h_pairs = 1, the pair layout
+ * (batch, SSM_REF_SLOTS * ssm_scan_ref_nchunks(seqlen), 2 * nstate, dim):
+ * slot s holds in row 2n + 1 the state after SSM_CHUNK * (s + 1) steps
+ * (s < ssm_scan_nchunks(seqlen)), and slot SSM_REF_SLOTS * c + 7, the last of
+ * the reference's 128-step chunk c, holds in row 2n the product of the decays
+ * exp(delta_t A) from step 0 to that chunk's end and in row 2n + 1 the state
+ * at its end (the final state for the last chunk, also when seqlen is not a
+ * multiple of 128): the reference's (prod a, h) chunk carry
+ * (csrc/selective_scan/forward_kernel.cu:225-228, chunks of
+ * kernel_config::chunk_size = 128 steps, kernel_config.h:4-10), seen in the
+ * reference's (batch, dim, nchunks, 2 * nstate) index order as a strided view
+ * with chunk stride SSM_REF_SLOTS slots and offset 7 slots; the other slots'
+ * even rows are not written;
  * length (batch) int64.
  */
 #ifndef SSM_MAMBA_H_
@@ -38,7 +45,7 @@ extern "C" {
 
 enum { SSM_F32 = 0, SSM_BF16 = 1 };
 enum { SSM_OK = 0, SSM_ERR_INVALID = 1, SSM_ERR_UNSUPPORTED = 2, SSM_ERR_HIP = 3 };
-enum { SSM_CHUNK = 16 };
+enum { SSM_CHUNK = 16, SSM_REF_CHUNK = 128, SSM_REF_SLOTS = SSM_REF_CHUNK / SSM_CHUNK };
 
 /* Message for the last failed call on this thread ("" if none). */
 const char* ssm_last_error(void);
@@ -60,6 +67,10 @@ int ssm_profile_end(char* buf, size_t buf_bytes);
 
 /* Number of saved states per row: ceil(seqlen / SSM_CHUNK). */
 int64_t ssm_scan_nchunks(int64_t seqlen);
+/* Number of the reference's chunks per row, ceil(seqlen / SSM_REF_CHUNK)
+ * (kernel_config::get_num_chunks, csrc/selective_scan/kernel_config.h:8-10):
+ * the chunk count of the pair layout (h_pairs = 1). */
+int64_t ssm_scan_ref_nchunks(int64_t seqlen);
 
 /* Device workspace (bytes) for ssm_selective_scan_fwd / _bwd. */
 size_t ssm_scan_fwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate);
@@ -74,9 +85,10 @@ size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, 
  *   out      = (D*u + sum_n C*h) [* silu(z)]  with h_t = exp(delta_t*A) h_{t-1}
  *              + delta_t*u_t*B_t, delta = softplus(delta_raw + delta_bias)
  *              (no softplus when delta_softplus == 0)
- *   h_chunks = states after each SSM_CHUNK steps (h_pairs = 1: with the
- *              chunk decays, see above), or NULL (inference); then h_last
- *              (nullable) receives the final state.
+ *   h_chunks = states after each SSM_CHUNK steps (h_pairs = 1: the pair
+ *              layout with the reference's 128-step chunk carry, see above),
+ *              or NULL (inference); then h_last (nullable) receives the
+ *              final state.
  *   out_ungated (nullable, requires z) = D*u + sum_n C*h, the output before
  *              the gate: the backward needs it for dz.  The reference gates
  *              outside the kernel (modules/mamba.py:182), where autograd
@@ -331,9 +343,14 @@ int ssm_decode_ssm_step(int64_t batch, int64_t dim, int64_t nstate, int64_t rank
  * nlayers: each layer has its own hand-off buffers), 256-byte aligned,
  * zero-filled before its first use and then left to the launches (it holds a
  * launch counter); one workspace per stream of launches.  Every wait is
- * bounded: should one ever time out, the launch and every later launch on
- * the workspace do nothing further until ssm_decode_layers_status reports it
- * (SSM_ERR_HIP) and zero-fills the workspace.
+ * bounded: should one ever time out, the workgroup that gave up sets the
+ * error word (the 32-bit word at byte offset 512 of the workspace, nonzero
+ * once set), the launch and every later launch on the workspace do nothing
+ * further (their outputs are not written) until ssm_decode_layers_status
+ * reports it (SSM_ERR_HIP) and zero-fills the workspace.  The launches
+ * advance the layers' SSM states and conv windows in place, so those caches
+ * may then have been advanced partly (some layers, some channels): they are
+ * invalid as well, and the caller re-runs the prefill.
  */
 enum {
   SSM_LAYER_IN_PROJ_W = 0, SSM_LAYER_IN_PROJ_B, SSM_LAYER_NORM_W, SSM_LAYER_CONV_W,
@@ -348,7 +365,8 @@ int ssm_decode_layers(int64_t batch, int64_t nlayers, int64_t model_dim, int64_t
                       void* out, float norm_eps, void* workspace, int64_t workspace_bytes,
                       void* stream);
 /* Synchronises the stream; SSM_OK, or SSM_ERR_HIP after a wait timed out
- * (the workspace is zero-filled then). */
+ * (the workspace is zero-filled then, and the outputs and the layers' caches
+ * since the previous check are invalid). */
 int ssm_decode_layers_status(void* workspace, int64_t workspace_bytes, void* stream);
 
 /*

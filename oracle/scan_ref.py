@@ -22,12 +22,15 @@ float32 for the timed CPU baseline), what the reference computes:
 
 Padding (``length``): a padded position is an identity step of the recurrence
 (a = 1, b = 0; ``forward_kernel.cu:196-205``), ``out`` is still produced at
-every position, and the backward treats the loss as not depending on padded
-outputs (upstream gradient masked to zero there), which is the reference's
-behaviour for right padding on its scalar-load path
+every position, and the scan's backward treats the loss as not depending on
+padded outputs (upstream gradient masked to zero there), which is the
+reference's behaviour for right padding on its scalar-load path
 (``backward_kernel.cu:225-246,299-303,374,389``).  Left padding uses the same
 rule mirrored (the reference's left-padding backward is inconsistent, see the
-design notes).
+design notes).  The z gate is the reference's elementwise product outside the
+scan (``modules/mamba.py:181-182``), which autograd differentiates at every
+position: dz = dy * out * silu'(z) with the unmasked dy, padded positions
+included, while the scan itself receives the masked dy * silu(z).
 
 The chunk-state carrier ``h_chunks`` holds the state at the end of every
 ``chunk``-step chunk, shape (B, D, nchunks, N); the reference stores the pair
@@ -205,6 +208,7 @@ def scan_bwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
         dsp = dsp.abs()
     dtf = dt.abs() if magnitude else dt  # the step size as a factor (decays keep dt)
     dtu = dtf * u
+    dy_gate = dy  # the gate sees every position: dz = dy * out * silu'(z)
     dy = torch.where(mask, dy, torch.zeros_like(dy))
     dout = dy * gate if z is not None else dy
 
@@ -260,7 +264,7 @@ def scan_bwd(u, delta, A, B, C, D=None, delta_bias=None, h_init=None,
     }
     if z is not None:
         out_pre = out_pre + D[None, :, None] * u
-        res["dz"] = dy * out_pre * gate_grad
+        res["dz"] = dy_gate * out_pre * gate_grad
     return res
 
 

@@ -23,6 +23,8 @@ _sz = ctypes.c_size_t
 SSM_F32 = 0
 SSM_BF16 = 1
 SSM_CHUNK = 16
+SSM_REF_CHUNK = 128  # the reference's chunk (kernel_config.h:4-10): the pair layout's chunks
+SSM_REF_SLOTS = SSM_REF_CHUNK // SSM_CHUNK
 SSM_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 # exported symbol -> (restype, argtypes)
@@ -32,6 +34,7 @@ SIGNATURES = {
     "ssm_profile_begin": (_i32, []),
     "ssm_profile_end": (_i32, [ctypes.c_char_p, _sz]),
     "ssm_scan_nchunks": (_i64, [_i64]),
+    "ssm_scan_ref_nchunks": (_i64, [_i64]),
     "ssm_scan_fwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "ssm_scan_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "ssm_selective_scan_fwd": (_i32, [
@@ -116,7 +119,7 @@ SIGNATURES = {
     ]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 def lib() -> ctypes.CDLL:

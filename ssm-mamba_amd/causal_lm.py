@@ -432,6 +432,28 @@ class CausalLM(nn.Module):
         x = self.norm(x, dim=1).transpose(1, 2).contiguous()
         return self.lm_head(x)
 
+    def forward_last(self, input_ids: torch.Tensor, lengths: Optional[torch.Tensor] = None,
+                     use_cache: bool = False) -> torch.Tensor:
+        """Logits at position lengths - 1 of each row, (batch, vocab): the rows
+        of ``forward``'s logits that the reference's ``generate`` keeps
+        (``models/causal_lm.py:104-113``, the same index, negative wrapping
+        included).  The final norm and the LM head run on those rows only."""
+        batch, seqlen = input_ids.shape
+        x = self.embedding(input_ids).transpose(1, 2).contiguous()
+        for layer in self.layers:
+            x, _ = layer.forward_cm(x, lengths=lengths, use_cache=use_cache, inplace=True)
+        last = (torch.full((batch,), seqlen, dtype=torch.long, device=input_ids.device)
+                if lengths is None else lengths) - 1
+        x = x[torch.arange(batch, device=x.device), :, last]  # (batch, model_dim)
+        return self._head(x)
+
+    def _head(self, x: torch.Tensor) -> torch.Tensor:
+        """Final norm and LM head of (batch, model_dim) rows."""
+        if _dec.gemv_supported(self.lm_head.weight, x, self.norm.weight):
+            return _dec.gemv(self.lm_head.weight, x, norm_weight=self.norm.weight,
+                             eps=self.norm.eps)
+        return self.lm_head(self.norm(x))
+
     def step(self, input_ids: torch.Tensor) -> torch.Tensor:
         """input_ids (batch,) -> logits (batch, vocab), advancing every cache."""
         x = self.embedding(input_ids)
@@ -443,10 +465,7 @@ class CausalLM(nn.Module):
         else:
             for layer in self.layers:
                 x = layer.step(x)
-        if _dec.gemv_supported(self.lm_head.weight, x, self.norm.weight):
-            return _dec.gemv(self.lm_head.weight, x, norm_weight=self.norm.weight,
-                             eps=self.norm.eps)
-        return self.lm_head(self.norm(x))
+        return self._head(x)
 
     def decoder(self, batch: int, max_new_tokens: int, temperature: float = 1.0) -> "GreedyDecoder":
         key = (batch, max_new_tokens, float(temperature))
@@ -480,8 +499,7 @@ class CausalLM(nn.Module):
         batch = input_ids.shape[0]
         dev = input_ids.device
         lengths = (input_ids != self.config.pad_token_id).sum(dim=1)
-        logits = self.forward(input_ids, lengths, use_cache=True)
-        logits = logits[torch.arange(batch, device=dev), lengths - 1]
+        logits = self.forward_last(input_ids, lengths, use_cache=True)
         finished = torch.zeros(batch, dtype=torch.bool, device=dev)
         out = []
         for _ in range(max_new_tokens):
@@ -560,18 +578,18 @@ class GreedyDecoder:
 
     def prefill(self, input_ids: torch.Tensor, lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Run the prompt, fill the caches and pick the first new token (stored
-        as generated token 0).  Returns the prompt logits."""
+        as generated token 0).  Returns the logits at position lengths - 1,
+        (batch, vocab): the LM head runs on those rows only."""
         self._install()
         with torch.no_grad():
             if lengths is None:
                 lengths = (input_ids != self.model.config.pad_token_id).sum(dim=1)
-            logits = self.model.forward(input_ids, lengths, use_cache=True)
-            last = logits[torch.arange(self.batch, device=self.device), lengths - 1]
+            last = self.model.forward_last(input_ids, lengths, use_cache=True)
             first = _greedy_pick(last, self.temperature)
             self.token.copy_(first)
             self.tokens[:, 0] = first
             self.pos.fill_(1)
-        return logits
+        return last
 
     def replay(self, steps: int) -> None:
         """Advance ``steps`` tokens (one model step each)."""

@@ -17,6 +17,7 @@ namespace ssm {
 hipError_t launch_scan_fwd(const ScanParams& p, int dtype, bool aligned, float* bc, hipStream_t st);
 hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* bc, hipStream_t st);
 hipError_t launch_chunk_decay(const ScanParams& p, int dtype, float* pairs, hipStream_t st);
+hipError_t launch_chunk_tail(const ScanParams& p, float* pairs, hipStream_t st);
 hipError_t launch_state_update(const UpdateParams& p, int dtype, bool vecN, hipStream_t st);
 size_t bc_prep_floats(int batch, int nstate, int seqlen);
 size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen);
@@ -247,7 +248,7 @@ extern "C" {
 
 const char* ssm_last_error(void) { return g_err.c_str(); }
 
-int ssm_abi_version(void) { return 7; }
+int ssm_abi_version(void) { return 8; }
 
 int ssm_profile_begin(void) {
   g_err.clear();
@@ -298,6 +299,9 @@ int ssm_profile_end(char* buf, size_t buf_bytes) {
 }
 
 int64_t ssm_scan_nchunks(int64_t seqlen) { return seqlen <= 0 ? 0 : (seqlen + SSM_CHUNK - 1) / SSM_CHUNK; }
+int64_t ssm_scan_ref_nchunks(int64_t seqlen) {
+  return seqlen <= 0 ? 0 : (seqlen + SSM_REF_CHUNK - 1) / SSM_REF_CHUNK;
+}
 
 size_t ssm_scan_fwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate) {
   if (batch < 1 || dim < 1 || seqlen < 1 || nstate < 1) return 0;
@@ -348,10 +352,12 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                                        h_init, length, padding_right, z, delta_softplus);
   p.out = out;
   p.out_ungated = out_ungated;
-  // pair layout: the states go to the odd slots (one row of dim in), the
-  // chunk decays to the even slots
+  // pair layout: the states go to the odd rows (one row of dim in), the
+  // chunk decays to the even rows of each 128-step chunk's carry slot; a
+  // batch row holds SSM_REF_SLOTS slots per 128-step chunk
   p.h_chunks = (h_chunks && h_pairs) ? h_chunks + dim : h_chunks;
   p.hs = h_pairs ? 2 : 1;
+  if (h_pairs) p.nchunks = (int)(SSM_REF_SLOTS * ssm_scan_ref_nchunks(seqlen));
   p.h_last = h_last;
   // workspace: [prepped B/C][segment states and step sums][dummy]
   char* ws = static_cast<char*>(workspace) +
@@ -363,15 +369,18 @@ int ssm_selective_scan_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));
   p.dummy = ws;
   const bool aligned = scan_aligned(dtype, seqlen, {u, delta, z, out, out_ungated});
+  const hipStream_t st = static_cast<hipStream_t>(stream);
   if (h_pairs) {
-    if (int e = hip_status(ssm::launch_chunk_decay(p, dtype, h_chunks,
-                                                   static_cast<hipStream_t>(stream)),
+    if (int e = hip_status(ssm::launch_chunk_decay(p, dtype, h_chunks, st),
                            "selective_scan chunk decay launch"))
       return e;
   }
-  return hip_status(ssm::launch_scan_fwd(p, dtype, aligned, static_cast<float*>(workspace),
-                                         static_cast<hipStream_t>(stream)),
-                    "selective_scan forward launch");
+  if (int e = hip_status(ssm::launch_scan_fwd(p, dtype, aligned, static_cast<float*>(workspace), st),
+                         "selective_scan forward launch"))
+    return e;
+  if (h_pairs)
+    return hip_status(ssm::launch_chunk_tail(p, h_chunks, st), "selective_scan chunk tail launch");
+  return SSM_OK;
 }
 
 int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int dtype,
@@ -405,6 +414,7 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
                                        h_init, length, padding_right, z, delta_softplus);
   p.h_chunks_in = h_pairs ? h_chunks + dim : h_chunks;
   p.hs = h_pairs ? 2 : 1;
+  if (h_pairs) p.nchunks = (int)(SSM_REF_SLOTS * ssm_scan_ref_nchunks(seqlen));
   p.dout = dout;
   p.dh_last = dh_last;
   p.du = du;
@@ -707,7 +717,8 @@ int ssm_decode_layers_status(void* workspace, int64_t workspace_bytes, void* str
   return fail(SSM_ERR_HIP,
               "decode_layers: a wait for another workgroup's data timed out (not every workgroup "
               "was resident); the outputs of the launches since the last status check are "
-              "invalid, and the workspace is cleared");
+              "invalid, and so are the layers' SSM states and conv windows, which those launches "
+              "may have advanced in part (re-run the prefill); the workspace is cleared");
 }
 
 int ssm_rms_norm_cm(int64_t batch, int64_t channels, int64_t seqlen, int dtype, const void* x,

@@ -1377,11 +1377,16 @@ __global__ __launch_bounds__(kPickThreads) void pick_kernel(const T* __restrict_
       if (pick_beats(s_v[w], s_i[w], v, i)) { v = s_v[w]; i = s_i[w]; }
     const u32x2_v pr = {__float_as_uint(v), (uint32_t)i};
     __builtin_amdgcn_raw_buffer_store_b64(pr, r, (int)((64 + 2 * blockIdx.x) * 4), 0, kSC1);
-    __builtin_amdgcn_s_waitcnt(0);  // the slice is stored before it is counted
-    s_last = dev_add_u32(ws, 1u) == gridDim.x - 1;
+    // release: the slice is visible at device scope before it is counted;
+    // acquire: the last workgroup sees every other workgroup's slice
+    s_last = __hip_atomic_fetch_add(ws, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+             gridDim.x - 1;
   }
   __syncthreads();
   if (!s_last) return;
+  // every thread of the last workgroup reads slices: order its loads after
+  // the counter as well (the barrier orders them only within the workgroup)
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   // the last workgroup: wave w combines rows w, w + 4, ... (no barrier inside)
   const int64_t ps = pos ? *pos : 0;
   const int64_t col = ps < cols - 1 ? ps : cols - 1;
@@ -1651,6 +1656,7 @@ const char* decode_layers_unsupported(int K, int dim, int nout, int bf16) {
 }
 
 int64_t decode_layers_error_offset() { return (int64_t)kSyncErr * sizeof(unsigned); }
+static_assert(kSyncErr * sizeof(unsigned) == 512, "the error word's offset is part of the ABI");
 
 int64_t decode_pick_workspace(int B) { return (int64_t)(64 + 2 * B * kPickParts) * 4; }
 

@@ -12,10 +12,14 @@
 // keep the reference's names, argument order, validation messages and
 // padding rule ("right" unless given, selective_scan.cpp:248).  `h` is the
 // reference's chunk carry: (batch, dim, nchunks, 2 * state_dim) holding
-// (prod a, state) pairs, so h[..., -1, 1::2] is the final state
-// (ops/selective_scan_interface.py:60).  Here a chunk is 16 steps and h is a
-// strided view of a channel-contiguous (batch, nchunks, 2 * state_dim, dim)
-// buffer, the layout the kernels save and reload with coalesced accesses.
+// (prod a, state) pairs per 128-step chunk (nchunks = ceil(seq_len / 128),
+// kernel_config.h:4-10, selective_scan.cpp:270-274), so h[..., -1, 1::2] is
+// the final state (ops/selective_scan_interface.py:60).  h is a strided view
+// of a channel-contiguous (batch, 8 * nchunks, 2 * state_dim, dim) buffer
+// that also holds the state after every 16 steps, which the backward reloads
+// (coalesced) instead of recomputing the chunks' states; given any other
+// tensor of h's shape (a copy), the backward recomputes those states with the
+// forward kernel first.
 //
 // Extensions used by this package's operator layer:
 //   fwd_ext(..., z, delta_softplus, save, out_ungated) with save = 0 (final
@@ -114,6 +118,24 @@ bool has_strides(const at::Tensor& t, at::IntArrayRef sizes, at::IntArrayRef str
   return true;
 }
 
+// The reference-shaped view (batch, dim, nchunks, 2 * state_dim) of the pair
+// buffer (batch, SSM_REF_SLOTS * nchunks, 2 * state_dim, dim): chunk c is slot
+// SSM_REF_SLOTS * c + SSM_REF_SLOTS - 1.
+std::vector<int64_t> pair_view_strides(const Shape& s) {
+  const int64_t K = ssm_scan_ref_nchunks(s.seqlen), N2 = 2 * s.nstate;
+  return {SSM_REF_SLOTS * K * N2 * s.dim, 1, SSM_REF_SLOTS * N2 * s.dim, s.dim};
+}
+int64_t pair_view_offset(const Shape& s) { return (SSM_REF_SLOTS - 1) * 2 * s.nstate * s.dim; }
+
+// Whether h is exactly the view forward returns: its shape, strides and
+// offset into a storage of exactly the pair buffer's size.
+bool is_pair_view(const at::Tensor& h, const Shape& s) {
+  const int64_t K = ssm_scan_ref_nchunks(s.seqlen), N2 = 2 * s.nstate;
+  const auto st = pair_view_strides(s);
+  return has_strides(h, {s.batch, s.dim, K, N2}, st) && h.storage_offset() == pair_view_offset(s) &&
+         h.storage().nbytes() == (size_t)(s.batch * SSM_REF_SLOTS * K * N2 * s.dim) * sizeof(float);
+}
+
 std::vector<at::Tensor> fwd_impl(const at::Tensor& u, const at::Tensor& A, const at::Tensor& B,
                                  const at::Tensor& C, const OptT& D_, const at::Tensor& delta,
                                  const OptT& bias_, const OptT& h_init_, const OptT& length_,
@@ -141,9 +163,12 @@ std::vector<at::Tensor> fwd_impl(const at::Tensor& u, const at::Tensor& A, const
     h = at::empty({s.batch, s.nchunks, s.nstate, s.dim}, f32);
     h_chunks = h.data_ptr<float>();
   } else {
-    store = at::empty({s.batch, s.nchunks, 2 * s.nstate, s.dim}, f32);
+    // the pair layout: SSM_REF_SLOTS slots of 16 steps per 128-step chunk,
+    // the chunk's (prod a, state) carry in its last slot
+    const int64_t K = ssm_scan_ref_nchunks(s.seqlen), N2 = 2 * s.nstate;
+    store = at::empty({s.batch, SSM_REF_SLOTS * K, N2, s.dim}, f32);
     h_chunks = store.data_ptr<float>();
-    h = store.permute({0, 3, 1, 2});  // (batch, dim, nchunks, 2 * state_dim)
+    h = store.as_strided({s.batch, s.dim, K, N2}, pair_view_strides(s), pair_view_offset(s));
   }
   const size_t wsb = ssm_scan_fwd_workspace_bytes(s.batch, s.dim, s.seqlen, s.nstate);
   at::Tensor ws = at::empty({(int64_t)wsb}, u.options().dtype(at::kByte));
@@ -178,26 +203,44 @@ std::vector<at::Tensor> bwd_impl(const at::Tensor& u, const at::Tensor& A, const
   if (dh_last)
     check(*dh_last, "dh_last", {s.batch, s.dim, s.nstate}, "batch_size, num_channels, state_dim",
           false, s.io_t);
-  // the chunk carry: the pair view forward returns, the state layout of
-  // fwd_ext(save=1), or a contiguous copy of the pair view
+  // the chunk carry: the pair view forward returns (its buffer holds the
+  // 16-step states), the state layout of fwd_ext(save=1), or another tensor
+  // of the pair view's shape (a copy: the states are recomputed)
   TORCH_CHECK(h_.is_cuda(), "h must be a CUDA tensor");
   TORCH_CHECK(h_.scalar_type() == at::kFloat, "h must be float32 tensor");
-  const int64_t K = s.nchunks, N2 = 2 * s.nstate, Dm = s.dim;
-  at::Tensor h = h_;
-  int pairs;
-  if (has_strides(h, {s.batch, Dm, K, N2}, {K * N2 * Dm, 1, N2 * Dm, Dm})) {
-    pairs = 1;
-  } else if (h.sizes() == at::IntArrayRef({s.batch, Dm, K, N2})) {
-    h = h.permute({0, 2, 3, 1}).contiguous().permute({0, 3, 1, 2});
-    pairs = 1;
-  } else {
-    TORCH_CHECK(h.sizes() == at::IntArrayRef({s.batch, K, s.nstate, Dm}) && h.is_contiguous(),
-                "h must have shape (batch_size, num_channels, num_chunks, 2*state_dim) "
-                "(num_chunks = ceil(seq_len / 16)), as returned by forward");
-    pairs = 0;
-  }
+  const int64_t K = ssm_scan_ref_nchunks(s.seqlen), N2 = 2 * s.nstate, Dm = s.dim;
   const bool pr = padding_right_of(padding_side);
   c10::hip::HIPGuard guard(u.get_device());
+  const float* hp = nullptr;
+  at::Tensor states;  // recomputed 16-step states
+  int pairs;
+  if (is_pair_view(h_, s)) {
+    hp = h_.data_ptr<float>() - pair_view_offset(s);  // the start of the pair buffer
+    pairs = 1;
+  } else if (h_.sizes() == at::IntArrayRef({s.batch, Dm, K, N2})) {
+    // the carry alone does not hold the 16-step states the backward reloads:
+    // the forward kernel recomputes them (the same kernel and inputs, so the
+    // same states as the forward that produced h)
+    states = at::empty({s.batch, s.nchunks, s.nstate, Dm}, u.options().dtype(at::kFloat));
+    at::Tensor scratch_out = at::empty_like(u);
+    const size_t fwsb = ssm_scan_fwd_workspace_bytes(s.batch, s.dim, s.seqlen, s.nstate);
+    at::Tensor fws = at::empty({(int64_t)fwsb}, u.options().dtype(at::kByte));
+    ok(ssm_selective_scan_fwd(
+        s.batch, s.dim, s.seqlen, s.nstate, s.io, u.data_ptr(), delta.data_ptr(),
+        A.data_ptr<float>(), B.data_ptr(), C.data_ptr(), s.bc_stride, ptr<float>(D),
+        ptr<float>(bias), ptr<float>(h_init), ptr<int64_t>(length), pr ? 1 : 0, ptr(z),
+        delta_softplus ? 1 : 0, scratch_out.data_ptr(), nullptr, states.data_ptr<float>(), 0,
+        nullptr, fws.data_ptr(), fwsb, stream_of(u)));
+    hp = states.data_ptr<float>();
+    pairs = 0;
+  } else {
+    TORCH_CHECK(h_.sizes() == at::IntArrayRef({s.batch, s.nchunks, s.nstate, Dm}) &&
+                    h_.is_contiguous(),
+                "h must have shape (batch_size, num_channels, num_chunks, 2*state_dim) "
+                "(num_chunks = ceil(seq_len / 128)), as returned by forward");
+    hp = h_.data_ptr<float>();
+    pairs = 0;
+  }
   at::Tensor du = at::empty_like(u);
   at::Tensor ddelta = at::empty_like(delta);
   at::Tensor dA = at::empty_like(A);
@@ -214,7 +257,7 @@ std::vector<at::Tensor> bwd_impl(const at::Tensor& u, const at::Tensor& A, const
       s.batch, s.dim, s.seqlen, s.nstate, s.io, u.data_ptr(), delta.data_ptr(),
       A.data_ptr<float>(), B.data_ptr(), C.data_ptr(), s.bc_stride, ptr<float>(D),
       ptr<float>(bias), ptr<float>(h_init), ptr<int64_t>(length), pr ? 1 : 0, ptr(z), ptr(yu),
-      delta_softplus ? 1 : 0, h.data_ptr<float>(), pairs, dout.data_ptr(), ptr<float>(dh_last),
+      delta_softplus ? 1 : 0, hp, pairs, dout.data_ptr(), ptr<float>(dh_last),
       du.data_ptr(), ddelta.data_ptr(), dA.data_ptr<float>(), dB.data_ptr(), dC.data_ptr(),
       static_cast<float*>(dptr(dD)), static_cast<float*>(dptr(dbias)),
       static_cast<float*>(dptr(dh_init)), dptr(dz), ws.data_ptr(), wsb, stream_of(u)));

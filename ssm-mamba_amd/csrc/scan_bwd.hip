@@ -12,7 +12,10 @@
 // dout is the upstream gradient masked to zero at padded positions (the loss
 // does not see them), times silu(z) when the z gate is fused; then
 // dz = dy * y * silu'(z) with y the forward's ungated output (saved by the
-// forward, so the backward does not recompute sum_n C h).
+// forward, so the backward does not recompute sum_n C h) and dy unmasked: the
+// gate is the caller's elementwise product outside the scan
+// (modules/mamba.py:181-182), which autograd differentiates at every
+// position, padded ones included.
 //
 // Work decomposition mirrors the forward (workgroup = batch row b x 64
 // channels, 8 waves, lane = channel, wave w = state pairs G = g*8 + w).  Tiles
@@ -345,7 +348,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
         if constexpr (kHasZ) {
           const float sz = sigmoidf_fast(v2[j]);
           dov[j] = dym * (v2[j] * sz);
-          dzo[j] = dym * v3[j] * (sz * fmaf(v2[j], 1.0f - sz, 1.0f));
+          dzo[j] = v1[j] * v3[j] * (sz * fmaf(v2[j], 1.0f - sz, 1.0f));  // every position
         } else {
           dov[j] = dym;
           dzo[j] = 0.0f;
@@ -851,7 +854,7 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
         decode4(r.y, yv);
         const float sz = sigmoidf_fast(zv[j]);
         dov[j] = dym * (zv[j] * sz);
-        dzo[j] = dym * yv[j] * (sz * fmaf(zv[j], 1.0f - sz, 1.0f));
+        dzo[j] = dyv[j] * yv[j] * (sz * fmaf(zv[j], 1.0f - sz, 1.0f));  // every position
       } else {
         dov[j] = dym;
         dzo[j] = 0.0f;

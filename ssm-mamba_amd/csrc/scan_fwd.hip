@@ -1090,23 +1090,35 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_segsum_kernel(
 // ---------------------------------------------------------------- chunk decays
 
 // The first half of the reference's (prod a, h) chunk carry
-// (csrc/selective_scan/forward_kernel.cu:225-228): the product of the decays
-// a_t = exp(delta_t A) from step 0 to the end of each chunk, which is
-// exp(A * S_c) with S_c the sum of the step sizes over those steps (padded
-// steps count zero, as their decay is 1).  Written into the even slots of the
-// pair layout pairs (batch, nchunks, 2 * nstate, dim) fp32 by two kernels that
-// run before the scan, whose states then fill the odd slots.
+// (csrc/selective_scan/forward_kernel.cu:225-228), whose chunks are
+// kRefChunk = 128 steps (kernel_config.h:4-10): the product of the decays
+// a_t = exp(delta_t A) from step 0 to the end of each 128-step chunk c, which
+// is exp(A * S_c) with S_c the sum of the step sizes over those steps (padded
+// steps count zero, as their decay is 1).  The pair layout pairs
+// (batch, nchunks, 2 * nstate, dim) fp32 has nchunks = kRefSlots * (number of
+// 128-step chunks) slots of 16 steps: the scan writes the states into the odd
+// rows of slots 0 .. ceil(seqlen / 16) - 1, and chunk c's carry is slot
+// kRefSlots * c + kRefSlots - 1, the last 16-step slot of the chunk.  The
+// decays go into that slot's even rows, by two kernels that run before the
+// scan; when seqlen is not a multiple of 128 the last chunk's carry slot lies
+// past the last state the scan writes, and chunk_tail_kernel copies the final
+// state there after the scan.
+constexpr int kRefChunk = 128;
+constexpr int kRefSlots = kRefChunk / kChunk;
 
-// Step-size sum of each chunk, per (b, d, chunk c), parked in the odd slot of
-// state 0 (the scan overwrites it); consecutive threads take consecutive
-// chunks of a row, so the row is read contiguously.
+__device__ __forceinline__ size_t ref_slot(int c) { return (size_t)c * kRefSlots + kRefSlots - 1; }
+
+// Step-size sum of each 128-step chunk, per (b, d, chunk c), parked in the
+// odd row of state 0 of the chunk's carry slot (the scan, or the tail copy,
+// overwrites it); consecutive threads take consecutive chunks of a row.
 template <typename T>
 __global__ __launch_bounds__(256) void chunk_dt_sum_kernel(const ScanDims p,
                                                            const T* __restrict__ dl,
                                                            const float* __restrict__ biasp,
                                                            const int64_t* __restrict__ length,
                                                            float* __restrict__ pairs) {
-  const int L = p.seqlen, Dm = p.dim, K = p.nchunks, N2 = 2 * p.nstate;
+  const int L = p.seqlen, Dm = p.dim, N2 = 2 * p.nstate;
+  const int slots = p.nchunks, K = slots / kRefSlots;
   const size_t total = (size_t)p.batch * Dm * K;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
@@ -1117,25 +1129,26 @@ __global__ __launch_bounds__(256) void chunk_dt_sum_kernel(const ScanDims p,
     valid_window(length, p.pad_right, b, L, vlo, vhi);
     const float bias = biasp ? biasp[d] : 0.0f;
     const T* row = dl + bd * L;
-    const int t1 = min(L, (c + 1) * kChunk);
+    const int t1 = min(L, (c + 1) * kRefChunk);
     float acc = 0.0f;
-    for (int t = c * kChunk; t < t1; ++t) {
+    for (int t = c * kRefChunk; t < t1; ++t) {
       const float x = Elem<T>::load1(row + t) + bias;
       const float dt = p.softplus ? softplus_t20(x) : x;
       acc += (t >= vlo && t < vhi) ? dt : 0.0f;
     }
-    pairs[(((size_t)b * K + c) * N2 + 1) * Dm + d] = acc;
+    pairs[(((size_t)b * slots + ref_slot(c)) * N2 + 1) * Dm + d] = acc;
   }
 }
 
-// prod a per (b, d, state n) at every chunk end: a running sum of the chunk
-// step sums, and exp2(A log2(e) S) into the even slot of each state.  One
-// thread per (b, d, group of 4 states); consecutive threads take consecutive
-// channels, so the slot writes are contiguous.
+// prod a per (b, d, state n) at every 128-step chunk end: a running sum of
+// the chunk step sums, and exp2(A log2(e) S) into the even rows of the
+// chunk's carry slot.  One thread per (b, d, group of 4 states);
+// consecutive threads take consecutive channels, so the writes are
+// contiguous.
 __global__ __launch_bounds__(256) void chunk_decay_kernel(const ScanDims p,
                                                           const float* __restrict__ Ap,
                                                           float* __restrict__ pairs) {
-  const int Dm = p.dim, K = p.nchunks, N = p.nstate, N2 = 2 * N;
+  const int Dm = p.dim, slots = p.nchunks, K = slots / kRefSlots, N = p.nstate, N2 = 2 * N;
   const int ng = (N + 3) / 4;
   const size_t total = (size_t)p.batch * ng * Dm;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
@@ -1151,8 +1164,8 @@ __global__ __launch_bounds__(256) void chunk_decay_kernel(const ScanDims p,
     }
     float S = 0.0f;
     for (int c = 0; c < K; ++c) {
-      float* slot = pairs + ((size_t)b * K + c) * N2 * Dm + d;
-      S += slot[Dm];  // the chunk's step sum (odd slot of state 0)
+      float* slot = pairs + ((size_t)b * slots + ref_slot(c)) * N2 * Dm + d;
+      S += slot[Dm];  // the chunk's step sum (odd row of state 0)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n = 4 * q + j;
@@ -1162,8 +1175,26 @@ __global__ __launch_bounds__(256) void chunk_decay_kernel(const ScanDims p,
   }
 }
 
+// After the scan, when the last 128-step chunk is partial: its carry slot
+// receives the final state (odd rows of the last slot the scan wrote).  One
+// thread per (b, n, d).
+__global__ __launch_bounds__(256) void chunk_tail_kernel(const ScanDims p, float* __restrict__ pairs) {
+  const int Dm = p.dim, N = p.nstate, N2 = 2 * N, slots = p.nchunks;
+  const int last = (p.seqlen + kChunk - 1) / kChunk - 1;
+  const size_t total = (size_t)p.batch * N * Dm;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int d = (int)(i % Dm);
+    const size_t r = i / Dm;
+    const int n = (int)(r % N), b = (int)(r / N);
+    const size_t row = (size_t)(2 * n + 1) * Dm + d;
+    pairs[((size_t)b * slots + slots - 1) * N2 * Dm + row] =
+        pairs[((size_t)b * slots + last) * N2 * Dm + row];
+  }
+}
+
 hipError_t launch_chunk_decay(const ScanParams& p, int dtype, float* pairs, hipStream_t st) {
-  const size_t n1 = (size_t)p.batch * p.dim * p.nchunks;
+  const size_t n1 = (size_t)p.batch * p.dim * (p.nchunks / kRefSlots);
   {
     ProfScope prof("chunk_dt_sum", st);
     const int blocks = (int)std::min<size_t>((n1 + 255) / 256, 65535);
@@ -1180,6 +1211,15 @@ hipError_t launch_chunk_decay(const ScanParams& p, int dtype, float* pairs, hipS
   const size_t n2 = (size_t)p.batch * ((p.nstate + 3) / 4) * p.dim;
   const int blocks = (int)std::min<size_t>((n2 + 255) / 256, 65535);
   hipLaunchKernelGGL(chunk_decay_kernel, dim3(blocks), dim3(256), 0, st, dims_of(p), p.A, pairs);
+  return hipGetLastError();
+}
+
+hipError_t launch_chunk_tail(const ScanParams& p, float* pairs, hipStream_t st) {
+  if ((p.seqlen + kChunk - 1) / kChunk == p.nchunks) return hipSuccess;  // 128 | seqlen
+  ProfScope prof("chunk_tail", st);
+  const size_t n = (size_t)p.batch * p.nstate * p.dim;
+  const int blocks = (int)std::min<size_t>((n + 255) / 256, 65535);
+  hipLaunchKernelGGL(chunk_tail_kernel, dim3(blocks), dim3(256), 0, st, dims_of(p), pairs);
   return hipGetLastError();
 }
 

@@ -7,6 +7,9 @@
 //   h_init, h_last, dh_last, dh_init       : (batch, dim, nstate)   fp32
 //   h_chunks                               : (batch, nchunks, nstate, dim) fp32,
 //                                            state after each kChunk steps
+//                                            (nchunks: the slots of a batch row,
+//                                            ceil(seqlen / kChunk), or 8 per
+//                                            128-step chunk in the pair layout)
 //   length                                 : (batch,) int64
 #pragma once
 

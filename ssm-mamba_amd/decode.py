@@ -232,9 +232,12 @@ def layers_supported(layers, x: torch.Tensor) -> bool:
 class LayerChain:
     """The device-side layer table and the workspace of ``ssm_decode_layers``
     for one stack of Blocks and one (device, batch, dtype).  The table holds
-    the layers' parameter and cache addresses; it is rebuilt when any of them
-    changes (a HIP graph that captured a launch keeps the old table alive and
-    must be re-captured then, as for any other buffer it bakes in)."""
+    the layers' parameter and cache addresses.  When any of them changes the
+    chain switches to the table for the new addresses, built once and kept
+    in ``tables`` for the chain's lifetime: a HIP graph that captured a
+    launch bakes in the address of the table it used, so no table is ever
+    freed while the chain lives (a graph replayed after the addresses changed
+    still reads the layer pointers it was captured with)."""
 
     def __init__(self, layers, x: torch.Tensor):
         s0 = layers[0].ssm
@@ -252,11 +255,15 @@ class LayerChain:
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=x.device)
         self.ptrs = None
         self.table = None
+        self.tables = {}  # pointer tuple -> device table; never pruned
 
     def update(self, layers) -> None:
-        ptrs = [0 if t is None else t.data_ptr() for blk in layers for t in _layer_tensors(blk)]
+        ptrs = tuple(0 if t is None else t.data_ptr() for blk in layers for t in _layer_tensors(blk))
         if ptrs != self.ptrs:
-            self.table = torch.tensor(ptrs, dtype=torch.int64).to(self.device)
+            table = self.tables.get(ptrs)
+            if table is None:
+                table = self.tables[ptrs] = torch.tensor(ptrs, dtype=torch.int64).to(self.device)
+            self.table = table
             self.ptrs = ptrs
 
     def step(self, layers, x: torch.Tensor) -> torch.Tensor:

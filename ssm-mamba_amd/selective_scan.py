@@ -16,8 +16,9 @@ and the model harness use (``fwd_ext`` / ``bwd_ext``):
 * The chunk-state carrier ``h`` holds the state after every 16 steps, shape
   (batch, ceil(seqlen/16), state_dim, dim), float32, channel-contiguous, so the
   kernels' saves and reloads are coalesced; ``h[:, -1].transpose(1, 2)`` is
-  the final state.  (The reference-API ``forward`` returns the pair view
-  (batch, dim, nchunks, 2*state_dim) with the chunk decays as well.)
+  the final state.  (The reference-API ``forward`` returns the reference's
+  (prod a, h) carry per 128-step chunk, (batch, dim, ceil(seqlen/128),
+  2*state_dim), a view of a buffer that also holds these 16-step states.)
 * Keyword extensions: ``z`` (fused output gate out * silu(z)),
   ``delta_softplus`` and, for ``forward``, ``save_chunks=False`` (inference:
   only the final state is produced).

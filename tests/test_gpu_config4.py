@@ -118,8 +118,7 @@ def test_config4_graph_steps_equal_eager_steps(cuda):
         g_state = _snapshot(m)
         g_logits = m.step(dec.token)           # one more step on the graph's caches
         # eager: the same prefill, then `steps` steps launched one by one
-        logits = m(ids, lengths, use_cache=True)
-        tok = _greedy_pick(logits[torch.arange(batch, device=cuda), lengths - 1], 1.0)
+        tok = _greedy_pick(m.forward_last(ids, lengths, use_cache=True), 1.0)
         e_tokens = [tok]
         for _ in range(steps):
             tok = _greedy_pick(m.step(tok), 1.0)

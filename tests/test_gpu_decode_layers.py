@@ -160,6 +160,47 @@ def test_chain_graph_replays_match_eager(cuda):
         DEC.layers_check(m)
 
 
+def test_chain_failure_path(cuda):
+    """The error word set from the host before a launch, as a timed-out wait
+    leaves it (a flag the host sets: no wait is made to time out): every
+    workgroup returns at its first check, so the launch changes no cache;
+    layers_check raises and zero-fills the workspace; the next step then
+    equals a fresh chain's step from the same caches, bit for bit."""
+    from ssm_mamba_amd import decode as DEC
+    m, cfg = make_lm(seed=62, vocab=89, model_dim=256, state_dim=16, layers=3)
+    m = m.to(cuda, torch.bfloat16)
+    ids = _ids(2, 7, cfg.vocab_size, seed=63)
+    snap = lambda: [(l.ssm._conv_context.clone(), l.ssm._ssm_hiddens.clone()) for l in m.layers]
+    with torch.no_grad():
+        m(ids.to(cuda), (ids != 0).sum(dim=1).to(cuda), use_cache=True)
+        x = m.embedding(torch.tensor([5, 17], device=cuda))
+        DEC.layers_step(m, m.layers, x)  # a normal launch first (generation 1)
+        DEC.layers_check(m)
+        (chain,) = m.__dict__["_layer_chains"].values()
+        caches0 = snap()
+        err = chain.workspace[512:516]  # the error word (include/ssm_mamba.h)
+        err.copy_(torch.tensor([1, 0, 0, 0], dtype=torch.uint8))
+        DEC.layers_step(m, m.layers, x)
+        torch.cuda.synchronize()
+        for (c0, h0), (c1, h1) in zip(caches0, snap()):
+            assert torch.equal(c0, c1) and torch.equal(h0, h1), "a launch ran past the error word"
+        with pytest.raises(RuntimeError, match="timed out"):
+            DEC.layers_check(m)
+        assert int(chain.workspace.count_nonzero()) == 0, "the workspace was not cleared"
+        got = DEC.layers_step(m, m.layers, x)
+        DEC.layers_check(m)
+        got_caches = snap()
+        for l, (c, h) in zip(m.layers, caches0):
+            l.ssm._conv_context.copy_(c)
+            l.ssm._ssm_hiddens.copy_(h)
+        fresh = DEC.LayerChain(m.layers, x)
+        ref = fresh.step(m.layers, x)
+        fresh.check()
+    assert torch.equal(got, ref), "the step after the reset differs from a fresh chain's"
+    for (c0, h0), (c1, h1) in zip(got_caches, snap()):
+        assert torch.equal(c0, c1) and torch.equal(h0, h1)
+
+
 def test_chain_step_matches_oracle(cuda):
     """fp32 model through the harness (the chain path) against the oracle's
     step chain in float64."""

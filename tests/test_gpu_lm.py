@@ -48,6 +48,23 @@ def test_prefill_logits_fp32(cuda, pads):
     _close(got, ref, "logits", **F32)
 
 
+@pytest.mark.parametrize("pads", [False, True])
+def test_forward_last_is_the_row_at_lengths_minus_1(cuda, pads):
+    """forward_last (the prefill of generate: norm and LM head on one row per
+    sequence) against the oracle's full logits at lengths - 1, the rows the
+    reference's generate keeps (an empty row's index -1 wraps to the end)."""
+    m, cfg = make_lm(seed=1, vocab=53, model_dim=32, state_dim=16, layers=2)
+    sd = lm_state64(m)
+    m = m.to(cuda)
+    ids = _ids(3, 37, cfg.vocab_size, seed=2, pads=pads)
+    lengths = (ids != cfg.pad_token_id).sum(dim=1)
+    with torch.no_grad():
+        got = m.forward_last(ids.to(cuda), lengths.to(cuda))
+    ref, _ = LR.lm_forward(sd, ids, lengths)
+    assert got.shape == (3, cfg.vocab_size)
+    _close(got, ref[torch.arange(3), lengths - 1], "last-position logits", **F32)
+
+
 def test_prefill_then_steps_fp32(cuda):
     m, cfg = make_lm(seed=3, vocab=41, model_dim=32, state_dim=16, layers=3, bias=False,
                      conv_bias=False)
@@ -113,9 +130,8 @@ def test_graph_replays_match_eager_steps(cuda):
     dec = m.decoder(2, steps + 1)
     dec.capture()
     with torch.no_grad():
-        logits = m(ids, lengths, use_cache=True)
         pick = lambda lg: torch.softmax(lg, dim=-1).argmax(-1)
-        tok = pick(logits[torch.arange(2, device=cuda), lengths - 1])
+        tok = pick(m.forward_last(ids, lengths, use_cache=True))
         eager_tokens = [tok]
         eager_states = []
         for _ in range(steps):

@@ -4,10 +4,12 @@ under the reference's top-level names (``import selective_scan``,
 (``ops/selective_scan_interface.py:2,45-80``,
 ``ops/selective_update_interface.py:2,42``):
 
-* forward -> out and the chunk carry h (batch, dim, nchunks, 2*state_dim);
+* forward -> out and the chunk carry h (batch, dim, nchunks, 2*state_dim)
+  with nchunks = ceil(seq_len / 128) (``csrc/selective_scan/kernel_config.h:4-10``,
+  ``selective_scan.cpp:270-274``);
 * h[..., -1, 1::2] is the final state (``ops/selective_scan_interface.py:60``);
-* h[..., 0::2] / h[..., 1::2] are the (prod a, state) pairs of every chunk
-  (``csrc/selective_scan/forward_kernel.cu:225-228``; chunks of 16 steps here);
+* h[..., 0::2] / h[..., 1::2] are the (prod a, state) pairs of every 128-step
+  chunk (``csrc/selective_scan/forward_kernel.cu:225-228``);
 * the saved h goes back into backward with dout and dh_last, returning the 8
   gradients in the reference's order;
 * selective_update.apply is out of place.
@@ -89,22 +91,26 @@ def test_reference_call_sequence(cuda, padding, seqlen):
         assert_close(leaves[k].grad, rb[nm], torch.float32, nm, bmag.get(nm))
 
 
-def test_chunk_carry_pairs(cuda):
-    """h holds (prod a, state) per 16-step chunk; a contiguous copy of h is
-    accepted by backward and gives the same gradients."""
+@pytest.mark.parametrize("seqlen,lengths", [(300, (300, 171)), (256, (256, 100)), (100, (100, 71)),
+                                            (7, (7, 3))])
+def test_chunk_carry_pairs(cuda, seqlen, lengths):
+    """h holds (prod a, state) per 128-step chunk, the last chunk's carry the
+    final state whether or not 128 divides seq_len; a copy of h (which lacks
+    the 16-step states of the view's buffer) is accepted by backward, which
+    then recomputes the states, and gives the same gradients bit for bit."""
     ss = _toplevel("selective_scan")
-    batch, dim, seqlen, nstate = 2, 64, 100, 8
+    batch, dim, nstate = 2, 64, 8
     c = make_case(batch, dim, seqlen, nstate, torch.float32, seed=3, with_z=False, h_init=True)
     d = to_dev(c, cuda)
-    length = torch.tensor([100, 71])
+    length = torch.tensor(lengths)
     out, h = ss.forward(d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"],
                         d["h_init"], length.to(cuda), "left")
-    K = (seqlen + 15) // 16
+    K = (seqlen + 127) // 128
     assert h.shape == (batch, dim, K, 2 * nstate)
     a = (c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["delta_bias"], c["h_init"], length,
          False, None, True)
-    ref = R.scan_fwd(*a)
-    fmag = Lazy(lambda: R.scan_fwd(*a, magnitude=True))
+    ref = R.scan_fwd(*a, chunk=128)
+    fmag = Lazy(lambda: R.scan_fwd(*a, chunk=128, magnitude=True))
     torch.cuda.synchronize()
     assert_close(h[..., 1::2], ref["h_chunks"], torch.float32, "h_chunks", fmag.get("h_chunks"))
     assert_close(h[..., 0::2], ref["prod_a"], torch.float32, "prod_a")
@@ -114,10 +120,15 @@ def test_chunk_carry_pairs(cuda):
     args = (d["u"], d["A"], d["B"], d["C"], d["D"], d["delta"], d["delta_bias"])
     g1 = ss.backward(*args, h, d["h_init"], dy, dl, length.to(cuda), "left")
     g2 = ss.backward(*args, h.contiguous(), d["h_init"], dy, dl, length.to(cuda), "left")
-    for x, y in zip(g1, g2):
-        assert torch.equal(x, y)
+    g3 = ss.backward(*args, h.clone(), d["h_init"], dy, dl, length.to(cuda), "left")
+    for x, y, w in zip(g1, g2, g3):
+        assert torch.equal(x, y) and torch.equal(x, w)
+    rb = R.scan_bwd(*a, dy=dy, dh_last=dl)
+    bmag = Lazy(lambda: R.scan_bwd(*a, dy=dy, dh_last=dl, magnitude=True))
+    for got, nm in zip(g1, ("du", "dA", "dB", "dC", "dD", "ddelta", "ddelta_bias", "dh_init")):
+        assert_close(got, rb[nm], torch.float32, nm, bmag.get(nm))
     with pytest.raises(RuntimeError, match="h must have shape"):
-        ss.backward(*args, h[:, :, 1:], d["h_init"], dy, dl, length.to(cuda), "left")
+        ss.backward(*args, h[:, :, :, 1:], d["h_init"], dy, dl, length.to(cuda), "left")
 
 
 def test_toplevel_update_apply(cuda):

@@ -31,6 +31,8 @@ def test_queries():
     lib = N.lib()
     assert lib.ssm_abi_version() == N.ABI_VERSION
     assert [lib.ssm_scan_nchunks(x) for x in (0, 1, 16, 17, 2048)] == [0, 1, 1, 2, 128]
+    # the reference's kernel_config::get_num_chunks (128-step chunks)
+    assert [lib.ssm_scan_ref_nchunks(x) for x in (0, 1, 128, 129, 2048)] == [0, 1, 1, 2, 16]
     # fwd workspace: prepped B/C, fp32, rows padded to 16 steps, states padded to 4
     # prepped B/C (batch x pairs x padded steps x 4 floats) + a 256-byte store sink
     assert lib.ssm_scan_fwd_workspace_bytes(8, 2048, 2048, 16) == 8 * 4 * 2048 * 8 * 4 + 256
@@ -261,3 +263,38 @@ def test_layer_chain_arguments_are_checked():
     assert call(dtype=N.SSM_F32, rank=32, ws_bytes=1 << 30) == 2 and b"single pass" in lib.ssm_last_error()
     assert call(ws=P * 64 + 16) == 2 and b"256-byte" in lib.ssm_last_error()
     assert call(table=None) == 1
+
+
+def test_layer_chain_keeps_every_table_it_built():
+    """A HIP graph captured with one layer table keeps reading that table's
+    address, so LayerChain.update() must not free it when the cache addresses
+    change (another decoder's caches, a re-allocation): the old table stays
+    alive and is reused when its addresses come back.  Host tensors stand in
+    for the device ones (update() only builds the table of addresses)."""
+    import gc
+    import weakref
+
+    from ssm_mamba_amd import decode as dec
+    from ssm_mamba_amd.causal_lm import CausalLM, CausalLMConfig
+
+    cfg = CausalLMConfig(vocab_size=64, model_dim=128, num_layers=2, device="cpu")
+    m = CausalLM(cfg).to(torch.bfloat16).eval()
+    x = torch.zeros(2, 128, dtype=torch.bfloat16)
+    m.allocate_cache(2)
+    chain = dec.LayerChain(m.layers, x)
+    chain.update(m.layers)
+    first = weakref.ref(chain.table)
+    first_ptrs = chain.ptrs
+    old = [(l.ssm._conv_context, l.ssm._ssm_hiddens) for l in m.layers]
+    for l in m.layers:  # new caches, as a decoder of another max length would make
+        l.ssm._conv_context = torch.zeros_like(l.ssm._conv_context)
+        l.ssm._ssm_hiddens = torch.zeros_like(l.ssm._ssm_hiddens)
+    chain.update(m.layers)
+    assert chain.ptrs != first_ptrs
+    gc.collect()
+    assert first() is not None and first() is not chain.table
+    assert len(chain.tables) == 2
+    for l, (ctx, ssm) in zip(m.layers, old):
+        l.ssm._conv_context, l.ssm._ssm_hiddens = ctx, ssm
+    chain.update(m.layers)
+    assert chain.table is first() and len(chain.tables) == 2

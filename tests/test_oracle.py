@@ -74,9 +74,10 @@ def brute_fwd(c, length=None, padding_right=True, delta_softplus=True):
     return out, hl
 
 
-def naive_fwd_autograd(c, length=None, padding_right=True, delta_softplus=True):
+def naive_fwd_autograd(c, length=None, padding_right=True, delta_softplus=True, gate=True):
     """Differentiable forward written independently of the oracle: per-step
-    exp2 form and explicit masking, used only to obtain autograd gradients."""
+    exp2 form and explicit masking, used only to obtain autograd gradients.
+    gate=False returns the output before the z gate."""
     u, dl, A, B, C = c["u"], c["delta"], c["A"], c["B"], c["C"]
     D, bias, h0, z = c["D"], c["delta_bias"], c["h_init"], c["z"]
     batch, dim, L = u.shape
@@ -96,7 +97,7 @@ def naive_fwd_autograd(c, length=None, padding_right=True, delta_softplus=True):
         a = torch.pow(2.0, (dt[:, :, None] * A[None]) * (1.0 / math.log(2.0)))
         h = a * h + (dt * u[:, :, t])[:, :, None] * B[:, None, :, t]
         y = (h * C[:, None, :, t]).sum(-1) + D[None] * u[:, :, t]
-        if z is not None:
+        if z is not None and gate:
             y = y * F.silu(z[:, :, t])
         outs.append(y)
     return torch.stack(outs, -1), h
@@ -131,9 +132,14 @@ def test_backward_matches_autograd(padding_right, use_len, with_z, with_h0):
     dy = torch.randn(2, 3, 29, generator=g)
     dlast = torch.randn(2, 3, 4, generator=g)
     leaves = {k: (v.clone().requires_grad_(True) if v is not None else None) for k, v in c.items()}
-    y, hl = naive_fwd_autograd(leaves, length, padding_right)
-    mask = R.valid_mask(2, 29, length, padding_right)[:, None, :].to(y.dtype)
-    loss = (y * mask * dy).sum() + (hl * dlast).sum()
+    # The reference's composition: the scan (whose backward drops the
+    # gradient of padded outputs) and then the gate out * silu(z) outside
+    # it, which autograd differentiates at every position.
+    out, hl = naive_fwd_autograd(leaves, length, padding_right, gate=False)
+    mask = R.valid_mask(2, 29, length, padding_right)[:, None, :].to(out.dtype)
+    out = out * mask + (out * (1.0 - mask)).detach()
+    y = out * F.silu(leaves["z"]) if with_z else out
+    loss = (y * dy).sum() + (hl * dlast).sum()
     loss.backward()
     res = R.scan_bwd(**c, length=length, padding_right=padding_right, dy=dy,
                      dh_last=dlast, seg=8)
