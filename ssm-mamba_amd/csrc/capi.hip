@@ -121,6 +121,10 @@ bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr
 size_t round256(size_t bytes) { return (bytes + 255) & ~(size_t)255; }
 
 // state chunks of the backward past ssm::kBwdChunkStates states (0: one pass)
+// Row length of the backward's dB/dC partials: seqlen padded to whole 16-step
+// tiles (bc_part_len in scan_bwd.hip).
+size_t bwd_part_len(int64_t seqlen) { return (size_t)(seqlen + ssm::kTileB - 1) / ssm::kTileB * ssm::kTileB; }
+
 size_t bwd_chunks(int64_t nstate) {
   return nstate > ssm::kBwdChunkStates
              ? (size_t)((nstate + ssm::kBwdChunkStates - 1) / ssm::kBwdChunkStates)
@@ -318,7 +322,7 @@ size_t ssm_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen, 
   ssm::fwd_segments((int)batch, (int)nblk, (int)seqlen, nseg, seg_len);
   const size_t rows = (size_t)batch * nseg;  // (segment, batch row) partial rows
   return round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float)) +
-         round256(2 * nblk * batch * nstate * seqlen * sizeof(float)) +
+         round256(2 * nblk * batch * nstate * bwd_part_len(seqlen) * sizeof(float)) +
          round256(rows * dim * nstate * sizeof(float)) +
          2 * round256(rows * dim * sizeof(float)) +
          round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) *
@@ -436,7 +440,7 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   float* bc = reinterpret_cast<float*>(ws);
   ws += round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
   p.ws_bc = reinterpret_cast<float*>(ws);
-  ws += round256(2 * (size_t)p.nblk * batch * nstate * seqlen * sizeof(float));
+  ws += round256(2 * (size_t)p.nblk * batch * nstate * bwd_part_len(seqlen) * sizeof(float));
   p.ws_A = reinterpret_cast<float*>(ws);
   ws += round256(rows * dim * nstate * sizeof(float));
   p.ws_D = reinterpret_cast<float*>(ws);

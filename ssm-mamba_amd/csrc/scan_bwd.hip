@@ -29,10 +29,13 @@
 // sums over states (sum G B, sum A G a h) leave each wave in its own
 // LDS slice and are added in a fixed order; the per-position sums over
 // channels (dB, dC) are reduced across the 64 lanes with a permlane/DPP
-// reduce-scatter and written as one partial per (channel block, b, n, t),
-// which a second small kernel adds up.  dA, dD and dbias are written as
+// reduce-scatter (two 4-step blocks at a time in the role-split kernel) and
+// written as one partial per (channel block, b, n, t), in rows padded to whole
+// tiles, which a second small kernel adds up.  dA, dD and dbias are written as
 // per-batch-row partials reduced by the same kernel, so the result is
 // deterministic (no atomics).
+#include <type_traits>
+
 #include "ss_io.cuh"
 #include "ss_params.h"
 #include "ss_prof.h"
@@ -40,6 +43,49 @@
 namespace ssm {
 
 namespace {
+
+// Row length of the dB/dC partials: seqlen padded to whole 16-step tiles, so
+// a tile's stores need no step check (the padding is never read).
+__host__ __device__ __forceinline__ int bc_part_len(int L) { return (L + kTileB - 1) / kTileB * kTileB; }
+
+// softplus and its derivative with the reference's threshold 20, as
+// softplus_and_grad_t20, without the select of the derivative above the
+// threshold: there e = exp(-x) < 2^-24, so 1 + e rounds to 1 and its
+// reciprocal is 1 exactly, the value the threshold gives.
+__device__ __forceinline__ void softplus_and_grad_u(float x, float& sp, float& sg) {
+  const float e = fast_exp2(-fabsf(x) * kLog2e);
+  const float r = fast_rcp(1.0f + e);
+  sp = fmaxf(x, 0.0f) + log1p_pos(e);
+  sg = x >= 0.0f ? r : e * r;
+}
+
+// Sum over the 64 lanes of 32 values per lane: afterwards v[0] of lane l
+// holds the total of value index l >> 1 (the two lanes of a pair hold the
+// same total).  Value bit 4 follows lane bit 5 (permlane32 swaps), bit 3 lane
+// bit 4 (permlane16 swaps), bits 2..0 lane bits 3..1 (DPP folds), and the
+// pair adds over lane bit 0: 70 VALU, as two wave_reduce16, with twice the
+// independent work at every level.
+__device__ __forceinline__ void wave_reduce32(float (&v)[32], int lane) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 16]),
+                                              false, false);
+    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]),
+                                              false, false);
+    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  const bool b3 = lane & 8, b2 = lane & 4, b1 = lane & 2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = rs_fold<kDppRowRor8>(v[i], v[i + 4], b3);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) v[i] = rs_fold<kDppRowHalfMirror>(v[i], v[i + 2], b2);
+  v[0] = rs_fold<kDppQuadXor2>(v[0], v[1], b1);
+  v[0] += dpp_mov<kDppQuadXor1>(v[0]);
+}
 
 struct StepVals {  // per-position LDS values of one 4-step block
   float4 dl, du, dout;
@@ -204,7 +250,8 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   const size_t srow = (size_t)seg * p.batch + b;  // (segment, batch row) of the partials
   const int ngroups = (N + 1) / 2;
   const size_t rb = (size_t)b * Dm;
-  const size_t nBC = (size_t)p.batch * N * L;
+  const int Lp = bc_part_len(L);  // partial rows padded to whole tiles
+  const size_t nBC = (size_t)p.batch * N * Lp;
   const T* __restrict__ Braw = Bp + (size_t)b * p.bc_bstride;
   const T* __restrict__ Craw = Cp + (size_t)b * p.bc_bstride;
   float* const dummyf = static_cast<float*>(dummy);
@@ -405,7 +452,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       const int vi = lane >> 2;
       const int rkind = vi >> 3, rs = (vi >> 2) & 1, rj = vi & 3;
       const int rn = n0 + G * 2 + rs;
-      float* const wsb = ws_bc + ((size_t)rkind * p.nblk + blk) * nBC + ((size_t)b * N + rn) * L;
+      float* const wsb = ws_bc + ((size_t)rkind * p.nblk + blk) * nBC + ((size_t)b * N + rn) * Lp;
       auto rev = [&](int jq, const StepVals& sv) {
         float gB[4], gD[4], vals[16];
         bwd_reverse_block(jq, sv, bcg[jq], Av[g], A2[g], hc[g], a, H, gam[g], dA[g], vals, gB,
@@ -429,6 +476,11 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       ld(1, Y, false); fwd(1, Y);
       ld(2, X, false); fwd(2, X);
       ld(3, Y, true);  fwd(3, Y);
+      // the reverse re-reads the block registers: hide their values from
+      // the recompute's, so each DPP broadcast folds into its own multiply
+      // (shared, it is materialised with an extra v_mov_dpp and a register)
+#pragma unroll
+      for (int jq = 0; jq < kT4; ++jq) asm volatile("" : "+v"(bcg[jq]));
       rev(3, Y);
       ld(2, X, true); rev(2, X);
       ld(1, Y, true); rev(1, Y);
@@ -625,8 +677,8 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
     const int ch = d0 + lane;
     const bool ch_ok = ch < Dm;
     const int chc = min(ch, Dm - 1);
-    const size_t nBC = (size_t)p.batch * N * L;
-    float* const dummyf = static_cast<float*>(dummy);
+    const int Lp = bc_part_len(L);  // partial rows padded to whole tiles
+    const size_t nBC = (size_t)p.batch * N * Lp;
     float gam[2], dA[2], Av[2], A2[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -644,34 +696,58 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
       }
       gam[s] = q;
     }
-    // the state the forward saved before tile t (h_init, or zero, before tile 0)
+    // The state the forward saved before tile t: h_init (or zero) before
+    // tile 0, else through a buffer range over the batch row's saved rows
+    // (the launch keeps them below 2^31 bytes), the lane's state row as the
+    // vector offset and the tile as the scalar offset.
+    const int nc0 = min(2 * w, N - 1), nc1 = min(2 * w + 1, N - 1);
+    const size_t hrow = (size_t)N * p.hs * Dm;  // floats per saved slot
+    const auto h_rsrc = raw_rsrc(const_cast<float*>(h_chunks) + (size_t)b * p.nchunks * hrow,
+                                 (uint32_t)((size_t)p.nchunks * hrow * sizeof(float)));
+    const uint32_t hv0 = (uint32_t)(((size_t)nc0 * p.hs * Dm + chc) * sizeof(float));
+    const uint32_t hv1 = (uint32_t)(((size_t)nc1 * p.hs * Dm + chc) * sizeof(float));
+    const float hi0 = h_init ? h_init[(rb + chc) * N + nc0] : 0.0f;
+    const float hi1 = h_init ? h_init[(rb + chc) * N + nc1] : 0.0f;
+    // (the loads are unconditional, from slot 0 for tile 0, and the choice is
+    // made where the state is used: a load inside a branch is waited for at
+    // the branch's end)
     auto saved_state = [&](int tile, float (&r)[2]) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int nc = min(2 * w + s, N - 1);
-        const float* src =
-            tile > 0 ? h_chunks + (((size_t)b * p.nchunks + (tile - 1)) * N + nc) * p.hs * (size_t)Dm + chc
-                     : (h_init ? h_init + (rb + chc) * N + nc : h_chunks);
-        r[s] = *src;
-      }
+      const int so = (int)((size_t)max(tile - 1, 0) * hrow * sizeof(float));
+      r[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(h_rsrc, (int)hv0, so, 0));
+      r[1] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(h_rsrc, (int)hv1, so, 0));
     };
     float hcn[2];
     saved_state(tile_end - 1, hcn);
-    const int vi = lane >> 2;  // the value of lane l after the reduction: index l >> 2
-    const int rkind = vi >> 3, rs = (vi >> 2) & 1, rj = vi & 3;
+    // the value of lane l after the reduction of two blocks: index l >> 1,
+    // (block of the pair, kind, state, step)
+    const int vi = lane >> 1;
+    const int rsel = vi >> 4, rkind = (vi >> 3) & 1, rs = (vi >> 2) & 1, rj = vi & 3;
     const int rn = 2 * w + rs;
-    float* const wsb = ws_bc + ((size_t)rkind * p.nblk + blk) * nBC + ((size_t)b * N + rn) * L;
+    // the partials go through a buffer range over all of them (the launch
+    // keeps them below 2^31 bytes): the lane's row and step as the vector
+    // offset, the tile's first step as the scalar offset, the block as the
+    // immediate; a state past N gets an offset past the range
+    const auto bc_rsrc = raw_rsrc(ws_bc, (uint32_t)(2 * (size_t)p.nblk * nBC * sizeof(float)));
+    // (the offset of the pair's second block, jq - 1; the first block adds 16
+    // bytes, 4 steps, so that no offset is negative)
+    const uint32_t bc_off =
+        rn < N ? (uint32_t)((((size_t)rkind * p.nblk + blk) * nBC + ((size_t)b * N + rn) * Lp + rj) *
+                            sizeof(float)) + 16u * (1 - rsel)
+               : kOffDrop;
     const bool hc_ok0 = ch_ok && 2 * w < N, hc_ok1 = ch_ok && 2 * w + 1 < N;
 
-    for (int i = 0; i < nbar; ++i) {
+    // One iteration per barrier; the staging parity is a template constant
+    // (the loop runs iterations in pairs), so every LDS address is a
+    // per-lane base plus an immediate.
+    auto iteration = [&](int i, auto parity) {
+      constexpr int buf = decltype(parity)::value;
       __syncthreads();
-      if (i >= nt) continue;
+      if (i >= nt) return;
       const int tile = tile_end - 1 - i;
       const int t0 = tile * kTileB;
-      const int buf = i & 1;
       float hc[2];
-      hc[0] = (hc_ok0 && (tile > 0 || h_init)) ? hcn[0] : 0.0f;
-      hc[1] = (hc_ok1 && (tile > 0 || h_init)) ? hcn[1] : 0.0f;
+      hc[0] = tile > 0 ? (hc_ok0 ? hcn[0] : 0.0f) : hi0;
+      hc[1] = tile > 0 ? (hc_ok1 ? hcn[1] : 0.0f) : hi1;
       saved_state(max(tile - 1, tile_beg), hcn);  // the next tile's (re-read at the last)
 
       float a[2][kChunk], H[2][kChunk];
@@ -686,15 +762,20 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
         float y[4];  // unused here (the forward saved the output)
         bwd_recompute_block(jq, sv, bcg[jq], A2, hc, a, H, y);
       };
-      auto rev = [&](int jq, const StepVals& sv) {
-        float gB[4], gD[4], vals[16];
-        bwd_reverse_block(jq, sv, bcg[jq], Av, A2, hc, a, H, gam, dA, vals, gB, gD);
+      // the reverse of block jq; its 16 dB/dC terms go to vals[16 * half ..]
+      auto rev = [&](int jq, const StepVals& sv, float (&vals)[32], int half) {
+        float gB[4], gD[4], v16[16];
+        bwd_reverse_block(jq, sv, bcg[jq], Av, A2, hc, a, H, gam, dA, v16, gB, gD);
         put4(sGB[buf][w], jq, gB);
         put4(sDD[buf][w], jq, gD);
-        // sum over the 64 channels of this block
-        wave_reduce16(vals, lane);
-        const int t = t0 + 4 * jq + rj;
-        *((rn < N && t < L) ? wsb + t : dummyf) = vals[0];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) vals[16 * half + k] = v16[k];
+      };
+      // sum over the 64 channels of blocks jq and jq - 1 together
+      auto reduce_store = [&](int jq, float (&vals)[32]) {
+        wave_reduce32(vals, lane);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(vals[0]), bc_rsrc,
+                                              (int)(bc_off + 16u * (jq - 1)), t0 * 4, 0);
       };
       auto ld = [&](int jq, StepVals& sv, bool with_dout) {
         const int li = lane ^ bws_swz(jq);
@@ -707,10 +788,24 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
       ld(1, Y, false); fwd(1, Y);
       ld(2, X, false); fwd(2, X);
       ld(3, Y, true);  fwd(3, Y);
-      rev(3, Y);
-      ld(2, X, true); rev(2, X);
-      ld(1, Y, true); rev(1, Y);
-      ld(0, X, true); rev(0, X);
+      // the reverse re-reads the block registers: hide their values from
+      // the recompute's, so each DPP broadcast folds into its own multiply
+      // (shared, it is materialised with an extra v_mov_dpp and a register)
+#pragma unroll
+      for (int jq = 0; jq < kT4; ++jq) asm volatile("" : "+v"(bcg[jq]));
+      float v32[32];
+      rev(3, Y, v32, 0);
+      ld(2, X, true); rev(2, X, v32, 1);
+      reduce_store(3, v32);
+      ld(1, Y, true); rev(1, Y, v32, 0);
+      ld(0, X, true); rev(0, X, v32, 1);
+      reduce_store(1, v32);
+    };
+    // nbar - 1 is a multiple of 4: iteration 0, then pairs of parity 1, 0
+    iteration(0, std::integral_constant<int, 0>{});
+    for (int i = 1; i < nbar; i += 2) {
+      iteration(i, std::integral_constant<int, 1>{});
+      iteration(i + 1, std::integral_constant<int, 0>{});
     }
     // per-row partials
 #pragma unroll
@@ -843,7 +938,7 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
     for (int j = 0; j < 4; ++j) {
       const float x = dv[j] + Bias;
       float sp, g;
-      softplus_and_grad_t20(x, sp, g);
+      softplus_and_grad_u(x, sp, g);
       de[j] = __uint_as_float(__float_as_uint(softplus ? sp : x) & keep[j]);
       k.sg[j] = __uint_as_float(__float_as_uint(softplus ? g : 1.0f) & keep[j]);
       du[j] = de[j] * uv[j];
@@ -1221,28 +1316,33 @@ __global__ __launch_bounds__(256) void scan_bwd_reduce_kernel(
     const float* __restrict__ ws_D, const float* __restrict__ ws_bias, T* __restrict__ dB,
     T* __restrict__ dC, float* __restrict__ dA, float* __restrict__ dD,
     float* __restrict__ dbias) {
-  constexpr int kW = kVec ? 4 : 1;  // dB/dC elements per work item
-  const size_t nBC = (size_t)batch * N * L;
+  // the partial rows are bc_part_len(L) long; a work item sums 4 steps of one
+  // (kind, b, n) row over the channel blocks, and writes the steps below L
+  // (as one vector when kVec: L % 4 == 0 and dB / dC 4-element aligned)
+  const int Lp = bc_part_len(L), L4 = Lp / 4;
+  const size_t nrow = (size_t)batch * N;
+  const size_t nBC = nrow * Lp;
   const size_t nA = (size_t)dim * N;
-  const size_t nbc_items = 2 * nBC / kW;
+  const size_t nbc_items = 2 * nrow * L4;
   const size_t total = nbc_items + nA + dim;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
     if (i < nbc_items) {
-      const size_t e = i * kW;
-      const size_t kind = e / nBC, r = e % nBC;
-      const float* src = ws_bc + kind * nblk * nBC + r;
-      T* dst = (kind ? dC : dB) + r;
-      if constexpr (kVec) {
-        float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        // 4 partial loads in flight per thread (8, 16 and 32 were slower: the
-        // partials of one output lie a channel block's plane apart)
+      const size_t rr = i / L4;  // kind * nrow + row
+      const int t = (int)(i % L4) * 4;
+      const size_t kind = rr / nrow, r = rr % nrow;
+      const float* src = ws_bc + kind * nblk * nBC + r * Lp + t;
+      float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      // 4 partial loads in flight per thread (8, 16 and 32 were slower: the
+      // partials of one output lie a channel block's plane apart)
 #pragma unroll 4
-        for (int k = 0; k < nblk; ++k) {
-          const float4 v = *reinterpret_cast<const float4*>(src + (size_t)k * nBC);
-          s4.x += v.x; s4.y += v.y; s4.z += v.z; s4.w += v.w;
-        }
-        const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+      for (int k = 0; k < nblk; ++k) {
+        const float4 v = *reinterpret_cast<const float4*>(src + (size_t)k * nBC);
+        s4.x += v.x; s4.y += v.y; s4.z += v.z; s4.w += v.w;
+      }
+      const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+      T* dst = (kind ? dC : dB) + r * L + t;
+      if (kVec && t + 4 <= L) {
         if constexpr (sizeof(T) == 4) {
           *reinterpret_cast<float4*>(dst) = s4;
         } else {
@@ -1250,9 +1350,9 @@ __global__ __launch_bounds__(256) void scan_bwd_reduce_kernel(
               make_uint2(pack_bf16x2(sv[0], sv[1]), pack_bf16x2(sv[2], sv[3]));
         }
       } else {
-        float acc = 0.0f;
-        for (int k = 0; k < nblk; ++k) acc += src[(size_t)k * nBC];
-        Elem<T>::store1(dst, acc);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (t + j < L) Elem<T>::store1(dst + j, sv[j]);
       }
     } else if (i < nbc_items + nA) {
       const size_t r = i - nbc_items;
@@ -1290,9 +1390,11 @@ static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t 
     if (e != hipSuccess) return e;
   }
   dim3 grid(p.nblk, p.batch, p.nseg * nsc);
-  // the role-split kernel's output buffer ranges (a wave's 16 rows) must fit
-  // 2^31 bytes
-  if (kSG == 1 && !kPart && (size_t)(kBlockCh / kWsProd) * p.seqlen * sizeof(T) < (1u << 31)) {
+  // the role-split kernel's buffer ranges must fit 2^31 bytes: a wave's 16
+  // output rows, all of the dB/dC partials, and a batch row's saved states
+  if (kSG == 1 && !kPart && (size_t)(kBlockCh / kWsProd) * p.seqlen * sizeof(T) < (1u << 31) &&
+      2 * (size_t)p.nblk * p.batch * p.nstate * bc_part_len(p.seqlen) * sizeof(float) < (1u << 31) &&
+      (size_t)p.nchunks * p.nstate * p.hs * p.dim * sizeof(float) < (1u << 31)) {
     ProfScope prof("scan_bwd", st);
     hipLaunchKernelGGL((scan_bwd_ws_kernel<T, kHasZ, kAligned>), grid, dim3(kWsThreads), 0, st,
                        dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, (const T*)p.B,
@@ -1340,11 +1442,11 @@ static hipError_t launch_bwd2(const ScanParams& p, const float* bc, bool aligned
   else if (p.nstate <= kBwdChunkStates) e = launch_bwd3<T, 4>(p, bc, aligned, st);
   else e = launch_bwd3<T, 4, true>(p, bc, aligned, st);
   if (e != hipSuccess) return e;
-  const size_t nBC = (size_t)p.batch * p.nstate * p.seqlen;
   const uintptr_t vec_align = 4 * sizeof(T);
-  const bool vec = nBC % 4 == 0 && (uintptr_t)p.dB % vec_align == 0 &&
+  const bool vec = p.seqlen % 4 == 0 && (uintptr_t)p.dB % vec_align == 0 &&
                    (uintptr_t)p.dC % vec_align == 0;
-  const size_t total = 2 * nBC / (vec ? 4 : 1) + (size_t)p.dim * p.nstate + p.dim;
+  const size_t total = 2 * (size_t)p.batch * p.nstate * (bc_part_len(p.seqlen) / 4) +
+                       (size_t)p.dim * p.nstate + p.dim;
   const int blocks = (int)std::min<size_t>((total + 255) / 256, 16384);
   ProfScope prof("scan_bwd_reduce", st);
   if (vec)
