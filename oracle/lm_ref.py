@@ -11,8 +11,9 @@ names:
 * ``mamba_forward`` -- ``modules/mamba.py:82-187``: in-projection split into
   (x, gate), conv + SiLU, x-projection split into (delta_r, B, C), delta =
   W_dt @ delta_r with the bias handed to the scan, A = -exp(log_A), the scan
-  with ``lengths`` and the reference call's default left padding, the gate
-  out*silu(gate), out-projection; with use_cache, the conv window of the k-1
+  with ``lengths`` and the reference call's default left padding (under
+  autograd the scan's gradient is dropped at padded outputs, as the
+  reference's backward kernel does), the gate out*silu(gate), out-projection; with use_cache, the conv window of the k-1
   pre-conv inputs ending at lengths-1 (zero before the sequence start,
   :113-135) and the last state;
 * ``mamba_step``    -- ``modules/mamba.py:189-243``;
@@ -31,7 +32,7 @@ from typing import Dict, List, Optional, Tuple
 
 import torch
 
-from .scan_ref import scan_fwd, update
+from .scan_ref import scan_fwd, update, valid_mask
 
 __all__ = ["rms_norm", "causal_conv", "mamba_forward", "mamba_step", "lm_forward", "lm_step",
            "generate", "layer_params"]
@@ -105,6 +106,15 @@ def mamba_forward(p: Dict[str, torch.Tensor], x: torch.Tensor, state_dim: int, d
     res = scan_fwd(xc, delta, A, Bm, Cm, g("D"), g("delta_proj.bias"), h0,
                    None if lengths is None else lengths.cpu(), padding_right=False, z=gate,
                    chunk=None, dtype=x.dtype, keep_graph=True)
+    out = res["out"]
+    if lengths is not None:
+        # the scan's backward drops the gradient of its padded outputs
+        # (backward_kernel.cu:241-246; the reference call's left padding),
+        # while the gate outside it (modules/mamba.py:181-182) is
+        # differentiated at every position: same values, that gradient rule
+        m = valid_mask(batch, seqlen, lengths.cpu(), False)[:, None, :].to(out.dtype)
+        out = out * m + (out * (1.0 - m)).detach()
+    y_gated = out * _silu(gate)
     if state_mag is not None:
         sm = scan_fwd(xc, delta, A, Bm, Cm, g("D"), g("delta_proj.bias"), h0,
                       None if lengths is None else lengths.cpu(), padding_right=False, z=gate,
@@ -122,7 +132,7 @@ def mamba_forward(p: Dict[str, torch.Tensor], x: torch.Tensor, state_dim: int, d
                     if t >= 0:
                         wm[b, :, j] = xm[b, :, t]
         state_mag.append((sm, wm))
-    y = res["y"].permute(0, 2, 1) @ g("out_proj.weight").t()
+    y = y_gated.permute(0, 2, 1) @ g("out_proj.weight").t()
     if g("out_proj.bias") is not None:
         y = y + g("out_proj.bias")
     return y, res["h_last"], ctx

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from oracle import lm_ref as LR
-from tests.helpers import lm_state64, make_lm
+from tests.helpers import assert_close, lm_state64, make_lm
 
 pytestmark = pytest.mark.gpu
 
@@ -169,13 +169,13 @@ def test_bf16_weights_close_to_oracle(cuda):
     _close(got, ref, "bf16 step logits", rtol=3e-2, atol=3e-2 * scale)
 
 
-def test_training_gradients_fp32(cuda):
+@pytest.mark.parametrize("pads", [False, True])
+def test_training_gradients_fp32(cuda, pads):
     """Parameter gradients of sum(logits * r) through the HIP scan backward,
-    against float64 autograd through the oracle model.  Unpadded: with
-    ``lengths`` the scan's backward ignores the upstream gradient at padded
-    positions (the reference's rule, covered by the operator tests), so the
-    model gradient is then not the autograd gradient of the forward."""
-    pads = False
+    against float64 autograd through the oracle model, at the stated fp32
+    bar.  With left-padded prompts (``lengths``) the oracle follows the
+    reference's training rule: the scan drops the upstream gradient of its
+    padded outputs, the gate and the other paths do not."""
     m, cfg = make_lm(seed=14, vocab=23, model_dim=32, state_dim=16, layers=2)
     sd = lm_state64(m)
     for v in sd.values():
@@ -195,9 +195,7 @@ def test_training_gradients_fp32(cuda):
               "layers.1.ssm.ssm_param_proj.weight", "layers.1.ssm.delta_proj.weight",
               "layers.1.ssm.delta_proj.bias", "layers.0.ssm.log_A", "layers.1.ssm.D",
               "layers.1.ssm.out_proj.weight"]:
-        gr = sd[k].grad
-        rms = float(gr.pow(2).mean().sqrt())
-        _close(names[k].grad, gr, f"grad {k}", rtol=2e-3, atol=2e-4 * max(rms, 1e-3))
+        assert_close(names[k].grad, sd[k].grad, torch.float32, f"grad {k}")
 
 
 @pytest.mark.parametrize("fold", [True, False])
