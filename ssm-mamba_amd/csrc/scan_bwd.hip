@@ -59,31 +59,67 @@ __device__ __forceinline__ void softplus_and_grad_u(float x, float& sp, float& s
   sg = x >= 0.0f ? r : e * r;
 }
 
-// Sum over the 64 lanes of 32 values per lane: afterwards v[0] of lane l
-// holds the total of value index l >> 1 (the two lanes of a pair hold the
-// same total).  Value bit 4 follows lane bit 5 (permlane32 swaps), bit 3 lane
-// bit 4 (permlane16 swaps), bits 2..0 lane bits 3..1 (DPP folds), and the
-// pair adds over lane bit 0: 70 VALU, as two wave_reduce16, with twice the
-// independent work at every level.
+// Reduce-scatter folds on lane bits 3 and 2 without selects: two DPP adds
+// with complementary bank masks write one register, the lanes whose bit is
+// clear adding the pair's first value with their partner's, the others the
+// second (the sums rs_fold forms, in the same operand order up to
+// commutation, so the same bits).  Banks are lane bits 3..2 of a row.  The
+// s_nop gives the two wait states a DPP read needs after a VALU write of its
+// source (the compiler does not see the DPP inside the asm).
+__device__ __forceinline__ float fold_ror8(float p, float q) {  // bit 3: partner l ^ 8
+  float r;
+  asm("s_nop 1\n\t"
+      "v_add_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %0, %2, %2 row_ror:8 row_mask:0xf bank_mask:0xc"
+      : "=&v"(r)
+      : "v"(p), "v"(q));
+  return r;
+}
+__device__ __forceinline__ float fold_half_mirror(float p, float q) {  // bit 2: partner 7 - l in 8
+  float r;
+  asm("s_nop 1\n\t"
+      "v_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0xa"
+      : "=&v"(r)
+      : "v"(p), "v"(q));
+  return r;
+}
+
+// Sum over the 64 lanes of 32 values per lane.  The cross-row moves
+// (v_permlane16/32_swap) cost about 2.4 issue slots each against 1 for the
+// in-row DPP forms (measured), so the in-row folds go first, on 32 and 16
+// values, and the swaps after them, on 8 and 4:
+//   lane bit 3 (row_ror:8, masked) -> value bit 4,
+//   lane bit 2 (row_half_mirror, masked; the partner 7 - l also differs in
+//     bits 1..0, which the last two levels sum over) -> value bit 3,
+//   lane bit 4 (permlane16 swaps) -> value bit 2,
+//   lane bit 5 (permlane32 swaps) -> value bit 1,
+//   lane bit 1 (quad_perm xor 2, with selects) -> value bit 0,
+// then an add over lane bit 0.  Afterwards v[0] of lane l holds the total of
+// value index (b3 b2 b4 b5 b1) of l's bits (lanes l and l ^ 1 hold the same):
+// 64 VALU with 6 swaps, against 70 with 24 for the permlane levels first.
+__device__ __forceinline__ int reduce32_index(int lane) {
+  return ((lane >> 3) & 1) << 4 | ((lane >> 2) & 1) << 3 | ((lane >> 4) & 1) << 2 |
+         ((lane >> 5) & 1) << 1 | ((lane >> 1) & 1);
+}
 __device__ __forceinline__ void wave_reduce32(float (&v)[32], int lane) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 16]),
+  for (int i = 0; i < 16; ++i) v[i] = fold_ror8(v[i], v[i + 16]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = fold_half_mirror(v[i], v[i + 8]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]),
                                               false, false);
     v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]),
+  for (int i = 0; i < 2; ++i) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 2]),
                                               false, false);
     v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
-  const bool b3 = lane & 8, b2 = lane & 4, b1 = lane & 2;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = rs_fold<kDppRowRor8>(v[i], v[i + 4], b3);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) v[i] = rs_fold<kDppRowHalfMirror>(v[i], v[i + 2], b2);
-  v[0] = rs_fold<kDppQuadXor2>(v[0], v[1], b1);
+  v[0] = rs_fold<kDppQuadXor2>(v[0], v[1], (lane & 2) != 0);
   v[0] += dpp_mov<kDppQuadXor1>(v[0]);
 }
 
@@ -718,9 +754,9 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
     };
     float hcn[2];
     saved_state(tile_end - 1, hcn);
-    // the value of lane l after the reduction of two blocks: index l >> 1,
-    // (block of the pair, kind, state, step)
-    const int vi = lane >> 1;
+    // the value of lane l after the reduction of two blocks (block of the
+    // pair, kind, state, step)
+    const int vi = reduce32_index(lane);
     const int rsel = vi >> 4, rkind = (vi >> 3) & 1, rs = (vi >> 2) & 1, rj = vi & 3;
     const int rn = 2 * w + rs;
     // the partials go through a buffer range over all of them (the launch
