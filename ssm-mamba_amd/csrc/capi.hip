@@ -435,6 +435,9 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   // [segment carries and step sums][dummy]; the dA/dD/dbias partials have one
   // row per (segment, batch row)
   ssm::fwd_segments((int)batch, p.nblk, (int)seqlen, p.nseg, p.seg_len);
+  // the role-split segment summaries split segments as the forward's do (the
+  // carries fit the same workspace range)
+  p.sub_k = ssm::fwd_summary_split((int)batch, p.nblk, p.nseg, p.seg_len);
   const size_t rows = (size_t)batch * p.nseg;
   char* ws = static_cast<char*>(workspace);
   float* bc = reinterpret_cast<float*>(ws);
@@ -448,7 +451,7 @@ int ssm_selective_scan_bwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t n
   p.ws_bias = reinterpret_cast<float*>(ws);
   ws += round256(rows * dim * sizeof(float));
   p.seg_h = reinterpret_cast<float*>(ws);
-  p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * batch * nstate * dim;
+  p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * p.sub_k * batch * nstate * dim;
   ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));
   p.nsc = (int)bwd_chunks(nstate);
   const size_t part_bytes = round256(p.nsc * (size_t)batch * dim * seqlen * sizeof(float));

@@ -311,11 +311,11 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
       A2[g][s] = Av[g][s] * kLog2e;
       // carry in from the later segments, last first:
       // gamma <- gamma_seg + exp(A sum dt) gamma (their summaries, zero carry-in)
+      // (summary row k = segment k + 1, k = nseg - 2 .. seg)
       float q = (ok && dh_last) ? dh_last[(rb + ch) * N + n] : 0.0f;
-      for (int sp = p.nseg - 1; ok && sp > seg; --sp) {
-        const size_t sb = (size_t)(sp - 1) * p.batch + b;
-        q = fmaf(fast_exp2(A2[g][s] * seg_dt[sb * Dm + ch]), q, seg_g[(sb * N + n) * Dm + ch]);
-      }
+      if (ok)
+        q = fold_carry(q, A2[g][s], seg_dt, seg_g, p.nseg - 2, -1, p.nseg - 1 - seg, p.batch, b, Dm,
+                       N, n, ch);
       gam[g][s] = q;
     }
 
@@ -725,11 +725,11 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
       A2[s] = Av[s] * kLog2e;
       // carry in from the later segments, last first:
       // gamma <- gamma_seg + exp(A sum dt) gamma (their summaries, zero carry-in)
+      // (summary row k: sub-segment k + sub_k of seg_len / sub_k steps)
       float q = (ok && dh_last) ? dh_last[(rb + ch) * N + n] : 0.0f;
-      for (int sp = p.nseg - 1; ok && sp > seg; --sp) {
-        const size_t sb = (size_t)(sp - 1) * p.batch + b;
-        q = fmaf(fast_exp2(A2[s] * seg_dt[sb * Dm + ch]), q, seg_g[(sb * N + n) * Dm + ch]);
-      }
+      if (ok)
+        q = fold_carry(q, A2[s], seg_dt, seg_g, (p.nseg - 1) * p.sub_k - 1, -1,
+                       (p.nseg - 1 - seg) * p.sub_k, p.batch, b, Dm, N, n, ch);
       gam[s] = q;
     }
     // The state the forward saved before tile t: h_init (or zero) before
@@ -1340,6 +1340,224 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_segsum_kernel(
   if (a_q == 0 && a_ok && n0 == 0) seg_dt[sb * Dm + a_ch] = dtsum;
 }
 
+// Role-split segment summaries of the backward for up to 16 states: the
+// numbers scan_bwd_segsum_kernel computes, per sub-segment of seg_len / sub_k
+// steps (blockIdx.z = k: global sub-segment k + sub_k, so the sub-segments
+// of segments 1 .. nseg-1), with the forward's role split so that staging
+// overlaps the recurrence:
+//   consumer waves 0..7   lane = channel, wave w = states 2w and 2w+1: from
+//                         gamma = 0 after the sub-segment's last step, down
+//                         to its first, G_t = gamma_t + dout_t C_t and
+//                         gamma_{t-1} = a_t G_t, reading delta, the effective
+//                         dout and (C_2w, C_2w+1) from LDS;
+//   producer waves 8..11  lane -> (channel row, 4-step column): stage the
+//                         16-step tiles two ahead of the walk (softplus, the
+//                         window mask, dout * silu(z), C), and sum the
+//                         steps' delta.
+// The main backward folds the summaries from the last sub-segment down to
+// the first one after its segment.  A sub-segment past the sequence end has
+// no tiles and leaves gamma = 0 and sum dt = 0 (the identity).
+template <typename T, bool kHasZ, bool kAligned>
+__global__ __launch_bounds__(kWsThreads, kAligned ? 6 : 5) void scan_bwd_segsum_ws_kernel(
+    const ScanDims p, const T* __restrict__ dl, const T* __restrict__ dyp,
+    const T* __restrict__ zp, const float* __restrict__ Ap, const T* __restrict__ Cp,
+    const float* __restrict__ biasp, const int64_t* __restrict__ length,
+    float* __restrict__ seg_g, float* __restrict__ seg_dt) {
+  // raw rows in flight: 4 tiles; 2 for fp32, whose 16-byte pieces would
+  // otherwise hold the producers above the registers of two workgroups per CU
+  constexpr int kTile = 16, kT4 = kTile / 4, kStage = 3, kRing = sizeof(T) == 4 ? 2 : 4;
+  constexpr int kRow = kBlockCh + 2;  // column length in float4s (the forward's padding)
+  static_assert(kWsProd * 64 == kBlockCh * kT4, "one producer lane per (row, column)");
+  static_assert(2 * kWsCons * kTile == 64 * kWsProd, "one C element per producer lane");
+  __shared__ float4 sSt[kStage][2][kT4][kRow];   // [delta | effective dout][column][row]
+  __shared__ float4 sC[kStage][kWsCons][kTile / 2];  // (C_2w, C_2w+1) of steps 2i, 2i+1
+
+  const int lane = threadIdx.x & 63;
+  const int w = wave_id_uniform();
+  const int b = blockIdx.y;
+  const int d0 = blockIdx.x * kBlockCh;
+  const int L = p.seqlen, Dm = p.dim, N = p.nstate;
+  int Tbeg, Lend;
+  sub_range(p, (int)blockIdx.z + p.sub_k, Tbeg, Lend);
+  const int ntiles = max(0, (Lend - Tbeg + kTile - 1) / kTile);
+  const size_t sb = (size_t)blockIdx.z * p.batch + b;  // summary row
+  // tile i of the walk starts at step tile_t(i): the last tile first
+  auto tile_t = [&](int i) { return Tbeg + (ntiles - 1 - i) * kTile; };
+  // as many barriers on both sides: 1 + 4 * ceil(ntiles / 4)
+  const int nbar = 1 + 4 * ((ntiles + 3) / 4);
+
+  if (w < kWsCons) {
+    // ------------------------------------------------ consumer: the reverse recurrence
+    const int ch = d0 + lane;
+    const bool ch_ok = ch < Dm;
+    float gam[2] = {0.0f, 0.0f}, A2[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int n = 2 * w + s;
+      A2[s] = (ch_ok && n < N) ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
+    }
+    // block k: delta and dout of steps 4k .. 4k+3, and (C0, C1) of those
+    // steps as two float4s (the same address in every lane: broadcast reads)
+    float4 dlb[2], dob[2], cb[2][2];
+    auto read_block = [&](int buf, int k, float4& dl4, float4& do4, float4 (&c)[2]) {
+      const float4* __restrict__ st = &sSt[buf][0][0][lane];
+      dl4 = st[k * kRow];
+      do4 = st[(kT4 + k) * kRow];
+      c[0] = sC[buf][w][2 * k];
+      c[1] = sC[buf][w][2 * k + 1];
+    };
+    int buf = 0;
+    for (int i = 0; i < nbar; ++i) {
+      __syncthreads();
+      if (i >= ntiles) continue;
+      if (i == 0) read_block(0, kT4 - 1, dlb[0], dob[0], cb[0]);
+      const int nbuf = buf == kStage - 1 ? 0 : buf + 1;
+      // block k - 1's LDS reads are issued before block k is computed; after
+      // block 0, the next tile's last block (staged one iteration ago)
+#pragma unroll
+      for (int kk = 0; kk < kT4; ++kk) {
+        const int c = kk & 1;
+        if (kk + 1 < kT4) read_block(buf, kT4 - 2 - kk, dlb[c ^ 1], dob[c ^ 1], cb[c ^ 1]);
+        else read_block(nbuf, kT4 - 1, dlb[c ^ 1], dob[c ^ 1], cb[c ^ 1]);
+        const float dlv[4] = {dlb[c].x, dlb[c].y, dlb[c].z, dlb[c].w};
+        const float dov[4] = {dob[c].x, dob[c].y, dob[c].z, dob[c].w};
+        const float c0[4] = {cb[c][0].x, cb[c][0].z, cb[c][1].x, cb[c][1].z};
+        const float c1[4] = {cb[c][0].y, cb[c][0].w, cb[c][1].y, cb[c][1].w};
+#pragma unroll
+        for (int j = 3; j >= 0; --j) {
+          gam[0] = fast_exp2(dlv[j] * A2[0]) * fmaf(dov[j], c0[j], gam[0]);
+          gam[1] = fast_exp2(dlv[j] * A2[1]) * fmaf(dov[j], c1[j], gam[1]);
+        }
+      }
+      static_assert(kT4 % 2 == 0, "the last block of every tile in register set 0");
+      buf = nbuf;
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int n = 2 * w + s;
+      if (ch_ok && n < N) seg_g[(sb * N + n) * Dm + ch] = gam[s];
+    }
+    return;
+  }
+
+  // ------------------------------------------------ producer: staging and step sums
+  const int pt = (w - kWsCons) * 64 + lane;
+  const int row = pt / kT4;
+  const int q = pt % kT4;
+  const int pch = d0 + row;
+  const bool pch_ok = pch < Dm;
+  const float Bias = (pch_ok && biasp) ? biasp[pch] : 0.0f;
+  const int chc = min(pch, Dm - 1);
+  const size_t rb = (size_t)b * Dm;
+  int vlo, vhi;
+  valid_window(length, p.pad_right, b, L, vlo, vhi);
+  vlo = max(vlo, Tbeg);  // steps outside the sub-segment are identity steps
+  vhi = min(vhi, Lend);
+  const bool softplus = p.softplus != 0;
+  // C staging: producer lane pt -> (state 2G + half, step) of a tile
+  const int c_half = pt / (kWsCons * kTile);
+  const int c_G = (pt / kTile) % kWsCons;
+  const int c_step = pt % kTile;
+  const int c_n = 2 * c_G + c_half;
+  const bool c_ok = c_n < N;
+  const size_t c_row = (size_t)b * p.bc_bstride + (size_t)min(c_n, N - 1) * L;
+  // aligned rows: buffer ranges over the wave's 16 channel rows (the launch
+  // keeps 16 * L * sizeof(T) below 2^31) and over the batch row's C rows
+  const int wrow0 = d0 + (w - kWsCons) * (kBlockCh / kWsProd);
+  const uint32_t wbytes =
+      (uint32_t)(max(0, min(kBlockCh / kWsProd, Dm - wrow0)) * (size_t)L * sizeof(T));
+  const uint32_t row_off = (uint32_t)((row % (kBlockCh / kWsProd)) * (size_t)L * sizeof(T));
+  const auto d_ld = raw_rsrc(const_cast<T*>(dl) + (rb + wrow0) * L, wbytes);
+  const auto y_ld = raw_rsrc(const_cast<T*>(dyp) + (rb + wrow0) * L, wbytes);
+  const auto z_ld = raw_rsrc(kHasZ ? const_cast<T*>(zp) + (rb + wrow0) * L : const_cast<T*>(dyp),
+                             kHasZ ? wbytes : 0u);
+  const auto C_ld = raw_rsrc(const_cast<T*>(Cp) + (size_t)b * p.bc_bstride,
+                             (uint32_t)((size_t)N * L * sizeof(T)));
+  const uint32_t c_row_off = (uint32_t)((size_t)min(c_n, N - 1) * L * sizeof(T));
+  const T* __restrict__ d_row = dl + (rb + chc) * L;
+  const T* __restrict__ y_row = dyp + (rb + chc) * L;
+  const T* __restrict__ z_row = kHasZ ? zp + (rb + chc) * L : y_row;
+
+  struct Rows {
+    typename Raw4<T>::type d, y, z;
+    uint32_t C;
+  };
+  // raw loads of tile i, the step clamped into the row (tiles past the walk
+  // load data that is never used)
+  auto issue = [&](Rows& r, int i) {
+    const int t0 = max(tile_t(i), 0);
+    if constexpr (kAligned) {
+      const uint32_t off = row_off + (uint32_t)min(t0 + 4 * q, L - 4) * sizeof(T);
+      r.d = buffer_load_raw4<T>(d_ld, off);
+      r.y = buffer_load_raw4<T>(y_ld, off);
+      if constexpr (kHasZ) r.z = buffer_load_raw4<T>(z_ld, off);
+      else r.z = typename Raw4<T>::type{};
+      r.C = buffer_load_bits1<T>(C_ld, c_row_off + (uint32_t)min(t0 + c_step, L - 1) * sizeof(T));
+    } else {
+      r.d = load_raw4_nb<T, kAligned>(d_row, t0 + 4 * q, L, pch_ok);
+      r.y = load_raw4_nb<T, kAligned>(y_row, t0 + 4 * q, L, pch_ok);
+      if constexpr (kHasZ) r.z = load_raw4_nb<T, kAligned>(z_row, t0 + 4 * q, L, pch_ok);
+      else r.z = typename Raw4<T>::type{};
+      r.C = elem_bits(Cp[c_row + min(t0 + c_step, L - 1)]);
+    }
+  };
+  float dtsum = 0.0f;
+  auto stage = [&](const Rows& r, int i, int sbuf) {
+    const int t = tile_t(i) + 4 * q;
+    float dv[4], yv[4], zv[4], de[4], dov[4];
+    decode4(r.d, dv);
+    decode4(r.y, yv);
+    if constexpr (kHasZ) decode4(r.z, zv);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool valid = t + j >= vlo && t + j < vhi;
+      const float x = dv[j] + Bias;
+      const float dt = softplus ? softplus_t20(x) : x;
+      de[j] = valid ? dt : 0.0f;
+      const float dym = valid ? yv[j] : 0.0f;
+      if constexpr (kHasZ) dov[j] = dym * (zv[j] * sigmoidf_fast(zv[j]));
+      else dov[j] = dym;
+      dtsum += de[j];
+    }
+    sSt[sbuf][0][q][row] = make_float4(de[0], de[1], de[2], de[3]);
+    sSt[sbuf][1][q][row] = make_float4(dov[0], dov[1], dov[2], dov[3]);
+    reinterpret_cast<float*>(&sC[sbuf][c_G][0])[2 * c_step + c_half] =
+        c_ok ? bits_to_f32<T>(r.C) : 0.0f;
+  };
+
+  // Iteration i after barrier i stages tile i + 2 into buffer (i + 2) % 3
+  // (last read during iteration i - 1); raw rows travel in a ring of kRing
+  // tiles, loaded kRing iterations ahead of their staging.  Iterations run
+  // in unrolled groups of four with no conditions around the memory
+  // operations (work past the last tile is harmless: clamped loads, unread
+  // buffers, masked sums).
+  Rows rows[kRing];
+#pragma unroll
+  for (int k = 0; k < kRing; ++k) issue(rows[k], k);
+  stage(rows[0], 0, 0);
+  issue(rows[0], kRing);
+  stage(rows[1 % kRing], 1, 1);
+  issue(rows[1 % kRing], kRing + 1);
+  __syncthreads();  // iteration 0
+  stage(rows[2 % kRing], 2, 2);
+  issue(rows[2 % kRing], kRing + 2);
+  int sbuf = 0;  // staging buffer of tile i + 2
+  for (int i0 = 1; i0 < nbar; i0 += 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j;  // (i + 2) % kRing == (j + 3) % kRing (kRing divides 4)
+      __syncthreads();
+      stage(rows[(j + 3) % kRing], i + 2, sbuf);
+      issue(rows[(j + 3) % kRing], i + 2 + kRing);
+      sbuf = sbuf == kStage - 1 ? 0 : sbuf + 1;
+    }
+  }
+  // the four lanes of a channel row are 4 consecutive lanes (q = lane % 4)
+#pragma unroll
+  for (int m = 1; m < kT4; m <<= 1) dtsum += __shfl_xor(dtsum, m, 64);
+  if (q == 0 && pch_ok) seg_dt[sb * Dm + pch] = dtsum;
+}
+
 // Adds the partial sums: dB/dC over channel blocks, dA/dD/dbias over the
 // (segment, batch row) rows, each in a fixed order.  kVec: dB/dC four
 // consecutive elements per thread (128-bit partial loads, 4-element stores;
@@ -1416,21 +1634,35 @@ hipError_t launch_bc_prep(const ScanParams& p, int dtype, float* bc, hipStream_t
 template <typename T, int kSG, bool kHasZ, bool kAligned, bool kPart>
 static hipError_t launch_bwd4(const ScanParams& p, const float* bc, hipStream_t st) {
   const int nsc = kPart ? p.nsc : 1;
+  // the role-split kernels' buffer ranges must fit 2^31 bytes: a wave's 16
+  // channel rows, all of the dB/dC partials, and a batch row's saved states
+  const bool ws =
+      kSG == 1 && !kPart && (size_t)(kBlockCh / kWsProd) * p.seqlen * sizeof(T) < (1u << 31) &&
+      2 * (size_t)p.nblk * p.batch * p.nstate * bc_part_len(p.seqlen) * sizeof(float) < (1u << 31) &&
+      (size_t)p.nchunks * p.nstate * p.hs * p.dim * sizeof(float) < (1u << 31);
   if (p.nseg > 1) {
     ProfScope prof("scan_bwd_segsum", st);
-    hipLaunchKernelGGL((scan_bwd_segsum_kernel<T, kSG, kHasZ, kAligned>),
-                       dim3(p.nblk, p.batch, (p.nseg - 1) * nsc), dim3(kThreads), 0, st,
-                       dims_of(p), (const T*)p.delta, (const T*)p.dout, (const T*)p.z, p.A, bc,
-                       p.bias, p.length, p.seg_h, p.seg_dt);
+    // the role-split summaries per sub-segment (p.sub_k per segment), the
+    // general ones per segment
+    if (ws) {
+      hipLaunchKernelGGL((scan_bwd_segsum_ws_kernel<T, kHasZ, kAligned>),
+                         dim3(p.nblk, p.batch, (p.nseg - 1) * p.sub_k), dim3(kWsThreads), 0, st,
+                         dims_of(p), (const T*)p.delta, (const T*)p.dout, (const T*)p.z, p.A,
+                         (const T*)p.C, p.bias, p.length, p.seg_h, p.seg_dt);
+    } else {
+      // only these summaries read the prepped B/C layout
+      hipError_t e = launch_bc_prep(p, sizeof(T) == 2 ? 1 : 0, const_cast<float*>(bc), st);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((scan_bwd_segsum_kernel<T, kSG, kHasZ, kAligned>),
+                         dim3(p.nblk, p.batch, (p.nseg - 1) * nsc), dim3(kThreads), 0, st,
+                         dims_of(p), (const T*)p.delta, (const T*)p.dout, (const T*)p.z, p.A, bc,
+                         p.bias, p.length, p.seg_h, p.seg_dt);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   dim3 grid(p.nblk, p.batch, p.nseg * nsc);
-  // the role-split kernel's buffer ranges must fit 2^31 bytes: a wave's 16
-  // output rows, all of the dB/dC partials, and a batch row's saved states
-  if (kSG == 1 && !kPart && (size_t)(kBlockCh / kWsProd) * p.seqlen * sizeof(T) < (1u << 31) &&
-      2 * (size_t)p.nblk * p.batch * p.nstate * bc_part_len(p.seqlen) * sizeof(float) < (1u << 31) &&
-      (size_t)p.nchunks * p.nstate * p.hs * p.dim * sizeof(float) < (1u << 31)) {
+  if (ws) {
     ProfScope prof("scan_bwd", st);
     hipLaunchKernelGGL((scan_bwd_ws_kernel<T, kHasZ, kAligned>), grid, dim3(kWsThreads), 0, st,
                        dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, (const T*)p.B,
@@ -1500,10 +1732,6 @@ static hipError_t launch_bwd2(const ScanParams& p, const float* bc, bool aligned
 // nstate <= 256 (past 64: p.nsc chunks with p.ws_gb / p.ws_gd).
 hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* bc,
                            hipStream_t st) {
-  if (p.nseg > 1) {  // only the segment summaries read the prepped layout
-    hipError_t e = launch_bc_prep(p, dtype, bc, st);
-    if (e != hipSuccess) return e;
-  }
   if (dtype == 1) return launch_bwd2<__hip_bfloat16>(p, bc, aligned, st);
   return launch_bwd2<float>(p, bc, aligned, st);
 }

@@ -174,12 +174,9 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       const bool ok = ch_ok && n < N;
       A2[g][s] = ok ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
       float hv = (ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
-      // carry in through the earlier sub-segments' affine maps, in order
-      for (int sp = 0; ok && sp < seg * p.sub_k; ++sp) {
-        const size_t sb = (size_t)sp * p.batch + b;
-        const float decay = fast_exp2(A2[g][s] * seg_dt[sb * Dm + ch]);
-        hv = fmaf(decay, hv, seg_h[(sb * N + n) * Dm + ch]);
-      }
+      // carry in through the earlier summaries' affine maps, in order
+      if (ok)
+        hv = fold_carry(hv, A2[g][s], seg_dt, seg_h, 0, 1, seg * p.sub_k, p.batch, b, Dm, N, n, ch);
       h[g][s] = hv;
     }
 
@@ -532,7 +529,9 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
 //   producer waves 8..11  lane -> (channel row, 4-step column): stage tile
 //                         i+2 (softplus, delta*u, B and C) and finish tile i-1
 //                         (the eight slices added in a fixed order, D*u, the z
-//                         gate, the stores).
+//                         gate, the stores; on the aligned path the outputs of
+//                         four tiles are gathered in LDS and stored as whole
+//                         64-step row pieces).
 // Both roles run at the same time with one barrier per tile, so the
 // producers' transcendental, conversion and store work fills the issue slots
 // the recurrence leaves (a SIMD runs two consumer waves and one producer
@@ -597,6 +596,12 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   __shared__ float4 sSt[kWsStage][2][kT4][kWsRow];
   __shared__ float4 sBC[kWsStage][kWsCons][kWsTile];       // (B0, C0, B1, C1) per pair and step
   __shared__ float4 sY[2][kWsCons][kT4][kWsRow];           // per-wave partial sums of C*h
+  // aligned rows: each producer wave's outputs of four tiles (its 16 rows x
+  // 64 steps: one 128-byte line per row in bf16, two in fp32), as pieces of
+  // 4 steps, [stream][row][tile][column], rows padded by 8 bytes
+  using Piece = typename Raw4<T>::type;
+  constexpr int kOutRowW = 16 * (int)sizeof(Piece) / 4 + 2;  // 32-bit words per padded row
+  __shared__ uint32_t sOut[kAligned && !kSum ? kWsProd : 1][2][16 * kOutRowW];
 
   const int lane = threadIdx.x & 63;
   const int w = wave_id_uniform();
@@ -604,10 +609,16 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   const int d0 = blockIdx.x * kBlockCh;
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
   const int seg = blockIdx.z;
-  const int span = kSum ? p.seg_len / p.sub_k : p.seg_len;  // a multiple of 2 kWsTile
-  const int Tbeg = seg * span;
-  const int Lend = min(L, Tbeg + span);
-  const int ntiles = (Lend - Tbeg + kWsTile - 1) / kWsTile;
+  // steps [Tbeg, Lend): segment seg, or with kSum summary part seg (whole
+  // 32-step tiles, so pairs of 16-step tiles, up to the sequence end)
+  int Tbeg, Lend;
+  if constexpr (kSum) {
+    sub_range(p, seg, Tbeg, Lend);
+  } else {
+    Tbeg = seg * p.seg_len;
+    Lend = min(L, Tbeg + p.seg_len);
+  }
+  const int ntiles = max(0, (Lend - Tbeg + kWsTile - 1) / kWsTile);
   const size_t rb = (size_t)b * Dm;
   const size_t sb = (size_t)seg * p.batch + b;  // summary row (kSum)
 
@@ -622,12 +633,9 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       const bool ok = ch_ok && n < N;
       A2[s] = ok ? Ap[(size_t)ch * N + n] * kLog2e : 0.0f;
       float hv = (!kSum && ok && h_init) ? h_init[(rb + ch) * N + n] : 0.0f;
-      // carry in through the earlier sub-segments' affine maps, in order
-      for (int sp = 0; !kSum && ok && sp < seg * p.sub_k; ++sp) {
-        const size_t spb = (size_t)sp * p.batch + b;
-        const float decay = fast_exp2(A2[s] * seg_dt[spb * Dm + ch]);
-        hv = fmaf(decay, hv, seg_h[(spb * N + n) * Dm + ch]);
-      }
+      // carry in through the earlier summaries' affine maps, in order
+      if (!kSum && ok)
+        hv = fold_carry(hv, A2[s], seg_dt, seg_h, 0, 1, seg * p.sub_k, p.batch, b, Dm, N, n, ch);
       h[s] = hv;
     }
     const bool save = !kSum && h_chunks != nullptr;
@@ -858,6 +866,63 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     }
   };
 
+  // Aligned rows: the outputs of four consecutive tiles go to the wave's
+  // LDS rows and are stored together, 16 bytes per lane and access, after
+  // the fourth: each 64-step row piece is then written whole by back-to-back
+  // stores (piece by piece, a line was completed over four tiles, and lines
+  // evicted from L2 in between were written back more than once).
+  const int prow = row % 16;  // this lane's row within the wave's 16
+  const int pw = kAligned ? max(w - kWsCons, 0) : 0;
+  uint32_t* const so_out = &sOut[pw][0][0];
+  uint32_t* const so_yu = &sOut[pw][1][0];
+  auto put_piece = [&](uint32_t* dst, const float (&y)[4]) {
+    if constexpr (sizeof(T) == 2) {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+    } else {
+      // rows are 8-byte aligned only (padding), so two 8-byte writes
+      reinterpret_cast<uint2*>(dst)[0] = make_uint2(__float_as_uint(y[0]), __float_as_uint(y[1]));
+      reinterpret_cast<uint2*>(dst)[1] = make_uint2(__float_as_uint(y[2]), __float_as_uint(y[3]));
+    }
+  };
+  auto finish_lds = [&](int i, const float4 (&v)[kWsCons], const float (&sk)[4],
+                        const float (&gt)[4], int j) {
+    float4 acc = v[0];
+#pragma unroll
+    for (int ww = 1; ww < kWsCons; ++ww) {
+      acc.x += v[ww].x; acc.y += v[ww].y; acc.z += v[ww].z; acc.w += v[ww].w;
+    }
+    float y[4] = {sk[0] + acc.x, sk[1] + acc.y, sk[2] + acc.z, sk[3] + acc.w};
+    const int slot = prow * kOutRowW + (4 * j + q) * (int)(sizeof(Piece) / 4);
+    if constexpr (kSaveY) put_piece(so_yu + slot, y);
+    if constexpr (kHasZ) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) y[k] *= gt[k];
+    }
+    put_piece(so_out + slot, y);
+  };
+  // tiles i - 3 .. i: the wave's 16 rows x 64 steps as 16-byte chunks, lane
+  // l storing chunks l, l + 64, ...
+  auto flush = [&](int i) {
+    constexpr int kChunksRow = 64 * (int)sizeof(T) / 16;
+    const int tl = Tbeg + (i - 3) * kWsTile;
+#pragma unroll
+    for (int m = 0; m < kChunksRow / 4; ++m) {
+      const int c = lane + 64 * m;
+      const int r = c / kChunksRow, pc = c % kChunksRow;
+      const int t = tl + pc * (16 / (int)sizeof(T));
+      const uint32_t off = t < Lend ? (uint32_t)((r * (size_t)L + t) * sizeof(T)) : kOffDrop;
+      const int sw = r * kOutRowW + 4 * pc;
+      const uint2* so = reinterpret_cast<const uint2*>(so_out + sw);
+      const u32x4_v xo = {so[0].x, so[0].y, so[1].x, so[1].y};
+      if constexpr (kSaveY) {
+        const uint2* sy = reinterpret_cast<const uint2*>(so_yu + sw);
+        const u32x4_v xy = {sy[0].x, sy[0].y, sy[1].x, sy[1].y};
+        __builtin_amdgcn_raw_buffer_store_b128(xy, yu_rsrc, (int)off, 0, 0);
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(xo, out_rsrc, (int)off, 0, 0);
+    }
+  };
+
   // Iteration i after barrier i: read tile i-1's slices (written during
   // iteration i-1), stage tile i+2 into buffer (i+2) % 3 (last read during
   // iteration i-1), finish tile i-1.  Raw rows travel in a ring of kWsRing
@@ -893,7 +958,14 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       // i0 % 4 == 1, so tile i + 2 has the parity of j + 3
       stage(rows[(j + 3) % kWsRing], i + 2, sbuf, sk[(j + 3) & 3], gt[(j + 3) & 3], (j + 3) & 1);
       issue(rows[(j + 3) % kWsRing], i + 2 + kWsRing);
-      if constexpr (!kSum) finish(i - 1, v, sk[j], gt[j]);
+      if constexpr (!kSum) {
+        if constexpr (kAligned) {
+          finish_lds(i - 1, v, sk[j], gt[j], j);
+          if (j == 3) flush(i - 1);
+        } else {
+          finish(i - 1, v, sk[j], gt[j]);
+        }
+      }
       sbuf = sbuf == kWsStage - 1 ? 0 : sbuf + 1;
     }
   }
@@ -938,11 +1010,10 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_segsum_kernel(
   const int w = wave_id_uniform();
   const int b = blockIdx.y;
   const int d0 = blockIdx.x * kBlockCh;
-  const int seg = blockIdx.z;  // sub-segment index
+  const int seg = blockIdx.z;  // summary part
   const int L = p.seqlen, Dm = p.dim, N = p.nstate;
-  const int sub_len = p.seg_len / p.sub_k;
-  const int Tbeg = seg * sub_len;
-  const int Lend = min(L, Tbeg + sub_len);
+  int Tbeg, Lend;
+  sub_range(p, seg, Tbeg, Lend);
   const int npair = bc_pairs(N);
   const int Lp = bc_row_len(L);
   const size_t rb = (size_t)b * Dm;
@@ -1243,21 +1314,28 @@ void fwd_segments(int batch, int nblk, int seqlen, int& nseg, int& seg_len) {
   nseg = (seqlen + seg_len - 1) / seg_len;
 }
 
-// Forward summaries per segment: the summaries cover segments 0 .. nseg - 2
-// only, so with few segments they may leave CUs idle; each segment's summary
-// is split into 1, 2 or 4 sub-segments (each a whole number of 32-step
-// tiles): as many as keep to one workgroup per CU, and twice that where it still
-// leaves CUs idle and the sub-segments stay at least kMinSub steps long (a
-// summary workgroup holds at most 37 KB of LDS, so a CU runs two; shorter
-// sub-segments cost more in pipeline start-up than the extra workgroups gain).
+// Summary parts per segment (the forward's cover segments 0 .. nseg - 2, the
+// backward's 1 .. nseg - 1; sub_span steps each, sub_range).  The summary
+// kernels are VALU-bound and a CU holds two of their workgroups, so with k
+// parts the busiest CU runs about ceil(workgroups / CUs) of them one after
+// the other, each sub_span steps plus a pipeline start-up of about kStartup
+// steps (the loads of the first tiles): k = 1 .. 8 is picked for the least
+// such cost, the smaller k on a tie.
 int fwd_summary_split(int batch, int nblk, int nseg, int seg_len) {
-  constexpr int kTargetWG = 256, kMinSub = 512;
+  constexpr long kCUs = 256;
+  constexpr int kStartup = 64, kMaxK = 8;
   if (nseg <= 1) return 1;
   const long wg = (long)(nseg - 1) * batch * nblk;
-  int k = 1;
-  while (k < 4 && wg * 2 * k <= kTargetWG) k *= 2;
-  if (k < 4 && wg * k < kTargetWG && seg_len / (2 * k) >= kMinSub) k *= 2;
-  return k;
+  int best = 1;
+  long best_cost = (wg + kCUs - 1) / kCUs * (seg_len + kStartup);
+  for (int k = 2; k <= kMaxK; ++k) {
+    const long cost = (wg * k + kCUs - 1) / kCUs * (sub_span(seg_len, k) + kStartup);
+    if (cost < best_cost) {
+      best = k;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 size_t fwd_seg_floats(int batch, int dim, int nstate, int seqlen) {

@@ -84,6 +84,33 @@ template <> struct Elem<__hip_bfloat16> {
 
 // 2^x on the transcendental unit (v_exp_f32).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The carry through a run of segment summaries for one (batch row b, channel
+// ch, state n): x <- exp2(A2 dt_k) x + g_k for k = k_first, k_first + step,
+// ... (count terms), with dt_k = dtp[(k * batch + b) * Dm + ch] and g_k =
+// gp[((k * batch + b) * N + n) * Dm + ch].  The loads are issued eight at a
+// time ahead of their multiply-adds, so a long run waits for memory once per
+// eight terms instead of once per term; the arithmetic and its order are
+// those of the plain loop.
+__device__ __forceinline__ float fold_carry(float x, float A2, const float* __restrict__ dtp,
+                                            const float* __restrict__ gp, int k_first, int step,
+                                            int count, int batch, int b, int Dm, int N, int n,
+                                            int ch) {
+  for (int c0 = 0; c0 < count; c0 += 8) {
+    float dt[8], g[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = min(c0 + u, count - 1);
+      const size_t kb = (size_t)(k_first + step * c) * batch + b;
+      dt[u] = dtp[kb * Dm + ch];
+      g[u] = gp[(kb * N + n) * Dm + ch];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (c0 + u < count) x = fmaf(fast_exp2(A2 * dt[u]), x, g[u]);
+  }
+  return x;
+}
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 

@@ -38,10 +38,35 @@ struct ScanDims {
   int softplus;
   int seg_len;  // steps per sequence segment (a multiple of the forward super-tile)
   int nseg;     // segments (1: the whole row in one workgroup)
-  int sub_k;    // forward summaries per segment (sub-segments of seg_len / sub_k steps)
+  int sub_k;    // summaries per segment (sub-segments of sub_span(seg_len, sub_k) steps)
   int64_t bc_bstride;  // elements between batch rows of B and of C (rows of a batch are seqlen apart)
   int hs;              // h_chunks state-slot stride in rows of dim (1: states only; 2: (prod a, h) pairs)
 };
+
+// Sub-segments of the segment summaries: segment s is cut into sub_k parts
+// of sub_span steps (a multiple of the 32-step summary tile), the last part
+// ending at the segment's end (shorter, or empty when the others already
+// cover the segment).
+#if defined(__HIPCC__)
+__host__ __device__
+#endif
+inline int sub_span(int seg_len, int sub_k) {
+  return ((seg_len + sub_k - 1) / sub_k + kTileF - 1) / kTileF * kTileF;
+}
+
+// Steps [t0, t1) of summary z = s * sub_k + j (part j of segment s); t1 <= t0
+// for an empty part.
+#if defined(__HIPCC__)
+__host__ __device__
+#endif
+inline void sub_range(const ScanDims& p, int z, int& t0, int& t1) {
+  const int s = z / p.sub_k, j = z % p.sub_k;
+  const int span = sub_span(p.seg_len, p.sub_k);
+  const int base = s * p.seg_len;
+  t0 = base + (j * span < p.seg_len ? j * span : p.seg_len);
+  const int e = base + ((j + 1) * span < p.seg_len ? (j + 1) * span : p.seg_len);
+  t1 = e < p.seqlen ? e : p.seqlen;
+}
 
 struct ScanParams {
   int batch, dim, seqlen, nstate, nchunks, nblk;
