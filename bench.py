@@ -200,6 +200,28 @@ def time_decode_flush(su, dev, steps, flush_mb=512):
     x, dt, z = (torch.randn(batch, dim, generator=g).bfloat16().to(dev) for _ in range(3))
     B, C = (torch.randn(batch, nstate, generator=g).bfloat16().to(dev) for _ in range(2))
     out = torch.empty(batch, dim, dtype=torch.bfloat16, device=dev)
+    return time_after_flush(
+        dev, lambda: su.apply_ext(x, A, B, C, D, dt, bias, state, z=z, inplace=True, out=out),
+        steps, flush_mb)
+
+
+def time_copy_flush(dev, nbytes, steps, flush_mb=512):
+    """A plain device-to-device copy of `nbytes` (torch's copy kernel) timed
+    as time_decode_flush times the decode step: the reference for what a
+    kernel that reads and writes that many bytes costs from a flushed cache.
+    Returns microseconds per copy."""
+    import torch
+    src = torch.randn(nbytes // 4, device=dev)
+    dst = torch.empty_like(src)
+    return time_after_flush(dev, lambda: dst.copy_(src), steps, flush_mb)
+
+
+def time_after_flush(dev, fn, steps, flush_mb):
+    """`steps` calls of fn, each after a `flush_mb` MB fill kernel, captured
+    in one HIP graph; a second graph holds the fills alone, and the difference
+    of the two replays is the time of the calls.  Returns microseconds per
+    call."""
+    import torch
     # float32, so the fill is a kernel (a byte pattern could become a memset node)
     junk = torch.empty((flush_mb << 20) // 4, dtype=torch.float32, device=dev)
 
@@ -207,7 +229,7 @@ def time_decode_flush(su, dev, steps, flush_mb=512):
         for k in range(steps):
             junk.fill_(float(k))
             if with_steps:
-                su.apply_ext(x, A, B, C, D, dt, bias, state, z=z, inplace=True, out=out)
+                fn()
 
     side = torch.cuda.Stream(dev)
     side.wait_stream(torch.cuda.current_stream(dev))
@@ -546,6 +568,20 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def time_config3(ss, N, dev, steps=10, warmup=2):
+    """B=1, D=2560, L=16384, N=16, fp32, z, delta_raw
+    shifted by +2; the sequence split (40 channel blocks fill 40 of 256 CUs).
+    summary_share: the two segment-summary kernels' part of the kernel time."""
+    import torch
+    x3 = inputs(1, 2560, 16384, 16, torch.float32, dev, seed=3, delta_shift=2.0)
+    ms3, k3 = time_scan(ss, N, x3, steps, warmup, clock_warmup_ms=50.0)
+    f3, b3 = scan_bytes(1, 2560, 16384, 16, 4)
+    summ = k3.get("scan_fwd_segsum", 0.0) + k3.get("scan_bwd_segsum", 0.0)
+    return {"ms_per_step": round(ms3, 4), "GBs": round((f3 + b3) / (ms3 * 1e-3) / 1e9, 1),
+            "kernels_ms": {k: round(v, 4) for k, v in k3.items()},
+            "summary_share": round(summ / sum(k3.values()), 4)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -563,6 +599,9 @@ def main():
     ap.add_argument("--e2e", action="store_true",
                     help="only config 4 end to end (causal LM prefill + 128 decode steps); "
                          "prints its own JSON line")
+    ap.add_argument("--config3", action="store_true",
+                    help="only config 3 (B=1, D=2560, L=16384, fp32, sequence split) fwd+bwd; "
+                         "prints its own JSON line (for a kernel trace of that config)")
     ap.add_argument("--profile-run", action="store_true",
                     help="for rocprofv3 counter runs: one 256 MiB device-to-device copy (reference for "
                          "the byte counters), config-1 fwd+bwd (--steps times), 32 eager config-2 "
@@ -586,6 +625,9 @@ def main():
     x = inputs(batch, dim, seqlen, nstate, torch.bfloat16, dev, seed=1)
     if args.e2e:
         print(json.dumps({"e2e": time_e2e(dev)}), flush=True)
+        return
+    if args.config3:
+        print(json.dumps({"config3_fwd_bwd": time_config3(ss, N, dev)}), flush=True)
         return
     if args.profile_run:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -650,6 +692,7 @@ def main():
         cold = time_decode(su, dev, 256, cold=True)
         warm = time_decode(su, dev, 256, cold=False)
         flushed = time_decode_flush(su, dev, 256)
+        copy_us = time_copy_flush(dev, 64 * 5120 * 16 * 4, 256)
         res["decode"] = {"config": "B=64 D=5120 N=16, fp32 state, bf16 x/dt/z/B/C, 256 steps "
                                    "replayed from one HIP graph; cold: a 512 MB fill between "
                                    "steps (flush), and 16 rotating states (rotation)",
@@ -658,7 +701,11 @@ def main():
                          "us_per_step_warm": round(warm, 3),
                          "floor_us": round(floor_us, 3),
                          "cold_over_floor": round(flushed / floor_us, 3),
-                         "cold_GBs": round(44_937_216 / (flushed * 1e-6) / 1e9, 1)}
+                         "cold_GBs": round(44_937_216 / (flushed * 1e-6) / 1e9, 1),
+                         # torch's device copy of the state's 21 MB (42 MB moved against
+                         # the step's 45 MB), timed the same way
+                         "copy_state_bytes_us_cold": round(copy_us, 3),
+                         "cold_over_copy": round(flushed / copy_us, 3)}
         res["host_overhead"] = time_host_overhead(dev)
         x0 = inputs(2, 1536, 512, 16, torch.float32, dev, seed=0)
         ms0, k0 = time_scan(ss, N, x0, 20, 3, fwd_only=True, clock_warmup_ms=50.0)
@@ -666,13 +713,7 @@ def main():
         res["config0_fwd"] = {"ms": round(k0["scan_fwd"], 4),
                               "GBs": round(f0 / (k0["scan_fwd"] * 1e-3) / 1e9, 1)}
         del x0
-        x3 = inputs(1, 2560, 16384, 16, torch.float32, dev, seed=3, delta_shift=2.0)
-        ms3, k3 = time_scan(ss, N, x3, 10, 2, clock_warmup_ms=50.0)
-        f3, b3 = scan_bytes(1, 2560, 16384, 16, 4)
-        res["config3_fwd_bwd"] = {"ms_per_step": round(ms3, 4),
-                                  "GBs": round((f3 + b3) / (ms3 * 1e-3) / 1e9, 1),
-                                  "kernels_ms": {k: round(v, 4) for k, v in k3.items()}}
-        del x3
+        res["config3_fwd_bwd"] = time_config3(ss, N, dev)
         try:
             if not args.no_e2e:
                 res["e2e"] = time_e2e(dev)
