@@ -140,6 +140,17 @@ def test_sequence_split_many_segments(cuda, padding_side, lengths, dtype):
              padding_side=padding_side, h_init=True, dlast=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batch,seqlen", [(2, 200), (1, 264)])
+def test_partial_channel_block_aligned(cuda, dtype, batch, seqlen):
+    """The aligned path with the last channel block part-filled (80 channels:
+    the second block has 16 rows, and three of its four producer waves none)
+    and a length that ends inside a 64-step output piece, so the forward's
+    four-tile output staging drops the chunks past the end.  Both shapes
+    run the sequence split (2 and 3 segments of 128 steps)."""
+    run_case(cuda, batch, 80, seqlen, 16, dtype, seed=seqlen + batch, h_init=True, dlast=True)
+
+
 @pytest.mark.parametrize("nstate", [32, 64])
 def test_sequence_split_state_groups(cuda, nstate):
     """More than 16 states take the summaries' multi-group path."""
