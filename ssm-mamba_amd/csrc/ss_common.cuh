@@ -255,14 +255,17 @@ __device__ __forceinline__ float bc_mul(int k, float blk, float x) {
 }
 
 // acc + value k * x as one v_fmac_f32_dpp.  The compiler does not fold a DPP
-// operand into v_fmac on this architecture, hence the inline instruction;
-// its s_nop provides the two wait states a DPP read of blk needs after a
-// VALU write of blk (the compiler does not see the DPP inside the asm).
+// operand into v_fmac on this architecture, hence the inline instruction.
+// A DPP read of blk needs two wait states after a VALU write of blk, which the
+// compiler cannot see inside the asm; blk is a block register read from LDS
+// and never written by a VALU instruction, so none are inserted here (an
+// s_nop per use cost the backward 2%).  tests/test_dpp_hazards.py checks the
+// compiled kernels for any VALU write of a DPP source within two wait states.
 __device__ __forceinline__ float bc_fmac(int k, float acc, float blk, float x) {
   switch (k) {
 #define SSM_BC_FMAC(n)                                                                         \
   case n:                                                                                     \
-    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:" #n                                \
+    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:" #n                                           \
         " row_mask:0xf bank_mask:0xf bound_ctrl:1"                                             \
         : "+v"(acc)                                                                           \
         : "v"(blk), "v"(x));                                                                  \
