@@ -63,9 +63,13 @@ __device__ __forceinline__ void softplus_and_grad_u(float x, float& sp, float& s
 // with complementary bank masks write one register, the lanes whose bit is
 // clear adding the pair's first value with their partner's, the others the
 // second (the sums rs_fold forms, in the same operand order up to
-// commutation, so the same bits).  Banks are lane bits 3..2 of a row.  The
-// s_nop gives the two wait states a DPP read needs after a VALU write of its
-// source (the compiler does not see the DPP inside the asm).
+// commutation, so the same bits).  Banks are lane bits 3..2 of a row.  A DPP
+// read needs two wait states after a VALU write of its source, which the
+// compiler does not see inside the asm: fold_ror8's s_nop provides them (its
+// inputs are the products computed just before); fold_half_mirror reads
+// fold_ror8 results of the level before and goes without (an s_nop per fold
+// cost the backward 0.7%).  tests/test_dpp_hazards.py checks the compiled
+// kernels for any DPP source written by VALU within two wait states.
 __device__ __forceinline__ float fold_ror8(float p, float q) {  // bit 3: partner l ^ 8
   float r;
   asm("s_nop 1\n\t"
@@ -77,8 +81,7 @@ __device__ __forceinline__ float fold_ror8(float p, float q) {  // bit 3: partne
 }
 __device__ __forceinline__ float fold_half_mirror(float p, float q) {  // bit 2: partner 7 - l in 8
   float r;
-  asm("s_nop 1\n\t"
-      "v_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+  asm("v_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
       "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0xa"
       : "=&v"(r)
       : "v"(p), "v"(q));
