@@ -65,15 +65,24 @@ __device__ __forceinline__ void softplus_and_grad_u(float x, float& sp, float& s
 // second (the sums rs_fold forms, in the same operand order up to
 // commutation, so the same bits).  Banks are lane bits 3..2 of a row.  A DPP
 // read needs two wait states after a VALU write of its source, which the
-// compiler does not see inside the asm: fold_ror8's s_nop provides them (its
-// inputs are the products computed just before); fold_half_mirror reads
-// fold_ror8 results of the level before and goes without (an s_nop per fold
-// cost the backward 0.7%).  tests/test_dpp_hazards.py checks the compiled
-// kernels for any DPP source written by VALU within two wait states.
+// compiler does not see inside the asm: fold_ror8's s_nop provides them where
+// its inputs may be the products computed just before; fold_ror8_nn, for
+// inputs computed a block's reverse earlier, and fold_half_mirror, which reads
+// fold_ror8 results of the level before, go without (an s_nop per fold cost
+// the backward 1.7%).  tests/test_dpp_hazards.py checks the compiled kernels
+// for any DPP source written by VALU within two wait states.
 __device__ __forceinline__ float fold_ror8(float p, float q) {  // bit 3: partner l ^ 8
   float r;
   asm("s_nop 1\n\t"
       "v_add_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %0, %2, %2 row_ror:8 row_mask:0xf bank_mask:0xc"
+      : "=&v"(r)
+      : "v"(p), "v"(q));
+  return r;
+}
+__device__ __forceinline__ float fold_ror8_nn(float p, float q) {  // fold_ror8 without the s_nop
+  float r;
+  asm("v_add_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
       "v_add_f32_dpp %0, %2, %2 row_ror:8 row_mask:0xf bank_mask:0xc"
       : "=&v"(r)
       : "v"(p), "v"(q));
@@ -105,9 +114,13 @@ __device__ __forceinline__ int reduce32_index(int lane) {
   return ((lane >> 3) & 1) << 4 | ((lane >> 2) & 1) << 3 | ((lane >> 4) & 1) << 2 |
          ((lane >> 5) & 1) << 1 | ((lane >> 1) & 1);
 }
+// kOld: the values were computed well before the call (no fresh VALU
+// results), so the first level's folds go without their s_nop.
+template <bool kOld = false>
 __device__ __forceinline__ void wave_reduce32(float (&v)[32], int lane) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) v[i] = fold_ror8(v[i], v[i + 16]);
+  for (int i = 0; i < 16; ++i)
+    v[i] = kOld ? fold_ror8_nn(v[i], v[i + 16]) : fold_ror8(v[i], v[i + 16]);
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = fold_half_mirror(v[i], v[i + 8]);
 #pragma unroll
@@ -811,8 +824,8 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
         for (int k = 0; k < 16; ++k) vals[16 * half + k] = v16[k];
       };
       // sum over the 64 channels of blocks jq and jq - 1 together
-      auto reduce_store = [&](int jq, float (&vals)[32]) {
-        wave_reduce32(vals, lane);
+      auto reduce_store = [&](int jq, float (&vals)[32], auto old) {
+        wave_reduce32<decltype(old)::value>(vals, lane);
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(vals[0]), bc_rsrc,
                                               (int)(bc_off + 16u * (jq - 1)), t0 * 4, 0);
       };
@@ -832,13 +845,15 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
       // (shared, it is materialised with an extra v_mov_dpp and a register)
 #pragma unroll
       for (int jq = 0; jq < kT4; ++jq) asm volatile("" : "+v"(bcg[jq]));
-      float v32[32];
+      // blocks 3 and 2 are reduced after block 1's reverse, so their terms
+      // are not fresh VALU results at the folds
+      float v32[32], w32[32];
       rev(3, Y, v32, 0);
       ld(2, X, true); rev(2, X, v32, 1);
-      reduce_store(3, v32);
-      ld(1, Y, true); rev(1, Y, v32, 0);
-      ld(0, X, true); rev(0, X, v32, 1);
-      reduce_store(1, v32);
+      ld(1, Y, true); rev(1, Y, w32, 0);
+      reduce_store(3, v32, std::true_type{});
+      ld(0, X, true); rev(0, X, w32, 1);
+      reduce_store(1, w32, std::false_type{});
     };
     // nbar - 1 is a multiple of 4: iteration 0, then pairs of parity 1, 0
     iteration(0, std::integral_constant<int, 0>{});
