@@ -151,6 +151,17 @@ def test_partial_channel_block_aligned(cuda, dtype, batch, seqlen):
     run_case(cuda, batch, 80, seqlen, 16, dtype, seed=seqlen + batch, h_init=True, dlast=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("nstate", [1, 5, 12])
+def test_sequence_split_few_states(cuda, dtype, nstate):
+    """Fewer than 16 states on the role-split path with the sequence split
+    (one channel block: 3 segments of L = 300, summaries in 4 parts of 32
+    steps, the backward's last parts cut at L or empty): consumer waves and C
+    rows past N carry zeros through the summaries and the carries."""
+    run_case(cuda, 1, 64, 300, nstate, dtype, seed=50 + nstate, h_init=True, dlast=True,
+             length=torch.tensor([283]), padding_side="left")
+
+
 @pytest.mark.parametrize("nstate", [32, 64])
 def test_sequence_split_state_groups(cuda, nstate):
     """More than 16 states take the summaries' multi-group path."""
