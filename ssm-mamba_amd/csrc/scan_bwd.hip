@@ -88,6 +88,24 @@ __device__ __forceinline__ float fold_ror8_nn(float p, float q) {  // fold_ror8 
       : "v"(p), "v"(q));
   return r;
 }
+// Four fold_ror8 at once behind one s_nop: the two wait states cover every
+// input of the block.
+__device__ __forceinline__ void fold_ror8_x4(float (&v)[32], int i0) {
+  float r0, r1, r2, r3;
+  asm("s_nop 1\n\t"
+      "v_add_f32_dpp %0, %4, %4 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %0, %5, %5 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %1, %6, %6 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %1, %7, %7 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %2, %8, %8 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %2, %9, %9 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %3, %10, %10 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %3, %11, %11 row_ror:8 row_mask:0xf bank_mask:0xc"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(v[i0]), "v"(v[i0 + 16]), "v"(v[i0 + 1]), "v"(v[i0 + 17]), "v"(v[i0 + 2]),
+        "v"(v[i0 + 18]), "v"(v[i0 + 3]), "v"(v[i0 + 19]));
+  v[i0] = r0; v[i0 + 1] = r1; v[i0 + 2] = r2; v[i0 + 3] = r3;
+}
 __device__ __forceinline__ float fold_half_mirror(float p, float q) {  // bit 2: partner 7 - l in 8
   float r;
   asm("v_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
@@ -115,12 +133,17 @@ __device__ __forceinline__ int reduce32_index(int lane) {
          ((lane >> 5) & 1) << 1 | ((lane >> 1) & 1);
 }
 // kOld: the values were computed well before the call (no fresh VALU
-// results), so the first level's folds go without their s_nop.
+// results), so the first level's folds go without their s_nop; otherwise
+// they run four to an asm block behind one s_nop.
 template <bool kOld = false>
 __device__ __forceinline__ void wave_reduce32(float (&v)[32], int lane) {
+  if constexpr (kOld) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    v[i] = kOld ? fold_ror8_nn(v[i], v[i + 16]) : fold_ror8(v[i], v[i + 16]);
+    for (int i = 0; i < 16; ++i) v[i] = fold_ror8_nn(v[i], v[i + 16]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) fold_ror8_x4(v, i);
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = fold_half_mirror(v[i], v[i + 8]);
 #pragma unroll
