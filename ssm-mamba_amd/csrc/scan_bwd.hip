@@ -871,11 +871,17 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
       // blocks 3 and 2 are reduced after block 1's reverse, so their terms
       // are not fresh VALU results at the folds
       float v32[32], w32[32];
+      // X still holds block 2's delta and delta*u: read its dout only, and
+      // block 1's values a block ahead of their use
+      X.dout = sSt[buf][2][2][lane ^ bws_swz(2)];
+      StepVals Z;
+      ld(1, Z, true);
       rev(3, Y, v32, 0);
-      ld(2, X, true); rev(2, X, v32, 1);
-      ld(1, Y, true); rev(1, Y, w32, 0);
+      rev(2, X, v32, 1);
+      ld(0, Y, true);
+      rev(1, Z, w32, 0);
       reduce_store(3, v32, std::true_type{});
-      ld(0, X, true); rev(0, X, w32, 1);
+      rev(0, Y, w32, 1);
       reduce_store(1, w32, std::false_type{});
     };
     // nbar - 1 is a multiple of 4: iteration 0, then pairs of parity 1, 0
