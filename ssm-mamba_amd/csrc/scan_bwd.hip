@@ -1633,14 +1633,24 @@ __global__ __launch_bounds__(256) void scan_bwd_reduce_kernel(
       const int t = (int)(i % L4) * 4;
       const size_t kind = rr / nrow, r = rr % nrow;
       const float* src = ws_bc + kind * nblk * nBC + r * Lp + t;
-      float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
-      // 4 partial loads in flight per thread (8, 16 and 32 were slower: the
-      // partials of one output lie a channel block's plane apart)
-#pragma unroll 4
-      for (int k = 0; k < nblk; ++k) {
-        const float4 v = *reinterpret_cast<const float4*>(src + (size_t)k * nBC);
-        s4.x += v.x; s4.y += v.y; s4.z += v.z; s4.w += v.w;
+      auto part = [&](int k) { return *reinterpret_cast<const float4*>(src + (size_t)k * nBC); };
+      auto add = [](float4& a, const float4& v) { a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w; };
+      // 4 partial loads in flight per thread (8, 16 and 32 were slower), into
+      // four accumulators (blocks k = 4m + j into a_j, the remainder into a_0)
+      // added pairwise at the end: a term passes through about nblk / 4 + 2
+      // additions instead of nblk, in a fixed order
+      const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 a0 = zero, a1 = zero, a2 = zero, a3 = zero;
+      int k = 0;
+      for (; k + 4 <= nblk; k += 4) {
+        const float4 v0 = part(k), v1 = part(k + 1), v2 = part(k + 2), v3 = part(k + 3);
+        add(a0, v0); add(a1, v1); add(a2, v2); add(a3, v3);
       }
+      for (; k < nblk; ++k) add(a0, part(k));
+      add(a0, a1);
+      add(a2, a3);
+      float4 s4 = a0;
+      add(s4, a2);
       const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
       T* dst = (kind ? dC : dB) + r * L + t;
       if (kVec && t + 4 <= L) {
