@@ -920,7 +920,6 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
   int vlo, vhi;
   valid_window(length, p.pad_right, b, L, vlo, vhi);
   const bool softplus = p.softplus != 0;
-  const uint32_t okm = pch_ok ? 0xffffffffu : 0u;
   // B/C staging: lane pt -> state n = (pt / 16) % 16 and step pt % 16 of B
   // (first element) and of C (second)
   const int bc_n = (pt / kTileB) % (2 * kWsCons);
@@ -1011,30 +1010,48 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
     decode4(r.u, uv);
     decode4(r.d, dv);
     decode4(r.dy, dyv);
-    uint32_t keep[4] = {okm, okm, okm, okm};
-    if (!(t0 >= vlo && t0 + kTileB <= vhi)) {  // tiles wholly inside the window skip this
+    float de[4], du[4], dov[4], dzo[4], dym[4];
+    // (softplus is uniform: a branch, not a select after both forms)
+    if (softplus) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) keep[j] = (pch_ok && t + j >= vlo && t + j < vhi) ? ~0u : 0u;
+      for (int j = 0; j < 4; ++j) softplus_and_grad_u(dv[j] + Bias, de[j], k.sg[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        de[j] = dv[j] + Bias;
+        k.sg[j] = 1.0f;
+      }
     }
-    float de[4], du[4], dov[4], dzo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dym[j] = dyv[j];
+    // Steps outside the valid window are masked on the tiles that hold any (at
+    // most two per row).  Rows past the last channel read zero on the aligned
+    // path (outside the wave's buffer range), so their delta * u and dout, and
+    // every term those feed, are zero unmasked; the pointer path reads the
+    // clamped channel there and masks them on every tile.
+    if (!kAligned || !(t0 >= vlo && t0 + kTileB <= vhi)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t keep = (pch_ok & (t + j >= vlo) & (t + j < vhi)) ? ~0u : 0u;
+        de[j] = __uint_as_float(__float_as_uint(de[j]) & keep);
+        k.sg[j] = __uint_as_float(__float_as_uint(k.sg[j]) & keep);
+        dym[j] = __uint_as_float(__float_as_uint(dym[j]) & keep);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float x = dv[j] + Bias;
-      float sp, g;
-      softplus_and_grad_u(x, sp, g);
-      de[j] = __uint_as_float(__float_as_uint(softplus ? sp : x) & keep[j]);
-      k.sg[j] = __uint_as_float(__float_as_uint(softplus ? g : 1.0f) & keep[j]);
       du[j] = de[j] * uv[j];
-      const float dym = __uint_as_float(__float_as_uint(dyv[j]) & keep[j]);
       if constexpr (kHasZ) {
         float zv[4], yv[4];
         decode4(r.z, zv);
         decode4(r.y, yv);
+        // silu(z) = z s and silu'(z) = s + z s (1 - s), s = sigmoid(z)
         const float sz = sigmoidf_fast(zv[j]);
-        dov[j] = dym * (zv[j] * sz);
-        dzo[j] = dyv[j] * yv[j] * (sz * fmaf(zv[j], 1.0f - sz, 1.0f));  // every position
+        const float zs = zv[j] * sz;
+        dov[j] = dym[j] * zs;
+        dzo[j] = dyv[j] * yv[j] * fmaf(zs, 1.0f - sz, sz);  // every position
       } else {
-        dov[j] = dym;
+        dov[j] = dym[j];
         dzo[j] = 0.0f;
       }
     }
