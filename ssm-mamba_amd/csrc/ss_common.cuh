@@ -114,16 +114,16 @@ __device__ __forceinline__ float fold_carry(float x, float A2, const float* __re
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
-// log1p(e) for 0 <= e <= 1.  w = 1 + e rounds away c = (w - 1) - e; w - 1 is
-// exact (w is in [1, 2]) and so is c, the rounding error of a sum.  Then
-// log1p(e) = log(w) + log(1 - c / w) = log(w) - c / w to within c^2, and
-// -c / w = -c + c e / w: the dropped c e / w is below |c| <= 2^-24 relative
-// to log1p(e) (e / log1p(e) <= 1.45, w >= 1).  So log1p(e) = log(w) - c with
-// one subtraction for the correction: at most 2.1 ulp from log1p over
-// [0, 1] with a correctly rounded log2 (1.7 ulp with the 1 / w factor).
+// log1p(e) for 0 <= e <= 1.  w = 1 + e rounds away c = (w - 1) - e, which is
+// exact (Sterbenz: w - 1 and e are within a factor of two of each other, or
+// w == 1 and c = -e); then log1p(e) = log(w) + log(1 - c / w), and
+// log(1 - c / w) = -c / w to within c^2 / 2, and 1 / w = 2 - w to within
+// (w - 1)^2.  With |c| <= 2^-24 and |c| <= e, both dropped terms stay below
+// 2^-24 relative to log1p(e): no reciprocal and no select are needed.
 __device__ __forceinline__ float log1p_pos(float e) {
   const float w = 1.0f + e;
-  return fmaf(fast_log2(w), kLn2, e - (w - 1.0f));
+  const float c = (w - 1.0f) - e;
+  return fmaf(fast_log2(w), kLn2, -c * (2.0f - w));
 }
 
 // softplus with the reference threshold: x <= 20 ? log1p(exp(x)) : x.
