@@ -547,6 +547,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
 constexpr int kWsTile = 16;   // steps per tile
 constexpr int kWsStage = 3;   // staging buffers (tiles i, i+1 and i+2)
 constexpr int kWsRing = 4;    // producer register ring of raw rows, in tiles
+constexpr int kCacheNT = 2;   // cache-policy bit NT (nontemporal) of a buffer access
 static_assert(kWsTile == kChunk, "a tile is one saved chunk");
 static_assert(kWsProd * 4 == kWsTile, "one producer wave per 4-step column");
 static_assert(2 * kWsCons * kWsTile == 64 * kWsProd, "one B/C value pair per producer lane");
@@ -688,10 +689,11 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       // kT4 is even: the next tile's block 0 sits in buffer 0 again
       static_assert(kT4 % 2 == 0, "block 0 of every tile in register set 0");
       if (save) {
-        // layout (batch, nchunks, nstate, dim): one contiguous 256 B run per state
+        // layout (batch, nchunks, nstate, dim): one contiguous 256 B run per
+        // state; nontemporal, as the backward alone reads the saved states
         const auto hr = raw_rsrc(hc0 + (size_t)i * cstride, (uint32_t)(2 * hsD * sizeof(float)));
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h[0]), hr, (int)hoff0, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h[1]), hr, (int)hoff1, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h[0]), hr, (int)hoff0, 0, kCacheNT);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h[1]), hr, (int)hoff1, 0, kCacheNT);
       }
       buf = nbuf;
     }
@@ -917,7 +919,9 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       if constexpr (kSaveY) {
         const uint2* sy = reinterpret_cast<const uint2*>(so_yu + sw);
         const u32x4_v xy = {sy[0].x, sy[0].y, sy[1].x, sy[1].y};
-        __builtin_amdgcn_raw_buffer_store_b128(xy, yu_rsrc, (int)off, 0, 0);
+        // the ungated output is read only by the backward: a nontemporal
+        // store, which does not push the step's inputs out of the caches
+        __builtin_amdgcn_raw_buffer_store_b128(xy, yu_rsrc, (int)off, 0, kCacheNT);
       }
       __builtin_amdgcn_raw_buffer_store_b128(xo, out_rsrc, (int)off, 0, 0);
     }
