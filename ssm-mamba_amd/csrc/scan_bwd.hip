@@ -697,6 +697,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
 // VGPRs: the producers keep u as loaded and softplus'(x) for a tile's finish
 // and read delta and dout back from the staging buffer before overwriting it.
 constexpr int kBwsRing = 2;  // producer register ring of raw rows, in tiles (a tile takes microseconds)
+constexpr int kCacheNTb = 2;  // cache-policy bit NT (nontemporal) of a buffer access
 
 // LDS slot of column q of channel row r in the role-split backward: r ^
 // bws_swz(q).  The producers' 8-lane groups of a 128-bit access (rows r, r+1
@@ -786,10 +787,12 @@ __global__ __launch_bounds__(kWsThreads) void scan_bwd_ws_kernel(
     // (the loads are unconditional, from slot 0 for tile 0, and the choice is
     // made where the state is used: a load inside a branch is waited for at
     // the branch's end)
+    // (nontemporal loads: each saved state is read once, in whole 256-byte
+    // runs, so it need not displace the input lines that serve several tiles)
     auto saved_state = [&](int tile, float (&r)[2]) {
       const int so = (int)((size_t)max(tile - 1, 0) * hrow * sizeof(float));
-      r[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(h_rsrc, (int)hv0, so, 0));
-      r[1] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(h_rsrc, (int)hv1, so, 0));
+      r[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(h_rsrc, (int)hv0, so, kCacheNTb));
+      r[1] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(h_rsrc, (int)hv1, so, kCacheNTb));
     };
     float hcn[2];
     saved_state(tile_end - 1, hcn);
