@@ -42,8 +42,8 @@ VALU_PEAK_LANE_OPS = 256 * 4 * 16 * 2.4e9
 #   traffic: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB per dispatch, the factors
 #            being what the same counters read for a 256 MiB device copy;
 #   valu:    SQ_INSTS_VALU wave instructions per dispatch (x 64 lanes).
-TRAFFIC_BYTES = {"scan_fwd": (2 * 105_105 + 262_144) * 1024,
-                 "scan_bwd": (2 * 319_409 + 406_739) * 1024}
+TRAFFIC_BYTES = {"scan_fwd": (2 * 104_920 + 262_144) * 1024,
+                 "scan_bwd": (2 * 303_709 + 381_512) * 1024}
 VALU_INSTS = {"scan_fwd": 6.2962e7, "scan_bwd": 1.6993e8}
 COUNTERS_SOURCE = "profiles/scan_decode_hbm_bytes.md, profiles/scan_sq_counters_config1.md"
 
