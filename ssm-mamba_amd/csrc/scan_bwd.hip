@@ -691,9 +691,11 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
 //                         ddelta, the dD and dbias accumulators).
 // One barrier per tile; the staging buffers and the slices alternate between
 // two LDS buffers by tile parity (159,744 bytes in all).  The arithmetic and
-// its order are those of scan_bwd_kernel; the outputs agree bit for bit with
-// that kernel's except where the compiler contracts a multiply and an add
-// differently (the dbias accumulator).  Three waves per SIMD need at most 168
+// its order are those of scan_bwd_kernel, and the outputs agree bit for bit
+// with that kernel's except dbias (the compiler contracts a multiply and an
+// add of its accumulator differently), dB/dC (the channel sums run in another
+// order) and dz (silu'(z) is formed from silu(z) here, s + z s (1 - s), and as
+// s (1 + z (1 - s)) there).  Three waves per SIMD need at most 168
 // VGPRs: the producers keep u as loaded and softplus'(x) for a tile's finish
 // and read delta and dout back from the staging buffer before overwriting it.
 constexpr int kBwsRing = 2;  // producer register ring of raw rows, in tiles (a tile takes microseconds)
