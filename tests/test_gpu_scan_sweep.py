@@ -32,7 +32,7 @@ def _config(seed):
                 dlast=g.random() < 0.5)
 
 
-@pytest.mark.parametrize("seed", range(48))
+@pytest.mark.parametrize("seed", range(200))
 def test_sweep(cuda, seed):
     c = _config(1000 + seed)
     run_case(cuda, c["batch"], c["dim"], c["seqlen"], c["nstate"], c["dtype"], seed=2000 + seed,
