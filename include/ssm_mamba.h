@@ -134,6 +134,42 @@ int ssm_selective_scan_fwd_noalloc(int64_t batch, int64_t dim, int64_t seqlen, i
                                    float* h_chunks, int h_pairs, float* h_last, void* stream);
 
 /*
+ * Selective-scan forward with the step-size projection fused in: the
+ * inference prefill of a Mamba block from its x-projection output to the scan
+ * output, replacing modules/mamba.py:149-171 (the split of ssm_params, the
+ * delta projection delta_proj.weight @ delta.t(), the channel-major copies of
+ * delta, B and C, and SelectiveScanFn's forward).
+ *
+ *   ssm_params (batch, seqlen, P) bf16, P = dt_rank + 2 * nstate: the
+ *              token-major x-projection output (modules/mamba.py:141-145),
+ *              each token's row [dt | B | C]; batch row b starts
+ *              params_batch_stride elements after row b-1 (0: seqlen * P).
+ *   dt_weight  (dim, dt_rank) bf16, delta_proj.weight.
+ *   delta_raw  = dt_weight @ dt^T rounded to bf16 per element (the
+ *              reference's product in the model dtype), then the scan as
+ *              ssm_selective_scan_fwd with delta = delta_raw and B, C read in
+ *              place from ssm_params.  Written to delta_out (nullable;
+ *              (batch, dim, seqlen) bf16) when given.
+ * The other arguments as ssm_selective_scan_fwd; no saved chunk states and no
+ * ungated output (inference).  bf16 only, nstate <= 16 and a multiple of 4,
+ * dt_rank a multiple of 8 and <= 64, ssm_params and dt_weight 16-byte aligned,
+ * params_batch_stride a multiple of 8 (else SSM_ERR_UNSUPPORTED; the caller
+ * then runs the projection and ssm_selective_scan_fwd).  workspace:
+ * ssm_scan_fwd_workspace_bytes() bytes.
+ */
+int ssm_selective_scan_fwd_dt_proj(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate,
+                                   int64_t dt_rank, int dtype, const void* u,
+                                   const void* ssm_params, int64_t params_batch_stride,
+                                   const void* dt_weight, const float* A, const float* D,
+                                   const float* delta_bias, const float* h_init,
+                                   const int64_t* length, int padding_right, const void* z,
+                                   int delta_softplus, void* out, void* delta_out, float* h_last,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+/* 1 when ssm_selective_scan_fwd_dt_proj takes this shape and dtype, else 0. */
+int ssm_selective_scan_fwd_dt_proj_supported(int64_t batch, int64_t dim, int64_t seqlen,
+                                             int64_t nstate, int64_t dt_rank, int dtype);
+
+/*
  * Selective-scan backward.  Replaces selective_scan_backward
  * (csrc/selective_scan/selective_scan.cpp:294-380, declared at
  * csrc/selective_scan/selective_scan.h:86-99) behind selective_scan.backward

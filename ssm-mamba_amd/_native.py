@@ -53,6 +53,15 @@ SIGNATURES = {
         _p, _p, _p, _i32, _p,                  # out, out_ungated, h_chunks, h_pairs, h_last
         _p,                                    # stream
     ]),
+    "ssm_selective_scan_fwd_dt_proj": (_i32, [
+        _i64, _i64, _i64, _i64, _i64, _i32,    # batch, dim, seqlen, nstate, dt_rank, dtype
+        _p, _p, _i64, _p,                      # u, ssm_params, params_batch_stride, dt_weight
+        _p, _p, _p, _p, _p,                    # A, D, delta_bias, h_init, length
+        _i32, _p, _i32,                        # padding_right, z, delta_softplus
+        _p, _p, _p,                            # out, delta_out, h_last
+        _p, _sz, _p,                           # workspace, bytes, stream
+    ]),
+    "ssm_selective_scan_fwd_dt_proj_supported": (_i32, [_i64, _i64, _i64, _i64, _i64, _i32]),
     "ssm_selective_scan_bwd": (_i32, [
         _i64, _i64, _i64, _i64, _i32,
         _p, _p, _p, _p, _p, _i64,              # u, delta, A, B, C, bc_batch_stride
@@ -119,7 +128,7 @@ SIGNATURES = {
     ]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 def lib() -> ctypes.CDLL:

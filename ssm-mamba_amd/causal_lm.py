@@ -16,7 +16,11 @@ Every projection is computed as ``W @ X`` on channel-major ``X`` (one batched
 GEMM with the weight broadcast over the batch), so the reference's per-layer
 permute copies (``modules/mamba.py:104-111,156-163,181``) do not exist here:
 the sequence is transposed once after the embedding and once before the LM
-head.  The z gate is fused into the scan / state-update kernels.
+head.  The z gate is fused into the scan / state-update kernels.  In an
+inference prefill (bf16 on the GPU) the x-projection output is token-major,
+the reference's own layout of ssm_params, and the step-size projection runs
+inside the scan kernels (``ssm_selective_scan_fwd_dt_proj``), which read dt,
+B and C from it in place.
 
 Decode.  ``Mamba.step`` updates the per-layer caches in place (conv window and
 fp32 SSM state), so a whole token step -- all layers, final norm, LM head and
@@ -165,6 +169,7 @@ class Mamba(nn.Module):
         self._ssm_hiddens: Optional[torch.Tensor] = None   # (batch, inner, N) float32
         self._conv_context: Optional[torch.Tensor] = None  # (batch, inner, k-1)
         self._param_cache = None
+        self._xproj_t = None
 
     def _scan_params(self):
         """(A, D, delta_bias) for the scan: A = -exp(log_A) (``modules/mamba.py:166``)
@@ -181,6 +186,65 @@ class Mamba(nn.Module):
                                  self.D.detach().float(),
                                  None if bias is None else bias.detach().float())
         return self._param_cache[1:]
+
+    def _x_proj_t(self) -> torch.Tensor:
+        """W_x^T (inner, R + 2N), contiguous, for the token-major x-projection
+        xc^T W_x^T (the reference's layout of ssm_params, modules/mamba.py:
+        141-145).  Kept until the weight changes, as in _scan_params."""
+        w = self.ssm_param_proj.weight
+        key = (w._version, w.data_ptr(), w.dtype, w.device)
+        if self._xproj_t is None or self._xproj_t[0] != key:
+            self._xproj_t = (key, w.detach().t().contiguous())
+        return self._xproj_t[1]
+
+    def _dt_fusable(self, xc: torch.Tensor, z: torch.Tensor, h0: Optional[torch.Tensor],
+                    lengths: Optional[torch.Tensor]) -> bool:
+        """Whether the x-projection output can go to the scan with the step-size
+        projection fused in (ssm_selective_scan_fwd_dt_proj): inference, bf16
+        on the GPU, and a shape the fused kernel takes."""
+        w_dt = self.delta_proj.weight
+        if torch.is_grad_enabled() or not xc.is_cuda or xc.dtype != torch.bfloat16:
+            return False
+        if w_dt.dtype != torch.bfloat16 or self.ssm_param_proj.weight.dtype != torch.bfloat16:
+            return False
+        if not (xc.is_contiguous() and z.is_contiguous() and w_dt.is_contiguous()
+                and w_dt.data_ptr() % 16 == 0):
+            return False
+        if h0 is not None and tuple(h0.shape) != (xc.shape[0], self.inner_dim, self.state_dim):
+            return False
+        if lengths is not None and lengths.device != xc.device:
+            return False
+        batch, inner, seqlen = xc.shape
+        return bool(_N.lib().ssm_selective_scan_fwd_dt_proj_supported(
+            batch, inner, seqlen, self.state_dim, self.delta_rank, _N.SSM_BF16))
+
+    def _scan_dt_proj(self, xc: torch.Tensor, z: torch.Tensor, h0: Optional[torch.Tensor],
+                      lengths: Optional[torch.Tensor]):
+        """modules/mamba.py:141-171 for inference: the token-major x-projection
+        (one GEMM), then the scan with delta_raw = W_dt dt computed by the scan
+        kernels' producers on the matrix cores and B, C read in place from the
+        projection output (no delta or channel-major B/C tensors).  Returns
+        (out, last state)."""
+        batch, inner, seqlen = xc.shape
+        nstate, rank = self.state_dim, self.delta_rank
+        w_xt = self._x_proj_t()
+        params = torch.bmm(xc.transpose(1, 2), w_xt.expand(batch, *w_xt.shape))  # (batch, L, P)
+        A, D, dt_bias = self._scan_params()
+        h0 = None if h0 is None else h0.detach().float().contiguous()
+        lengths = None if lengths is None else lengths.to(torch.int64).contiguous()
+        out = torch.empty_like(xc)
+        last = torch.empty(batch, inner, nstate, dtype=torch.float32, device=xc.device)
+        lib = _N.lib()
+        ws = torch.empty(lib.ssm_scan_fwd_workspace_bytes(batch, inner, seqlen, nstate),
+                         dtype=torch.uint8, device=xc.device)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        with torch.cuda.device(xc.device):
+            _N.check(lib.ssm_selective_scan_fwd_dt_proj(
+                batch, inner, seqlen, nstate, rank, _N.SSM_BF16, xc.data_ptr(), params.data_ptr(),
+                0, self.delta_proj.weight.data_ptr(), A.data_ptr(), ptr(D), ptr(dt_bias), ptr(h0),
+                ptr(lengths), 0, z.data_ptr(), 1, out.data_ptr(), None, last.data_ptr(),
+                ws.data_ptr(), ws.numel(), torch.cuda.current_stream(xc.device).cuda_stream))
+        return out, last
 
     # ---- caches ---------------------------------------------------------
     def allocate_cache(self, batch: int, device=None, dtype=None) -> None:
@@ -248,17 +312,20 @@ class Mamba(nn.Module):
                               lengths=lengths if use_cache else None)
         if use_cache:
             self._conv_context = window
-        params = _proj_cm(self.ssm_param_proj.weight, xc)           # (batch, R + 2N, L)
-        delta = _proj_cm(self.delta_proj.weight, params[:, :rank])
-        # B and C go to the scan as slices of params (one shared batch stride)
-        Bm = params[:, rank:rank + nstate]
-        Cm = params[:, rank + nstate:]
-        A, D, dt_bias = self._scan_params()
         # padding_side "left" is the reference's default at this call
         # (modules/mamba.py:170-175 passes no padding argument)
-        y, last = selective_scan_fn(xc, delta, A, Bm, Cm, D, z=z, delta_bias=dt_bias,
-                                    return_last_state=True, h_init=ssm_hiddens, length=lengths,
-                                    padding_side="left")
+        if self._dt_fusable(xc, z, ssm_hiddens, lengths):
+            y, last = self._scan_dt_proj(xc, z, ssm_hiddens, lengths)
+        else:
+            params = _proj_cm(self.ssm_param_proj.weight, xc)           # (batch, R + 2N, L)
+            delta = _proj_cm(self.delta_proj.weight, params[:, :rank])
+            # B and C go to the scan as slices of params (one shared batch stride)
+            Bm = params[:, rank:rank + nstate]
+            Cm = params[:, rank + nstate:]
+            A, D, dt_bias = self._scan_params()
+            y, last = selective_scan_fn(xc, delta, A, Bm, Cm, D, z=z, delta_bias=dt_bias,
+                                        return_last_state=True, h_init=ssm_hiddens,
+                                        length=lengths, padding_side="left")
         if use_cache:
             self._ssm_hiddens = self._keep(self._ssm_hiddens, last.detach())
         if residual is not None and self.out_proj.bias is None:

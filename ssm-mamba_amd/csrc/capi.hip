@@ -18,6 +18,8 @@ hipError_t launch_scan_fwd(const ScanParams& p, int dtype, bool aligned, float* 
 hipError_t launch_scan_bwd(const ScanParams& p, int dtype, bool aligned, float* bc, hipStream_t st);
 hipError_t launch_chunk_decay(const ScanParams& p, int dtype, float* pairs, hipStream_t st);
 hipError_t launch_chunk_tail(const ScanParams& p, float* pairs, hipStream_t st);
+bool scan_fwd_dt_supported(const ScanParams& p);
+hipError_t launch_scan_fwd_dt(const ScanParams& p, const DtProj& dt, bool aligned, hipStream_t st);
 hipError_t launch_state_update(const UpdateParams& p, int dtype, bool vecN, hipStream_t st);
 size_t bc_prep_floats(int batch, int nstate, int seqlen);
 size_t bwd_ws_floats(int batch, int dim, int nstate, int seqlen);
@@ -252,7 +254,7 @@ extern "C" {
 
 const char* ssm_last_error(void) { return g_err.c_str(); }
 
-int ssm_abi_version(void) { return 8; }
+int ssm_abi_version(void) { return 9; }
 
 int ssm_profile_begin(void) {
   g_err.clear();
@@ -488,6 +490,94 @@ int ssm_selective_scan_fwd_noalloc(int64_t batch, int64_t dim, int64_t seqlen, i
                                 bc_batch_stride, D, delta_bias, h_init, length, padding_right, z,
                                 delta_softplus, out, out_ungated, h_chunks, h_pairs, h_last, ws,
                                 (size_t)SSM_NOALLOC_SCRATCH_BYTES, stream);
+}
+
+namespace {
+// Shape conditions of ssm_selective_scan_fwd_dt_proj (pointer conditions are
+// checked by the entry point).
+int check_dt_proj(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate, int64_t dt_rank,
+                  int dtype) {
+  if (int e = check_common(batch, dim, seqlen, nstate, dtype, 16)) return e;
+  if (dtype != SSM_BF16)
+    return fail(SSM_ERR_UNSUPPORTED, "the fused step-size projection takes bf16 only");
+  if (dt_rank < 1) return fail(SSM_ERR_INVALID, "dt_rank must be >= 1 (got %lld)", (long long)dt_rank);
+  if (dt_rank % 8 || dt_rank > 32 * ssm::kDtK)
+    return fail(SSM_ERR_UNSUPPORTED, "the fused step-size projection takes dt_rank a multiple of 8 "
+                "and <= %d (got %lld)", 32 * ssm::kDtK, (long long)dt_rank);
+  if (nstate % 4)
+    return fail(SSM_ERR_UNSUPPORTED, "the fused step-size projection takes nstate a multiple of 4 "
+                "(16-byte token rows; got %lld)", (long long)nstate);
+  const int64_t P = dt_rank + 2 * nstate;
+  if (seqlen * P * 2 >= ((int64_t)1 << 31))
+    return fail(SSM_ERR_UNSUPPORTED, "seqlen * (dt_rank + 2 nstate) * 2 bytes must be < 2^31");
+  ssm::ScanParams p{};
+  p.batch = (int)batch;
+  p.dim = (int)dim;
+  p.seqlen = (int)seqlen;
+  p.nstate = (int)nstate;
+  p.hs = 1;
+  if (!ssm::scan_fwd_dt_supported(p))
+    return fail(SSM_ERR_UNSUPPORTED, "the fused step-size projection: shape past the role-split "
+                "kernel's buffer ranges");
+  return SSM_OK;
+}
+}  // namespace
+
+int ssm_selective_scan_fwd_dt_proj_supported(int64_t batch, int64_t dim, int64_t seqlen,
+                                             int64_t nstate, int64_t dt_rank, int dtype) {
+  const std::string keep = g_err;
+  const int ok = check_dt_proj(batch, dim, seqlen, nstate, dt_rank, dtype) == SSM_OK;
+  g_err = keep;
+  return ok;
+}
+
+int ssm_selective_scan_fwd_dt_proj(int64_t batch, int64_t dim, int64_t seqlen, int64_t nstate,
+                                   int64_t dt_rank, int dtype, const void* u,
+                                   const void* ssm_params, int64_t params_batch_stride,
+                                   const void* dt_weight, const float* A, const float* D,
+                                   const float* delta_bias, const float* h_init,
+                                   const int64_t* length, int padding_right, const void* z,
+                                   int delta_softplus, void* out, void* delta_out, float* h_last,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  if (int e = check_dt_proj(batch, dim, seqlen, nstate, dt_rank, dtype)) return e;
+  if (!u || !ssm_params || !dt_weight || !A || !out)
+    return fail(SSM_ERR_INVALID, "u, ssm_params, dt_weight, A and out must be non-NULL");
+  const int64_t P = dt_rank + 2 * nstate;
+  if (params_batch_stride != 0 && params_batch_stride < seqlen * P)
+    return fail(SSM_ERR_INVALID, "params_batch_stride must be 0 (contiguous) or at least seqlen * "
+                "(dt_rank + 2 nstate) (got %lld)", (long long)params_batch_stride);
+  if (!aligned16(ssm_params) || !aligned16(dt_weight) || params_batch_stride % 8)
+    return fail(SSM_ERR_UNSUPPORTED, "the fused step-size projection needs 16-byte aligned "
+                "ssm_params rows and dt_weight");
+  const size_t need = ssm_scan_fwd_workspace_bytes(batch, dim, seqlen, nstate);
+  if (!workspace || workspace_bytes < need)
+    return fail(SSM_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+  ssm::ScanParams p = make_scan_params(batch, dim, seqlen, nstate, u, u, A, ssm_params, ssm_params,
+                                       0, D, delta_bias, h_init, length, padding_right, z,
+                                       delta_softplus);
+  p.out = out;
+  p.hs = 1;
+  p.h_last = h_last;
+  // workspace: [prepped B/C (unused here)][segment states and step sums][dummy]
+  char* ws = static_cast<char*>(workspace) +
+             round256(ssm::bc_prep_floats((int)batch, (int)nstate, (int)seqlen) * sizeof(float));
+  ssm::fwd_segments((int)batch, p.nblk, (int)seqlen, p.nseg, p.seg_len);
+  p.sub_k = ssm::fwd_summary_split((int)batch, p.nblk, p.nseg, p.seg_len);
+  p.seg_h = reinterpret_cast<float*>(ws);
+  p.seg_dt = p.seg_h + (size_t)(p.nseg - 1) * p.sub_k * batch * nstate * dim;
+  ws += round256(ssm::fwd_seg_floats((int)batch, (int)dim, (int)nstate, (int)seqlen) * sizeof(float));
+  p.dummy = ws;
+  ssm::DtProj dt{};
+  dt.params = ssm_params;
+  dt.pstride = params_batch_stride ? params_batch_stride : seqlen * P;
+  dt.P = (int)P;
+  dt.rank = (int)dt_rank;
+  dt.w = dt_weight;
+  dt.delta_out = delta_out;
+  const bool aligned = scan_aligned(dtype, seqlen, {u, z, out});
+  return hip_status(ssm::launch_scan_fwd_dt(p, dt, aligned, static_cast<hipStream_t>(stream)),
+                    "selective_scan forward with the step-size projection launch");
 }
 
 int ssm_selective_state_update(int64_t batch, int64_t dim, int64_t nstate, int dtype,

@@ -549,6 +549,9 @@ constexpr int kWsStage = 3;   // staging buffers (tiles i, i+1 and i+2)
 constexpr int kWsRing = 4;    // producer register ring of raw rows, in tiles
 constexpr int kCacheNT = 2;   // cache-policy bit NT (nontemporal) of a buffer access
 static_assert(kWsTile == kChunk, "a tile is one saved chunk");
+
+typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
 static_assert(kWsProd * 4 == kWsTile, "one producer wave per 4-step column");
 static_assert(2 * kWsCons * kWsTile == 64 * kWsProd, "one B/C value pair per producer lane");
 
@@ -562,10 +565,18 @@ constexpr int kWsRow = kBlockCh + 2;
 
 // One tile's raw loads of a producer lane, kept as loaded bits: converting
 // at the load would make the compiler wait for it right there.
-template <typename T>
+template <typename T, bool kDt = false>
 struct WsRows {
   typename Raw4<T>::type u, d, z;
   uint32_t B, C;  // element bits
+};
+// With the fused step-size projection: the tile's dt^T operand in place of
+// the delta row piece.
+template <typename T>
+struct WsRows<T, true> {
+  typename Raw4<T>::type u, z;
+  uint32_t B, C;
+  u32x4_v pa[kDtK];
 };
 
 
@@ -579,7 +590,10 @@ struct WsRows {
 // combine them as the summary kernel's eight lanes of 32-step tiles do
 // (((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)) over its columns c), so
 // both kernels add the same numbers in the same order.
-template <typename T, int kZ, bool kAligned, bool kSum>
+//
+// kDt: delta_raw from the fused step-size projection (DtProj) instead of dl,
+// and B / C from the token rows of dtp.params instead of Bp / Cp.
+template <typename T, int kZ, bool kAligned, bool kSum, bool kDt = false>
 __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
     const float* __restrict__ Ap, const T* __restrict__ Bp, const T* __restrict__ Cp,
@@ -587,8 +601,9 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     const float* __restrict__ h_init, const int64_t* __restrict__ length,
     const T* __restrict__ zp, T* __restrict__ out, T* __restrict__ yu,
     float* __restrict__ h_chunks, float* __restrict__ h_last, void* __restrict__ dummy,
-    float* __restrict__ seg_h, float* __restrict__ seg_dt) {
+    float* __restrict__ seg_h, float* __restrict__ seg_dt, const DtProj dtp) {
   static_assert(!kSum || kZ == 0, "the summaries read no gate");
+  static_assert(!kDt || sizeof(T) == 2, "the fused projection reads bf16");
   constexpr bool kHasZ = kZ != 0;
   constexpr bool kSaveY = kZ == 2;
   constexpr int kT4 = kWsTile / 4;
@@ -711,8 +726,10 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   // producer lane pt -> channel row pt / 4 and 4-step column q = pt % 4 of
   // every tile: the four lanes of a row read and write 16 consecutive steps
   const int pt = (w - kWsCons) * 64 + lane;
-  const int row = pt / kT4;
-  const int q = pt % kT4;
+  // kDt: the layout of the projection's MFMA result, row lane % 16 of the
+  // wave's 16 and column lane / 16, so each lane holds its own step sizes
+  const int row = kDt ? (w - kWsCons) * (kBlockCh / kWsProd) + (lane & 15) : pt / kT4;
+  const int q = kDt ? lane >> 4 : pt % kT4;
   const int pch = d0 + row;
   const bool pch_ok = pch < Dm;
   const float Dv = (pch_ok && Dp) ? Dp[pch] : 0.0f;
@@ -728,10 +745,12 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   vhi = min(vhi, Lend);  // steps past the segment are identity steps here
   const bool softplus = p.softplus != 0;
   const int last_t0 = Tbeg + (ntiles - 1) * kWsTile;
-  // B/C staging: producer lane pt -> (state 2G + half, step) of a tile
-  const int bc_half = pt / (kWsCons * kWsTile);
-  const int bc_G = (pt / kWsTile) % kWsCons;
-  const int bc_step = pt % kWsTile;
+  // B/C staging: producer lane pt -> (state 2G + half, step) of a tile.
+  // With kDt B and C are token-major: a wave reads 4 steps x 16 states, so
+  // one load touches 4 token rows (32 contiguous bytes each), not 16.
+  const int bc_half = kDt ? lane & 1 : pt / (kWsCons * kWsTile);
+  const int bc_G = kDt ? (lane >> 1) & 7 : (pt / kWsTile) % kWsCons;
+  const int bc_step = kDt ? (w - kWsCons) * 4 + (lane >> 4) : pt % kWsTile;
   const int bc_n = 2 * bc_G + bc_half;
   const bool bc_ok = bc_n < N;
   const size_t bc_row = (size_t)b * p.bc_bstride + (size_t)min(bc_n, N - 1) * L;
@@ -759,9 +778,58 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   const auto C_ld = raw_rsrc(const_cast<T*>(Cp) + (size_t)b * p.bc_bstride, bc_bytes);
   const uint32_t bc_row_off = (uint32_t)((size_t)min(bc_n, N - 1) * L * sizeof(T));
 
-  auto issue = [&](WsRows<T>& r, int i) {
+  // kDt: the batch row's token rows of params (the launch keeps L * P * 2 <
+  // 2^31), this lane's byte offsets from a tile's first token row -- its
+  // dt^T operand (token lane % 16; rank groups past the rank read group 0,
+  // which meets zero weights) and its B / C values (token bc_step) -- and its
+  // W_dt operand: channel d0 + 16 pw + lane % 16, ranks 32 s + 8 (lane / 16)
+  // .. + 7, zero past the rank or the last channel.  Tokens past the end of
+  // the sequence fall outside the buffer range and read zero: they are
+  // identity steps, whose outputs are never stored.
+  const uint32_t prow_bytes = kDt ? (uint32_t)dtp.P * 2u : 0u;
+  const auto pr_ld =
+      raw_rsrc(kDt ? static_cast<char*>(const_cast<void*>(dtp.params)) + (size_t)b * dtp.pstride * 2
+                   : static_cast<char*>(dummy),
+               (uint32_t)L * prow_bytes);
+  uint32_t pa_off[kDtK] = {}, pbc_off = 0;
+  bf16x8_v wdt[kDtK];
+  if constexpr (kDt) {
+    pbc_off = (uint32_t)bc_step * prow_bytes + (uint32_t)(dtp.rank + min(bc_n, N - 1)) * 2u;
+    const int pw = w - kWsCons;
+    const int wch = d0 + 16 * pw + (lane & 15);
+    const __hip_bfloat16* wrow =
+        static_cast<const __hip_bfloat16*>(dtp.w) + (size_t)min(wch, Dm - 1) * dtp.rank;
+#pragma unroll
+    for (int s = 0; s < kDtK; ++s) {
+      const int g = 32 * s + 8 * (lane >> 4);
+      const bool gok = g < dtp.rank;
+      pa_off[s] = (uint32_t)(lane & 15) * prow_bytes + (uint32_t)(gok ? g : 0) * 2u;
+      u32x4_v wv = {0u, 0u, 0u, 0u};
+      if (gok && wch < Dm) wv = *reinterpret_cast<const u32x4_v*>(wrow + g);
+      wdt[s] = __builtin_bit_cast(bf16x8_v, wv);
+    }
+  }
+
+  auto issue = [&](WsRows<T, kDt>& r, int i) {
     const int t0 = min(Tbeg + i * kWsTile, last_t0);
-    if constexpr (kAligned) {
+    if constexpr (kDt) {
+      const uint32_t tb = (uint32_t)t0 * prow_bytes;  // wave-uniform
+#pragma unroll
+      for (int s = 0; s < kDtK; ++s)
+        r.pa[s] = __builtin_amdgcn_raw_buffer_load_b128(pr_ld, (int)(tb + pa_off[s]), 0, 0);
+      r.B = buffer_load_bits1<T>(pr_ld, tb + pbc_off);
+      r.C = buffer_load_bits1<T>(pr_ld, tb + pbc_off + (uint32_t)N * 2u);
+      if constexpr (kAligned) {
+        const uint32_t off = row_off + (uint32_t)min(t0 + 4 * q, L - 4) * sizeof(T);
+        r.u = buffer_load_raw4<T>(u_ld, off);
+        if constexpr (kHasZ) r.z = buffer_load_raw4<T>(z_ld, off);
+        else r.z = typename Raw4<T>::type{};
+      } else {
+        r.u = load_raw4_nb<T, kAligned>(u_row, t0 + 4 * q, L, pch_ok);
+        if constexpr (kHasZ) r.z = load_raw4_nb<T, kAligned>(z_row, t0 + 4 * q, L, pch_ok);
+        else r.z = typename Raw4<T>::type{};
+      }
+    } else if constexpr (kAligned) {
       const uint32_t off = row_off + (uint32_t)min(t0 + 4 * q, L - 4) * sizeof(T);
       r.u = buffer_load_raw4<T>(u_ld, off);
       r.d = buffer_load_raw4<T>(d_ld, off);
@@ -786,12 +854,61 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   // for its finish; with kSum, delta is also added to the sum of tile parity
   // par (i % 2)
   float dts[2] = {0.0f, 0.0f};  // kSum: step sizes of the even and odd tiles
-  auto stage = [&](const WsRows<T>& r, int i, int sbuf, float (&sk)[4], float (&gt)[4], int par) {
+  // kDt: the wave's 16 rows of delta_out (rows past the last channel lie
+  // outside the range; an empty range without delta_out)
+  const auto dto_rsrc =
+      raw_rsrc(kDt && !kSum && dtp.delta_out
+                   ? static_cast<char*>(dtp.delta_out) + ((size_t)rb + wrow0) * L * sizeof(T)
+                   : static_cast<char*>(dummy),
+               kDt && !kSum && dtp.delta_out ? wbytes : 0u);
+  // kDt: a tile's delta_raw (steps 4 (lane / 16) .. + 3 of channel lane % 16
+  // of the wave's 16), issued an iteration before the tile is staged so that
+  // the MFMA latency runs under that iteration's other work
+  auto proj = [&](const WsRows<T, kDt>& r) {
+    f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (kDt) {
+#pragma unroll
+      for (int s = 0; s < kDtK; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, r.pa[s]), wdt[s],
+                                                      acc, 0, 0, 0);
+    }
+    return acc;
+  };
+  auto stage = [&](const WsRows<T, kDt>& r, const f32x4_v acc, int i, int sbuf, float (&sk)[4],
+                   float (&gt)[4], int par) {
     const int t_tile = Tbeg + i * kWsTile;
     const int t = t_tile + 4 * q;
     float uv[4], dv[4], de[4], du[4];
     decode4(r.u, uv);
-    decode4(r.d, dv);
+    if constexpr (kDt) {
+      // this lane's row (channel lane % 16) and 4-step column (lane / 16),
+      // rounded to bf16
+      const uint32_t x01 = pack_bf16x2(acc[0], acc[1]);
+      const uint32_t x23 = pack_bf16x2(acc[2], acc[3]);
+      decode4(make_uint2(x01, x23), dv);
+      if constexpr (!kSum) {
+        // delta_out: stored without a branch (a conditional path with memory
+        // operations makes the compiler wait for the ring's loads at the
+        // merge); without delta_out the range is empty and the stores are
+        // dropped.  Aligned rows: L and the segment ends are multiples of 4,
+        // so the 4 steps are one 8-byte piece inside the row or wholly past
+        // its end.
+        if constexpr (kAligned) {
+          const uint32_t off = t < Lend ? row_off + (uint32_t)t * 2u : kOffDrop;
+          const u32x2_v xv = {x01, x23};
+          __builtin_amdgcn_raw_buffer_store_b64(xv, dto_rsrc, (int)off, 0, 0);
+        } else {
+          const uint32_t bits[4] = {x01 & 0xffffu, x01 >> 16, x23 & 0xffffu, x23 >> 16};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t off = t + j < Lend ? row_off + (uint32_t)(t + j) * 2u : kOffDrop;
+            __builtin_amdgcn_raw_buffer_store_b16((unsigned short)bits[j], dto_rsrc, (int)off, 0, 0);
+          }
+        }
+      }
+    } else {
+      decode4(r.d, dv);
+    }
     if constexpr (kHasZ) {
       float zv[4];
       decode4(r.z, zv);
@@ -940,18 +1057,19 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   // into the loop header makes it wait for nearly all of them).  Work past
   // the last tile is harmless: its loads are clamped into the rows, its
   // staging buffers are never read and its stores fall outside the range.
-  WsRows<T> rows[kWsRing];
+  WsRows<T, kDt> rows[kWsRing];
   float sk[4][4], gt[4][4];
   float4 v[kWsCons];
 #pragma unroll
   for (int k = 0; k < kWsRing; ++k) issue(rows[k], k);
-  stage(rows[0], 0, 0, sk[0], gt[0], 0);
+  stage(rows[0], proj(rows[0]), 0, 0, sk[0], gt[0], 0);
   issue(rows[0], kWsRing);
-  stage(rows[1], 1, 1, sk[1], gt[1], 1);
+  stage(rows[1], proj(rows[1]), 1, 1, sk[1], gt[1], 1);
   issue(rows[1], kWsRing + 1);
   __syncthreads();  // iteration 0
-  stage(rows[2], 2, 2, sk[2], gt[2], 0);
+  stage(rows[2], proj(rows[2]), 2, 2, sk[2], gt[2], 0);
   issue(rows[2], kWsRing + 2);
+  f32x4_v dacc = proj(rows[3]);  // kDt: tile 3, staged at iteration 1
   int sbuf = 0;  // staging buffer of tile i + 2
   for (int i0 = 1; i0 <= ntiles; i0 += 4) {
 #pragma unroll
@@ -960,7 +1078,8 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       __syncthreads();
       if constexpr (!kSum) finish_read(i - 1, v);
       // i0 % 4 == 1, so tile i + 2 has the parity of j + 3
-      stage(rows[(j + 3) % kWsRing], i + 2, sbuf, sk[(j + 3) & 3], gt[(j + 3) & 3], (j + 3) & 1);
+      stage(rows[(j + 3) % kWsRing], dacc, i + 2, sbuf, sk[(j + 3) & 3], gt[(j + 3) & 3],
+            (j + 3) & 1);
       issue(rows[(j + 3) % kWsRing], i + 2 + kWsRing);
       if constexpr (!kSum) {
         if constexpr (kAligned) {
@@ -970,15 +1089,20 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
           finish(i - 1, v, sk[j], gt[j]);
         }
       }
+      // tile i + 3 sits in ring slot (i + 3) % 4 == j
+      dacc = proj(rows[j]);
       sbuf = sbuf == kWsStage - 1 ? 0 : sbuf + 1;
     }
   }
   if constexpr (kSum) {
-    // the four lanes of a channel row are 4 consecutive lanes (q = lane % 4)
+    // the four lanes of a channel row: 4 consecutive lanes (q = lane % 4), or
+    // with kDt lanes 16 apart (q = lane / 16); either way columns 0+1 and 2+3
+    // first, then their sums
 #pragma unroll
     for (int m = 1; m < kT4; m <<= 1) {
-      dts[0] += __shfl_xor(dts[0], m, 64);
-      dts[1] += __shfl_xor(dts[1], m, 64);
+      const int x = kDt ? 16 * m : m;
+      dts[0] += __shfl_xor(dts[0], x, 64);
+      dts[1] += __shfl_xor(dts[1], x, 64);
     }
     if (q == 0 && pch_ok) seg_dt[sb * Dm + pch] = dts[0] + dts[1];
   }
@@ -1385,7 +1509,7 @@ static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t 
                          dims_of(p), (const T*)p.u, (const T*)p.delta, p.A, (const T*)p.B,
                          (const T*)p.C, p.D, p.bias, p.h_init, p.length, (const T*)nullptr,
                          (T*)p.out, (T*)nullptr, (float*)nullptr, (float*)nullptr, p.dummy,
-                         p.seg_h, p.seg_dt);
+                         p.seg_h, p.seg_dt, DtProj{});
     else
       hipLaunchKernelGGL((scan_fwd_segsum_kernel<T, kSG, kAligned>),
                          dim3(p.nblk, p.batch, (p.nseg - 1) * p.sub_k), dim3(kThreads), 0, st,
@@ -1401,7 +1525,7 @@ static hipError_t launch_fwd4(const ScanParams& p, const float* bc, hipStream_t 
                        dim3(kWsThreads), 0, st, dims_of(p), (const T*)p.u, (const T*)p.delta, p.A,
                        (const T*)p.B, (const T*)p.C, p.D, p.bias, p.h_init, p.length,
                        (const T*)p.z, (T*)p.out, (T*)p.out_ungated, p.h_chunks, p.h_last, p.dummy,
-                       p.seg_h, p.seg_dt);
+                       p.seg_h, p.seg_dt, DtProj{});
     return hipGetLastError();
   }
   hipLaunchKernelGGL((scan_fwd_kernel<T, kSG, kZ, kAligned>),
@@ -1448,6 +1572,41 @@ hipError_t launch_scan_fwd(const ScanParams& p, int dtype, bool aligned, float* 
   }
   if (dtype == 1) return launch_fwd2<__hip_bfloat16>(p, bc, aligned, st);
   return launch_fwd2<float>(p, bc, aligned, st);
+}
+
+// The forward with the fused step-size projection (DtProj): bf16, the
+// role-split kernel only.  p.delta, p.B and p.C are not read; the kernels'
+// delta, B and C arguments get valid addresses they never load from.
+bool scan_fwd_dt_supported(const ScanParams& p) { return p.nstate <= 16 && ws_forward(p, 2); }
+
+template <int kZ, bool kAligned, bool kSum>
+static void launch_ws_dt(const ScanParams& p, const DtProj& dt, hipStream_t st) {
+  using T = __hip_bfloat16;
+  const int gz = kSum ? (p.nseg - 1) * p.sub_k : p.nseg;
+  const T* prm = static_cast<const T*>(dt.params);
+  hipLaunchKernelGGL((scan_fwd_ws_kernel<T, kZ, kAligned, kSum, true>), dim3(p.nblk, p.batch, gz),
+                     dim3(kWsThreads), 0, st, dims_of(p), (const T*)p.u, (const T*)p.u, p.A, prm,
+                     prm, p.D, p.bias, p.h_init, p.length, (const T*)p.z, (T*)p.out,
+                     (T*)nullptr, (float*)nullptr, p.h_last, p.dummy, p.seg_h, p.seg_dt, dt);
+}
+
+hipError_t launch_scan_fwd_dt(const ScanParams& p, const DtProj& dt, bool aligned, hipStream_t st) {
+  if (p.nseg > 1) {
+    ProfScope prof("scan_fwd_segsum", st);
+    if (aligned) launch_ws_dt<0, true, true>(p, dt, st);
+    else launch_ws_dt<0, false, true>(p, dt, st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  ProfScope prof("scan_fwd", st);
+  if (p.z) {
+    if (aligned) launch_ws_dt<1, true, false>(p, dt, st);
+    else launch_ws_dt<1, false, false>(p, dt, st);
+  } else {
+    if (aligned) launch_ws_dt<0, true, false>(p, dt, st);
+    else launch_ws_dt<0, false, false>(p, dt, st);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace ssm

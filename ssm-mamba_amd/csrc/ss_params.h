@@ -43,6 +43,30 @@ struct ScanDims {
   int hs;              // h_chunks state-slot stride in rows of dim (1: states only; 2: (prod a, h) pairs)
 };
 
+// The step-size projection of a Mamba block fused into the role-split
+// forward (modules/mamba.py:141-160): the block's x-projection output
+// ssm_params is token-major, (batch, seqlen, P) with P = rank + 2 N and each
+// token's row [dt (rank) | B (N) | C (N)], and the scan's step sizes are
+// delta_raw = W_dt dt rounded to bf16 (the reference's delta matrix product
+// in the model dtype), with W_dt (dim, rank).  Each producer wave computes
+// its 16 channels x 16 steps of delta_raw per tile with kDtK
+// v_mfma_f32_16x16x32_bf16 (32 ranks each) and reads B and C in place from
+// the same rows, so neither delta nor channel-major copies of B and C are
+// written or read.  Operand layout of the 16x16x32 bf16 MFMA (checked on
+// gfx950): lane l supplies A[l % 16][8 (l / 16) + i] and B[8 (l / 16) + i][l % 16],
+// i = 0..7, and holds D[4 (l / 16) + r][l % 16] in accumulator r.  Here A is
+// dt^T (16 steps x 32 ranks: one 16-byte load from a token row per lane and
+// k-step), B is W_dt^T (32 ranks x 16 channels: 16 bytes of a W_dt row, held
+// for the whole launch), and D is delta_raw (steps x channels).
+struct DtProj {
+  const void* params;   // (batch, seqlen, P) bf16, 16-byte aligned rows
+  int64_t pstride;      // elements between batch rows of params
+  int P, rank;
+  const void* w;        // (dim, rank) bf16
+  void* delta_out;      // nullable: delta_raw as (batch, dim, seqlen) bf16
+};
+constexpr int kDtK = 2;  // MFMA k-steps of 32 ranks: rank <= 64
+
 // Sub-segments of the segment summaries: segment s is cut into sub_k parts
 // of sub_span steps (a multiple of the 32-step summary tile), the last part
 // ending at the segment's end (shorter, or empty when the others already

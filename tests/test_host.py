@@ -142,6 +142,45 @@ def test_bc_batch_stride_is_checked():
     assert rc == 1 and b"bc_batch_stride" in lib.ssm_last_error()
 
 
+def test_dt_proj_shapes_and_arguments_are_checked():
+    """The fused step-size projection's shape query and argument checks run on
+    the host (fake addresses are never dereferenced: every call here returns
+    before any launch)."""
+    from ssm_mamba_amd import _native as N
+    lib = N.lib()
+    ok = lambda *a: lib.ssm_selective_scan_fwd_dt_proj_supported(*a)
+    assert ok(4, 2048, 2048, 16, 64, N.SSM_BF16) == 1
+    assert ok(1, 80, 37, 4, 8, N.SSM_BF16) == 1
+    assert ok(4, 2048, 2048, 16, 64, N.SSM_F32) == 0      # bf16 only
+    assert ok(4, 2048, 2048, 16, 72, N.SSM_BF16) == 0     # rank > 64
+    assert ok(4, 2048, 2048, 16, 60, N.SSM_BF16) == 0     # rank not a multiple of 8
+    assert ok(4, 2048, 2048, 32, 64, N.SSM_BF16) == 0     # N > 16
+    assert ok(4, 2048, 2048, 6, 64, N.SSM_BF16) == 0      # N not a multiple of 4
+    assert ok(1, 64, 1 << 24, 16, 64, N.SSM_BF16) == 0    # token rows past 2^31 bytes
+    P = 4096  # a 16-byte aligned fake address
+    ws = 1 << 30
+
+    def call(**kw):
+        a = dict(batch=2, dim=64, seqlen=16, nstate=16, rank=64, dtype=N.SSM_BF16, u=P, params=P,
+                 pstride=0, w=P, A=P, out=P, ws=P)
+        a.update(kw)
+        return lib.ssm_selective_scan_fwd_dt_proj(
+            a["batch"], a["dim"], a["seqlen"], a["nstate"], a["rank"], a["dtype"], a["u"],
+            a["params"], a["pstride"], a["w"], a["A"], None, None, None, None, 0, None, 1, a["out"],
+            None, None, a["ws"], ws, None)
+
+    # SSM_ERR_INVALID = 1, SSM_ERR_UNSUPPORTED = 2
+    assert call(dtype=N.SSM_F32) == 2 and b"bf16" in lib.ssm_last_error()
+    assert call(rank=0) == 1 and b"dt_rank" in lib.ssm_last_error()
+    assert call(params=None) == 1 and b"non-NULL" in lib.ssm_last_error()
+    assert call(pstride=16 * 96 - 8) == 1 and b"params_batch_stride" in lib.ssm_last_error()
+    assert call(pstride=16 * 96 + 4) == 2 and b"16-byte" in lib.ssm_last_error()
+    assert call(params=P + 8) == 2 and b"16-byte" in lib.ssm_last_error()
+    assert call(ws=None) == 1 and b"workspace" in lib.ssm_last_error()
+    # the shape query leaves the last error message alone
+    assert ok(2, 64, 16, 16, 72, N.SSM_BF16) == 0 and b"workspace" in lib.ssm_last_error()
+
+
 def _scan_args(batch=2, dim=4, seqlen=8, nstate=3):
     return dict(u=torch.randn(batch, dim, seqlen), A=torch.randn(dim, nstate),
                 B=torch.randn(batch, nstate, seqlen), C=torch.randn(batch, nstate, seqlen),
