@@ -150,6 +150,8 @@ int ssm_selective_scan_fwd_noalloc(int64_t batch, int64_t dim, int64_t seqlen, i
  *              ssm_selective_scan_fwd with delta = delta_raw and B, C read in
  *              place from ssm_params.  Written to delta_out (nullable;
  *              (batch, dim, seqlen) bf16) when given.
+ * z_batch_stride: elements between batch rows of z (0: dim * seqlen), so the
+ * gate half of the in-projection output is read in place.
  * The other arguments as ssm_selective_scan_fwd; no saved chunk states and no
  * ungated output (inference).  bf16 only, nstate <= 16 and a multiple of 4,
  * dt_rank a multiple of 8 and <= 64, ssm_params and dt_weight 16-byte aligned,
@@ -163,8 +165,9 @@ int ssm_selective_scan_fwd_dt_proj(int64_t batch, int64_t dim, int64_t seqlen, i
                                    const void* dt_weight, const float* A, const float* D,
                                    const float* delta_bias, const float* h_init,
                                    const int64_t* length, int padding_right, const void* z,
-                                   int delta_softplus, void* out, void* delta_out, float* h_last,
-                                   void* workspace, size_t workspace_bytes, void* stream);
+                                   int64_t z_batch_stride, int delta_softplus, void* out,
+                                   void* delta_out, float* h_last, void* workspace,
+                                   size_t workspace_bytes, void* stream);
 /* 1 when ssm_selective_scan_fwd_dt_proj takes this shape and dtype, else 0. */
 int ssm_selective_scan_fwd_dt_proj_supported(int64_t batch, int64_t dim, int64_t seqlen,
                                              int64_t nstate, int64_t dt_rank, int dtype);
@@ -244,10 +247,14 @@ int ssm_rms_norm_cm(int64_t batch, int64_t channels, int64_t seqlen, int dtype, 
  * prefill leaves (modules/mamba.py:113-135): the width-1 inputs x[b,c,t] for
  * t = len-(width-1) .. len-1, zero for t < 0, with len = lengths[b] clamped to
  * [0, seqlen] (lengths nullable: len = seqlen; lengths requires window).
+ * x_batch_stride: elements between batch rows of x (0: dim * seqlen), so a
+ * channel slice of a larger activation -- the x half of the in-projection
+ * output (modules/mamba.py:104-111) -- is read in place; out is contiguous.
  */
 int ssm_causal_conv1d_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t width, int dtype,
-                          const void* x, const void* weight, const void* bias, int silu, void* out,
-                          const int64_t* lengths, void* window, void* stream);
+                          const void* x, int64_t x_batch_stride, const void* weight,
+                          const void* bias, int silu, void* out, const int64_t* lengths,
+                          void* window, void* stream);
 
 /* Device workspace (bytes) for ssm_causal_conv1d_bwd. */
 size_t ssm_causal_conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t width);

@@ -57,7 +57,7 @@ SIGNATURES = {
         _i64, _i64, _i64, _i64, _i64, _i32,    # batch, dim, seqlen, nstate, dt_rank, dtype
         _p, _p, _i64, _p,                      # u, ssm_params, params_batch_stride, dt_weight
         _p, _p, _p, _p, _p,                    # A, D, delta_bias, h_init, length
-        _i32, _p, _i32,                        # padding_right, z, delta_softplus
+        _i32, _p, _i64, _i32,                  # padding_right, z, z_batch_stride, delta_softplus
         _p, _p, _p,                            # out, delta_out, h_last
         _p, _sz, _p,                           # workspace, bytes, stream
     ]),
@@ -78,7 +78,7 @@ SIGNATURES = {
     ]),
     "ssm_causal_conv1d_fwd": (_i32, [
         _i64, _i64, _i64, _i64, _i32,          # batch, dim, seqlen, width, dtype
-        _p, _p, _p, _i32, _p,                  # x, weight, bias, silu, out
+        _p, _i64, _p, _p, _i32, _p,            # x, x_batch_stride, weight, bias, silu, out
         _p, _p, _p,                            # lengths, window, stream
     ]),
     "ssm_causal_conv1d_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64]),
@@ -128,7 +128,7 @@ SIGNATURES = {
     ]),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 def lib() -> ctypes.CDLL:

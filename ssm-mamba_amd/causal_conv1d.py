@@ -37,8 +37,13 @@ class CausalConv1dFn(torch.autograd.Function):
                 silu: bool, lengths: Optional[torch.Tensor] = None,
                 window: Optional[torch.Tensor] = None) -> torch.Tensor:
         _check_x(x)
-        x = x.contiguous()
         batch, dim, seqlen = x.shape
+        # a channel slice of a larger activation (each batch row's (channels,
+        # seq_len) block contiguous) is read in place through its batch stride
+        if not (x.stride(2) == 1 and x.stride(1) == seqlen
+                and (batch == 1 or x.stride(0) >= dim * seqlen)):
+            x = x.contiguous()
+        xbs = 0 if batch == 1 else x.stride(0)
         width = weight.shape[-1]
         if weight.numel() != dim * width:
             raise RuntimeError("weight must have shape (channels, 1, width) or (channels, width)")
@@ -46,7 +51,7 @@ class CausalConv1dFn(torch.autograd.Function):
         b = None if bias is None else bias.to(x.dtype).contiguous()
         if b is not None and b.numel() != dim:
             raise RuntimeError("bias must have shape (channels,)")
-        out = torch.empty_like(x)
+        out = torch.empty((batch, dim, seqlen), dtype=x.dtype, device=x.device)
         if window is not None:
             if (tuple(window.shape) != (batch, dim, width - 1) or window.dtype != x.dtype
                     or not window.is_contiguous() or window.device != x.device):
@@ -62,7 +67,7 @@ class CausalConv1dFn(torch.autograd.Function):
         L = N.lib()
         with torch.cuda.device(x.device):
             N.check(L.ssm_causal_conv1d_fwd(batch, dim, seqlen, width, _DTYPES[x.dtype],
-                                            x.data_ptr(), w.data_ptr(),
+                                            x.data_ptr(), xbs, w.data_ptr(),
                                             None if b is None else b.data_ptr(), int(silu),
                                             out.data_ptr(),
                                             None if lengths is None else lengths.data_ptr(),
@@ -78,6 +83,7 @@ class CausalConv1dFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout: torch.Tensor):
         x, w, b = ctx.saved_tensors
+        x = x.contiguous()
         batch, dim, seqlen = x.shape
         width = w.shape[1]
         dout = dout.to(x.dtype).contiguous()

@@ -17,10 +17,11 @@ GEMM with the weight broadcast over the batch), so the reference's per-layer
 permute copies (``modules/mamba.py:104-111,156-163,181``) do not exist here:
 the sequence is transposed once after the embedding and once before the LM
 head.  The z gate is fused into the scan / state-update kernels.  In an
-inference prefill (bf16 on the GPU) the x-projection output is token-major,
-the reference's own layout of ssm_params, and the step-size projection runs
-inside the scan kernels (``ssm_selective_scan_fwd_dt_proj``), which read dt,
-B and C from it in place.
+inference prefill (bf16 on the GPU) the in-projection is one GEMM whose x and
+z halves the conv and scan kernels read in place, the x-projection output is
+token-major, the reference's own layout of ssm_params, and the step-size
+projection runs inside the scan kernels (``ssm_selective_scan_fwd_dt_proj``),
+which read dt, B and C from it in place.
 
 Decode.  ``Mamba.step`` updates the per-layer caches in place (conv window and
 fp32 SSM state), so a whole token step -- all layers, final norm, LM head and
@@ -197,34 +198,37 @@ class Mamba(nn.Module):
             self._xproj_t = (key, w.detach().t().contiguous())
         return self._xproj_t[1]
 
-    def _dt_fusable(self, xc: torch.Tensor, z: torch.Tensor, h0: Optional[torch.Tensor],
+    def _dt_fusable(self, x: torch.Tensor, h0: Optional[torch.Tensor],
                     lengths: Optional[torch.Tensor]) -> bool:
-        """Whether the x-projection output can go to the scan with the step-size
-        projection fused in (ssm_selective_scan_fwd_dt_proj): inference, bf16
-        on the GPU, and a shape the fused kernel takes."""
+        """Whether a forward of x (batch, model_dim, L) takes the inference
+        prefill path: the in-projection as one GEMM whose x and z halves are
+        read in place, and the scan with the step-size projection fused in
+        (ssm_selective_scan_fwd_dt_proj): no autograd, bf16 on the GPU, and a
+        shape the fused kernel takes."""
         w_dt = self.delta_proj.weight
-        if torch.is_grad_enabled() or not xc.is_cuda or xc.dtype != torch.bfloat16:
+        if torch.is_grad_enabled() or not x.is_cuda or x.dtype != torch.bfloat16:
             return False
-        if w_dt.dtype != torch.bfloat16 or self.ssm_param_proj.weight.dtype != torch.bfloat16:
+        if any(w.dtype != torch.bfloat16 for w in (w_dt, self.ssm_param_proj.weight,
+                                                     self.input_proj.weight)):
             return False
-        if not (xc.is_contiguous() and z.is_contiguous() and w_dt.is_contiguous()
-                and w_dt.data_ptr() % 16 == 0):
+        if not (w_dt.is_contiguous() and w_dt.data_ptr() % 16 == 0):
             return False
-        if h0 is not None and tuple(h0.shape) != (xc.shape[0], self.inner_dim, self.state_dim):
+        batch, seqlen = x.shape[0], x.shape[2]
+        if h0 is not None and tuple(h0.shape) != (batch, self.inner_dim, self.state_dim):
             return False
-        if lengths is not None and lengths.device != xc.device:
+        if lengths is not None and lengths.device != x.device:
             return False
-        batch, inner, seqlen = xc.shape
         return bool(_N.lib().ssm_selective_scan_fwd_dt_proj_supported(
-            batch, inner, seqlen, self.state_dim, self.delta_rank, _N.SSM_BF16))
+            batch, self.inner_dim, seqlen, self.state_dim, self.delta_rank, _N.SSM_BF16))
 
     def _scan_dt_proj(self, xc: torch.Tensor, z: torch.Tensor, h0: Optional[torch.Tensor],
                       lengths: Optional[torch.Tensor]):
         """modules/mamba.py:141-171 for inference: the token-major x-projection
         (one GEMM), then the scan with delta_raw = W_dt dt computed by the scan
         kernels' producers on the matrix cores and B, C read in place from the
-        projection output (no delta or channel-major B/C tensors).  Returns
-        (out, last state)."""
+        projection output (no delta or channel-major B/C tensors).  z may be
+        the gate half of the in-projection output (its batch stride is taken).
+        Returns (out, last state)."""
         batch, inner, seqlen = xc.shape
         nstate, rank = self.state_dim, self.delta_rank
         w_xt = self._x_proj_t()
@@ -234,6 +238,8 @@ class Mamba(nn.Module):
         lengths = None if lengths is None else lengths.to(torch.int64).contiguous()
         out = torch.empty_like(xc)
         last = torch.empty(batch, inner, nstate, dtype=torch.float32, device=xc.device)
+        assert z.stride(2) == 1 and z.stride(1) == seqlen
+        zbs = 0 if batch == 1 else z.stride(0)
         lib = _N.lib()
         ws = torch.empty(lib.ssm_scan_fwd_workspace_bytes(batch, inner, seqlen, nstate),
                          dtype=torch.uint8, device=xc.device)
@@ -242,7 +248,7 @@ class Mamba(nn.Module):
             _N.check(lib.ssm_selective_scan_fwd_dt_proj(
                 batch, inner, seqlen, nstate, rank, _N.SSM_BF16, xc.data_ptr(), params.data_ptr(),
                 0, self.delta_proj.weight.data_ptr(), A.data_ptr(), ptr(D), ptr(dt_bias), ptr(h0),
-                ptr(lengths), 0, z.data_ptr(), 1, out.data_ptr(), None, last.data_ptr(),
+                ptr(lengths), 0, z.data_ptr(), zbs, 1, out.data_ptr(), None, last.data_ptr(),
                 ws.data_ptr(), ws.numel(), torch.cuda.current_stream(xc.device).cuda_stream))
         return out, last
 
@@ -302,8 +308,14 @@ class Mamba(nn.Module):
         the last SSM state."""
         inner, rank, nstate = self.inner_dim, self.delta_rank, self.state_dim
         w_in, b_in = self.input_proj.weight, self.input_proj.bias
-        xs = _proj_cm(w_in[:inner], x, None if b_in is None else b_in[:inner])
-        z = _proj_cm(w_in[inner:], x, None if b_in is None else b_in[inner:])
+        fused = self._dt_fusable(x, ssm_hiddens, lengths)
+        if fused:
+            # one GEMM for both halves; the conv and the scan read them in place
+            xz = _proj_cm(w_in, x, b_in)                                  # (batch, 2 inner, L)
+            xs, z = xz[:, :inner], xz[:, inner:]
+        else:
+            xs = _proj_cm(w_in[:inner], x, None if b_in is None else b_in[:inner])
+            z = _proj_cm(w_in[inner:], x, None if b_in is None else b_in[inner:])
         # with use_cache the conv kernel also leaves the k-1 pre-conv inputs
         # ending at position lengths-1 (zero before the row start), the
         # reference's conv cache (modules/mamba.py:113-135)
@@ -314,7 +326,7 @@ class Mamba(nn.Module):
             self._conv_context = window
         # padding_side "left" is the reference's default at this call
         # (modules/mamba.py:170-175 passes no padding argument)
-        if self._dt_fusable(xc, z, ssm_hiddens, lengths):
+        if fused:
             y, last = self._scan_dt_proj(xc, z, ssm_hiddens, lengths)
         else:
             params = _proj_cm(self.ssm_param_proj.weight, xc)           # (batch, R + 2N, L)

@@ -56,9 +56,9 @@ hipError_t launch_decode_layers(int bf16, const void* table, int nlayers, int B,
 hipError_t launch_rms_norm_cm(int bf16, const void* x, const void* w, float eps, void* out, int B,
                               int C, int L, bool pair, hipStream_t st);
 hipError_t launch_causal_conv1d_fwd(int batch, int dim, int L, int K, int dtype_bf16,
-                                    const void* x, const void* w, const void* bias, int silu,
-                                    void* out, const int64_t* lengths, void* window, bool vec,
-                                    hipStream_t st);
+                                    const void* x, int64_t xbs, const void* w, const void* bias,
+                                    int silu, void* out, const int64_t* lengths, void* window,
+                                    bool vec, hipStream_t st);
 hipError_t launch_causal_conv1d_bwd(int batch, int dim, int L, int K, int dtype_bf16,
                                     const void* x, const void* w, const void* bias,
                                     const void* dout, int silu, void* dx, void* dw, void* dbias,
@@ -254,7 +254,7 @@ extern "C" {
 
 const char* ssm_last_error(void) { return g_err.c_str(); }
 
-int ssm_abi_version(void) { return 9; }
+int ssm_abi_version(void) { return 10; }
 
 int ssm_profile_begin(void) {
   g_err.clear();
@@ -537,8 +537,9 @@ int ssm_selective_scan_fwd_dt_proj(int64_t batch, int64_t dim, int64_t seqlen, i
                                    const void* dt_weight, const float* A, const float* D,
                                    const float* delta_bias, const float* h_init,
                                    const int64_t* length, int padding_right, const void* z,
-                                   int delta_softplus, void* out, void* delta_out, float* h_last,
-                                   void* workspace, size_t workspace_bytes, void* stream) {
+                                   int64_t z_batch_stride, int delta_softplus, void* out,
+                                   void* delta_out, float* h_last, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
   g_err.clear();
   if (int e = check_dt_proj(batch, dim, seqlen, nstate, dt_rank, dtype)) return e;
   if (!u || !ssm_params || !dt_weight || !A || !out)
@@ -550,6 +551,9 @@ int ssm_selective_scan_fwd_dt_proj(int64_t batch, int64_t dim, int64_t seqlen, i
   if (!aligned16(ssm_params) || !aligned16(dt_weight) || params_batch_stride % 8)
     return fail(SSM_ERR_UNSUPPORTED, "the fused step-size projection needs 16-byte aligned "
                 "ssm_params rows and dt_weight");
+  if (z_batch_stride != 0 && z_batch_stride < dim * seqlen)
+    return fail(SSM_ERR_INVALID, "z_batch_stride must be 0 (contiguous) or at least dim * seqlen "
+                "(got %lld)", (long long)z_batch_stride);
   const size_t need = ssm_scan_fwd_workspace_bytes(batch, dim, seqlen, nstate);
   if (!workspace || workspace_bytes < need)
     return fail(SSM_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
@@ -575,7 +579,8 @@ int ssm_selective_scan_fwd_dt_proj(int64_t batch, int64_t dim, int64_t seqlen, i
   dt.rank = (int)dt_rank;
   dt.w = dt_weight;
   dt.delta_out = delta_out;
-  const bool aligned = scan_aligned(dtype, seqlen, {u, z, out});
+  dt.zbstride = z_batch_stride ? z_batch_stride : dim * seqlen;
+  const bool aligned = scan_aligned(dtype, seqlen, {u, z, out}) && dt.zbstride % 8 == 0;
   return hip_status(ssm::launch_scan_fwd_dt(p, dt, aligned, static_cast<hipStream_t>(stream)),
                     "selective_scan forward with the step-size projection launch");
 }
@@ -841,16 +846,21 @@ size_t ssm_causal_conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t
 }
 
 int ssm_causal_conv1d_fwd(int64_t batch, int64_t dim, int64_t seqlen, int64_t width, int dtype,
-                          const void* x, const void* weight, const void* bias, int silu, void* out,
-                          const int64_t* lengths, void* window, void* stream) {
+                          const void* x, int64_t x_batch_stride, const void* weight,
+                          const void* bias, int silu, void* out, const int64_t* lengths,
+                          void* window, void* stream) {
   int rc = check_conv(batch, dim, seqlen, width, dtype);
   if (rc != SSM_OK) return rc;
   if (!x || !weight || !out) return fail(SSM_ERR_INVALID, "x, weight and out must be non-NULL");
   if (lengths && !window) return fail(SSM_ERR_INVALID, "lengths requires window");
-  const bool vec = seqlen % 8 == 0 && aligned16(x) && aligned16(out);
+  if (x_batch_stride != 0 && x_batch_stride < dim * seqlen)
+    return fail(SSM_ERR_INVALID, "x_batch_stride must be 0 (contiguous) or at least dim * seqlen "
+                "(got %lld)", (long long)x_batch_stride);
+  const int64_t xbs = x_batch_stride ? x_batch_stride : dim * seqlen;
+  const bool vec = seqlen % 8 == 0 && xbs % 8 == 0 && aligned16(x) && aligned16(out);
   return hip_status(ssm::launch_causal_conv1d_fwd((int)batch, (int)dim, (int)seqlen, (int)width,
-                                                  dtype == SSM_BF16, x, weight, bias, silu ? 1 : 0,
-                                                  out, lengths, window, vec,
+                                                  dtype == SSM_BF16, x, xbs, weight, bias,
+                                                  silu ? 1 : 0, out, lengths, window, vec,
                                                   static_cast<hipStream_t>(stream)),
                     "causal_conv1d_fwd launch");
 }

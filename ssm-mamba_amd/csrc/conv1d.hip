@@ -101,15 +101,16 @@ __device__ __forceinline__ void block_sum(float (&v)[K + 1], float* red) {
 // window (nullable): the decode cache of the row, the K-1 inputs ending at
 // position len-1 (len = lengths[b] clamped to [0, L], or L), zero where the
 // window starts before the row (the conv context the reference keeps after a
-// prefill, modules/mamba.py:113-135).
+// prefill, modules/mamba.py:113-135).  x's batch rows are xbs elements apart
+// (a channel slice of a larger activation); out is contiguous.
 template <typename T, int K, bool kVec>
 __global__ __launch_bounds__(kConvThreads) void causal_conv1d_fwd_kernel(
-    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+    const T* __restrict__ x, int64_t xbs, const T* __restrict__ w, const T* __restrict__ bias,
     T* __restrict__ out, int dim, int L, int silu, const int64_t* __restrict__ lengths,
     T* __restrict__ window) {
   const size_t row = blockIdx.x;
   const int c = (int)(row % (size_t)dim);
-  const T* __restrict__ xr = x + row * (size_t)L;
+  const T* __restrict__ xr = x + (row / (size_t)dim) * (size_t)xbs + (size_t)c * L;
   T* __restrict__ orow = out + row * (size_t)L;
   float wk[K], bs;
   // the decode cache's row length, fetched now and used after the main loop
@@ -299,9 +300,9 @@ __global__ __launch_bounds__(256) void causal_conv1d_wgrad_kernel(const float* _
 }
 
 template <typename T, int K>
-hipError_t launch_fwd_k(int batch, int dim, int L, const void* x, const void* w, const void* bias,
-                        int silu, void* out, const int64_t* lengths, void* window, bool vec,
-                        hipStream_t st) {
+hipError_t launch_fwd_k(int batch, int dim, int L, const void* x, int64_t xbs, const void* w,
+                        const void* bias, int silu, void* out, const int64_t* lengths, void* window,
+                        bool vec, hipStream_t st) {
   ProfScope prof("causal_conv1d_fwd", st);
   const dim3 grid((unsigned)((size_t)batch * dim));
   auto* xp = static_cast<const T*>(x);
@@ -311,10 +312,10 @@ hipError_t launch_fwd_k(int batch, int dim, int L, const void* x, const void* w,
   auto* wo = static_cast<T*>(window);
   if (vec)
     hipLaunchKernelGGL((causal_conv1d_fwd_kernel<T, K, true>), grid, dim3(kConvThreads), 0, st, xp,
-                       wp, bp, op, dim, L, silu, lengths, wo);
+                       xbs, wp, bp, op, dim, L, silu, lengths, wo);
   else
     hipLaunchKernelGGL((causal_conv1d_fwd_kernel<T, K, false>), grid, dim3(kConvThreads), 0, st, xp,
-                       wp, bp, op, dim, L, silu, lengths, wo);
+                       xbs, wp, bp, op, dim, L, silu, lengths, wo);
   return hipGetLastError();
 }
 
@@ -347,18 +348,18 @@ hipError_t launch_bwd_k(int batch, int dim, int L, const void* x, const void* w,
 }
 
 template <typename T>
-hipError_t dispatch_fwd(int batch, int dim, int L, int K, const void* x, const void* w,
+hipError_t dispatch_fwd(int batch, int dim, int L, int K, const void* x, int64_t xbs, const void* w,
                         const void* bias, int silu, void* out, const int64_t* lengths,
                         void* window, bool vec, hipStream_t st) {
   switch (K) {
-    case 1: return launch_fwd_k<T, 1>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
-    case 2: return launch_fwd_k<T, 2>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
-    case 3: return launch_fwd_k<T, 3>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
-    case 4: return launch_fwd_k<T, 4>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
-    case 5: return launch_fwd_k<T, 5>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
-    case 6: return launch_fwd_k<T, 6>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
-    case 7: return launch_fwd_k<T, 7>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
-    case 8: return launch_fwd_k<T, 8>(batch, dim, L, x, w, bias, silu, out, lengths, window, vec, st);
+    case 1: return launch_fwd_k<T, 1>(batch, dim, L, x, xbs, w, bias, silu, out, lengths, window, vec, st);
+    case 2: return launch_fwd_k<T, 2>(batch, dim, L, x, xbs, w, bias, silu, out, lengths, window, vec, st);
+    case 3: return launch_fwd_k<T, 3>(batch, dim, L, x, xbs, w, bias, silu, out, lengths, window, vec, st);
+    case 4: return launch_fwd_k<T, 4>(batch, dim, L, x, xbs, w, bias, silu, out, lengths, window, vec, st);
+    case 5: return launch_fwd_k<T, 5>(batch, dim, L, x, xbs, w, bias, silu, out, lengths, window, vec, st);
+    case 6: return launch_fwd_k<T, 6>(batch, dim, L, x, xbs, w, bias, silu, out, lengths, window, vec, st);
+    case 7: return launch_fwd_k<T, 7>(batch, dim, L, x, xbs, w, bias, silu, out, lengths, window, vec, st);
+    case 8: return launch_fwd_k<T, 8>(batch, dim, L, x, xbs, w, bias, silu, out, lengths, window, vec, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -390,13 +391,13 @@ hipError_t dispatch_bwd(int batch, int dim, int L, int K, const void* x, const v
 int conv1d_max_width() { return kMaxWidth; }
 
 hipError_t launch_causal_conv1d_fwd(int batch, int dim, int L, int K, int dtype_bf16,
-                                    const void* x, const void* w, const void* bias, int silu,
-                                    void* out, const int64_t* lengths, void* window, bool vec,
-                                    hipStream_t st) {
-  return dtype_bf16 ? dispatch_fwd<__hip_bfloat16>(batch, dim, L, K, x, w, bias, silu, out, lengths,
-                                                   window, vec, st)
-                    : dispatch_fwd<float>(batch, dim, L, K, x, w, bias, silu, out, lengths, window,
-                                          vec, st);
+                                    const void* x, int64_t xbs, const void* w, const void* bias,
+                                    int silu, void* out, const int64_t* lengths, void* window,
+                                    bool vec, hipStream_t st) {
+  return dtype_bf16 ? dispatch_fwd<__hip_bfloat16>(batch, dim, L, K, x, xbs, w, bias, silu, out,
+                                                   lengths, window, vec, st)
+                    : dispatch_fwd<float>(batch, dim, L, K, x, xbs, w, bias, silu, out, lengths,
+                                          window, vec, st);
 }
 
 hipError_t launch_causal_conv1d_bwd(int batch, int dim, int L, int K, int dtype_bf16,

@@ -739,7 +739,11 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   const int chc = min(pch, Dm - 1);
   const T* __restrict__ u_row = u + (rb + chc) * L;
   const T* __restrict__ d_row = dl + (rb + chc) * L;
-  const T* __restrict__ z_row = zp + (rb + chc) * L;
+  // kDt: z's batch rows may lie dtp.zbstride elements apart (the gate half of
+  // the in-projection output, read in place); zb offsets z so that the row
+  // arithmetic below, which assumes dim * L, lands on them
+  const T* __restrict__ zb = kDt ? zp + (size_t)b * dtp.zbstride - (size_t)rb * L : zp;
+  const T* __restrict__ z_row = zb + (rb + chc) * L;
   int vlo, vhi;
   valid_window(length, p.pad_right, b, L, vlo, vhi);
   vhi = min(vhi, Lend);  // steps past the segment are identity steps here
@@ -771,7 +775,7 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   const uint32_t row_off = (uint32_t)((row % (kBlockCh / kWsProd)) * (size_t)L * sizeof(T));
   const auto u_ld = raw_rsrc(const_cast<T*>(u) + ((size_t)rb + wrow0) * L, wbytes);
   const auto d_ld = raw_rsrc(const_cast<T*>(dl) + ((size_t)rb + wrow0) * L, wbytes);
-  const auto z_ld = raw_rsrc(kHasZ ? const_cast<T*>(zp) + ((size_t)rb + wrow0) * L : const_cast<T*>(u),
+  const auto z_ld = raw_rsrc(kHasZ ? const_cast<T*>(zb) + ((size_t)rb + wrow0) * L : const_cast<T*>(u),
                              kHasZ ? wbytes : 0u);
   const uint32_t bc_bytes = (uint32_t)((size_t)N * L * sizeof(T));
   const auto B_ld = raw_rsrc(const_cast<T*>(Bp) + (size_t)b * p.bc_bstride, bc_bytes);

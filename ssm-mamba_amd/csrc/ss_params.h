@@ -64,6 +64,7 @@ struct DtProj {
   int P, rank;
   const void* w;        // (dim, rank) bf16
   void* delta_out;      // nullable: delta_raw as (batch, dim, seqlen) bf16
+  int64_t zbstride;     // elements between batch rows of z (>= dim * seqlen)
 };
 constexpr int kDtK = 2;  // MFMA k-steps of 32 ranks: rank <= 64
 

@@ -124,3 +124,25 @@ def test_deterministic_and_rejects_bad_width(cuda):
     assert torch.equal(grads[0], grads[1])
     with pytest.raises(RuntimeError, match="width"):
         causal_conv1d_fn(x.to(cuda), torch.randn(64, 1, 9, device=cuda), None)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("seqlen", [37, 2048])
+def test_forward_batch_strided(cuda, dtype, seqlen):
+    """x as a channel slice of a larger activation (the x half of the
+    in-projection output): read in place through its batch stride, the same
+    bits as from a contiguous copy, window and lengths included."""
+    from ssm_mamba_amd.causal_conv1d import causal_conv1d_fn
+    x, w, b = _case(3, 2 * 40, seqlen, 4, seed=seqlen)
+    big = x.to(dtype).to(cuda)
+    xs = big[:, 8:48]                       # batch stride 80 * seqlen, offset 8 rows
+    assert not xs.is_contiguous() and xs.stride(0) == 80 * seqlen
+    wd, bd = w[:40].to(dtype).to(cuda), b[:40].to(dtype).to(cuda)
+    lens = torch.tensor([seqlen, 5, 0], dtype=torch.long, device=cuda)
+    win_a = torch.zeros(3, 40, 3, dtype=dtype, device=cuda)
+    win_b = torch.zeros_like(win_a)
+    got = causal_conv1d_fn(xs, wd, bd, window=win_a, lengths=lens)
+    ref = causal_conv1d_fn(xs.contiguous(), wd, bd, window=win_b, lengths=lens)
+    assert torch.equal(got, ref) and torch.equal(win_a, win_b)
+    assert_close(got, _ref(x[:, 8:48].to(dtype).double(), w[:40].to(dtype).double(),
+                           b[:40].to(dtype).double(), True), dtype, "out strided")

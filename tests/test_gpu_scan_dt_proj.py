@@ -28,7 +28,7 @@ TOL_DELTA = dict(rtol=EPS_BF16, atol=0.0)
 
 
 def run_dt_case(cuda, batch, dim, seqlen, nstate, rank, seed, with_z=True, h_init=False,
-                length=None, padding_side="left", pstride_pad=0):
+                length=None, padding_side="left", pstride_pad=0, z_strided=False):
     print(f"dt_proj case B={batch} D={dim} L={seqlen} N={nstate} R={rank} seed={seed} "
           f"z={with_z} h0={h_init} len={None if length is None else length.tolist()} "
           f"pad={padding_side} pstride+{pstride_pad}", flush=True)
@@ -49,6 +49,12 @@ def run_dt_case(cuda, batch, dim, seqlen, nstate, rank, seed, with_z=True, h_ini
         buf[b * pstride:b * pstride + seqlen * P] = rows[b].reshape(-1)
     dev = lambda t: None if t is None else t.to(cuda).contiguous()
     u, z, A, Dv, bias, h0 = (dev(c[k]) for k in ("u", "z", "A", "D", "delta_bias", "h_init"))
+    zbs = 0
+    if z_strided and z is not None:
+        # z as the gate half of a (batch, 2 dim, L) in-projection output
+        zz = torch.empty(batch, 2 * dim, seqlen, dtype=z.dtype, device=cuda).normal_()
+        zz[:, dim:] = z
+        z, zbs = zz[:, dim:], 2 * dim * seqlen
     params, wd = dev(buf), dev(w)
     ln = None if length is None else length.to(cuda)
     out = torch.full((batch, dim, seqlen), float("nan"), dtype=torch.bfloat16, device=cuda)
@@ -64,7 +70,7 @@ def run_dt_case(cuda, batch, dim, seqlen, nstate, rank, seed, with_z=True, h_ini
         N.check(lib.ssm_selective_scan_fwd_dt_proj(
             batch, dim, seqlen, nstate, rank, N.SSM_BF16, u.data_ptr(), params.data_ptr(),
             pstride, wd.data_ptr(), A.data_ptr(), Dv.data_ptr(), bias.data_ptr(), ptr(h0), ptr(ln),
-            pr, ptr(z), 1, o.data_ptr(), ptr(delta_out), hl.data_ptr(), ws.data_ptr(), ws.numel(),
+            pr, ptr(z), zbs, 1, o.data_ptr(), ptr(delta_out), hl.data_ptr(), ws.data_ptr(), ws.numel(),
             stream))
 
     call(dout, out, last)
@@ -120,6 +126,14 @@ def test_dt_proj_batch_stride(cuda):
     """Batch rows of ssm_params further apart than seqlen * P (a padded or
     sliced buffer)."""
     run_dt_case(cuda, 2, 64, 64, 16, 64, seed=8, pstride_pad=24)
+
+
+def test_dt_proj_gate_batch_stride(cuda):
+    """z read in place as the gate half of the in-projection output, aligned
+    and ragged lengths."""
+    run_dt_case(cuda, 3, 128, 256, 16, 64, seed=11, z_strided=True)
+    run_dt_case(cuda, 2, 64, 37, 16, 64, seed=12, z_strided=True,
+                length=torch.tensor([37, 20], dtype=torch.int64))
 
 
 def test_dt_proj_sequence_split(cuda):

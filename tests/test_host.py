@@ -162,12 +162,12 @@ def test_dt_proj_shapes_and_arguments_are_checked():
 
     def call(**kw):
         a = dict(batch=2, dim=64, seqlen=16, nstate=16, rank=64, dtype=N.SSM_BF16, u=P, params=P,
-                 pstride=0, w=P, A=P, out=P, ws=P)
+                 pstride=0, w=P, A=P, z=None, zbs=0, out=P, ws=P)
         a.update(kw)
         return lib.ssm_selective_scan_fwd_dt_proj(
             a["batch"], a["dim"], a["seqlen"], a["nstate"], a["rank"], a["dtype"], a["u"],
-            a["params"], a["pstride"], a["w"], a["A"], None, None, None, None, 0, None, 1, a["out"],
-            None, None, a["ws"], ws, None)
+            a["params"], a["pstride"], a["w"], a["A"], None, None, None, None, 0, a["z"], a["zbs"],
+            1, a["out"], None, None, a["ws"], ws, None)
 
     # SSM_ERR_INVALID = 1, SSM_ERR_UNSUPPORTED = 2
     assert call(dtype=N.SSM_F32) == 2 and b"bf16" in lib.ssm_last_error()
@@ -176,9 +176,20 @@ def test_dt_proj_shapes_and_arguments_are_checked():
     assert call(pstride=16 * 96 - 8) == 1 and b"params_batch_stride" in lib.ssm_last_error()
     assert call(pstride=16 * 96 + 4) == 2 and b"16-byte" in lib.ssm_last_error()
     assert call(params=P + 8) == 2 and b"16-byte" in lib.ssm_last_error()
+    assert call(z=P, zbs=64 * 16 - 8) == 1 and b"z_batch_stride" in lib.ssm_last_error()
     assert call(ws=None) == 1 and b"workspace" in lib.ssm_last_error()
     # the shape query leaves the last error message alone
     assert ok(2, 64, 16, 16, 72, N.SSM_BF16) == 0 and b"workspace" in lib.ssm_last_error()
+
+
+def test_conv_batch_stride_is_checked():
+    """The conv forward's x batch stride: 0 (contiguous) or at least dim * seqlen."""
+    from ssm_mamba_amd import _native as N
+    lib = N.lib()
+    P = 4096  # never dereferenced
+    rc = lib.ssm_causal_conv1d_fwd(2, 8, 16, 4, N.SSM_BF16, P, 8 * 16 - 1, P, None, 1, P, None,
+                                   None, None)
+    assert rc == 1 and b"x_batch_stride" in lib.ssm_last_error()
 
 
 def _scan_args(batch=2, dim=4, seqlen=8, nstate=3):
