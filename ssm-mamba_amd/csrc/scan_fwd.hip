@@ -591,9 +591,10 @@ struct WsRows<T, true> {
 // (((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)) over its columns c), so
 // both kernels add the same numbers in the same order.
 //
-// kDt: delta_raw from the fused step-size projection (DtProj) instead of dl,
-// and B / C from the token rows of dtp.params instead of Bp / Cp.
-template <typename T, int kZ, bool kAligned, bool kSum, bool kDt = false>
+// kDt (1, or 2 to also store delta_raw to dtp.delta_out): delta_raw from the
+// fused step-size projection (DtProj) instead of dl, and B / C from the token
+// rows of dtp.params instead of Bp / Cp.
+template <typename T, int kZ, bool kAligned, bool kSum, int kDt = 0>
 __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     const ScanDims p, const T* __restrict__ u, const T* __restrict__ dl,
     const float* __restrict__ Ap, const T* __restrict__ Bp, const T* __restrict__ Cp,
@@ -604,6 +605,8 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     float* __restrict__ seg_h, float* __restrict__ seg_dt, const DtProj dtp) {
   static_assert(!kSum || kZ == 0, "the summaries read no gate");
   static_assert(!kDt || sizeof(T) == 2, "the fused projection reads bf16");
+  static_assert(kDt != 2 || !kSum, "the summaries store no delta_raw");
+  constexpr bool kDtOut = kDt == 2;
   constexpr bool kHasZ = kZ != 0;
   constexpr bool kSaveY = kZ == 2;
   constexpr int kT4 = kWsTile / 4;
@@ -814,7 +817,7 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     }
   }
 
-  auto issue = [&](WsRows<T, kDt>& r, int i) {
+  auto issue = [&](WsRows<T, kDt != 0>& r, int i) {
     const int t0 = min(Tbeg + i * kWsTile, last_t0);
     if constexpr (kDt) {
       const uint32_t tb = (uint32_t)t0 * prow_bytes;  // wave-uniform
@@ -858,17 +861,16 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   // for its finish; with kSum, delta is also added to the sum of tile parity
   // par (i % 2)
   float dts[2] = {0.0f, 0.0f};  // kSum: step sizes of the even and odd tiles
-  // kDt: the wave's 16 rows of delta_out (rows past the last channel lie
-  // outside the range; an empty range without delta_out)
+  // kDtOut: the wave's 16 rows of delta_out (rows past the last channel lie
+  // outside the range)
   const auto dto_rsrc =
-      raw_rsrc(kDt && !kSum && dtp.delta_out
-                   ? static_cast<char*>(dtp.delta_out) + ((size_t)rb + wrow0) * L * sizeof(T)
-                   : static_cast<char*>(dummy),
-               kDt && !kSum && dtp.delta_out ? wbytes : 0u);
+      raw_rsrc(kDtOut ? static_cast<char*>(dtp.delta_out) + ((size_t)rb + wrow0) * L * sizeof(T)
+                      : static_cast<char*>(dummy),
+               kDtOut ? wbytes : 0u);
   // kDt: a tile's delta_raw (steps 4 (lane / 16) .. + 3 of channel lane % 16
   // of the wave's 16), issued an iteration before the tile is staged so that
   // the MFMA latency runs under that iteration's other work
-  auto proj = [&](const WsRows<T, kDt>& r) {
+  auto proj = [&](const WsRows<T, kDt != 0>& r) {
     f32x4_v acc = {0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (kDt) {
 #pragma unroll
@@ -878,7 +880,7 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
     }
     return acc;
   };
-  auto stage = [&](const WsRows<T, kDt>& r, const f32x4_v acc, int i, int sbuf, float (&sk)[4],
+  auto stage = [&](const WsRows<T, kDt != 0>& r, const f32x4_v acc, int i, int sbuf, float (&sk)[4],
                    float (&gt)[4], int par) {
     const int t_tile = Tbeg + i * kWsTile;
     const int t = t_tile + 4 * q;
@@ -890,11 +892,10 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
       const uint32_t x01 = pack_bf16x2(acc[0], acc[1]);
       const uint32_t x23 = pack_bf16x2(acc[2], acc[3]);
       decode4(make_uint2(x01, x23), dv);
-      if constexpr (!kSum) {
-        // delta_out: stored without a branch (a conditional path with memory
-        // operations makes the compiler wait for the ring's loads at the
-        // merge); without delta_out the range is empty and the stores are
-        // dropped.  Aligned rows: L and the segment ends are multiples of 4,
+      if constexpr (kDtOut) {
+        // delta_out (its own instantiation: a conditional path with memory
+        // operations would make the compiler wait for the ring's loads at the
+        // merge).  Aligned rows: L and the segment ends are multiples of 4,
         // so the 4 steps are one 8-byte piece inside the row or wholly past
         // its end.
         if constexpr (kAligned) {
@@ -1061,7 +1062,7 @@ __global__ __launch_bounds__(kWsThreads) void scan_fwd_ws_kernel(
   // into the loop header makes it wait for nearly all of them).  Work past
   // the last tile is harmless: its loads are clamped into the rows, its
   // staging buffers are never read and its stores fall outside the range.
-  WsRows<T, kDt> rows[kWsRing];
+  WsRows<T, kDt != 0> rows[kWsRing];
   float sk[4][4], gt[4][4];
   float4 v[kWsCons];
 #pragma unroll
@@ -1583,12 +1584,12 @@ hipError_t launch_scan_fwd(const ScanParams& p, int dtype, bool aligned, float* 
 // delta, B and C arguments get valid addresses they never load from.
 bool scan_fwd_dt_supported(const ScanParams& p) { return p.nstate <= 16 && ws_forward(p, 2); }
 
-template <int kZ, bool kAligned, bool kSum>
+template <int kZ, bool kAligned, bool kSum, int kDt>
 static void launch_ws_dt(const ScanParams& p, const DtProj& dt, hipStream_t st) {
   using T = __hip_bfloat16;
   const int gz = kSum ? (p.nseg - 1) * p.sub_k : p.nseg;
   const T* prm = static_cast<const T*>(dt.params);
-  hipLaunchKernelGGL((scan_fwd_ws_kernel<T, kZ, kAligned, kSum, true>), dim3(p.nblk, p.batch, gz),
+  hipLaunchKernelGGL((scan_fwd_ws_kernel<T, kZ, kAligned, kSum, kDt>), dim3(p.nblk, p.batch, gz),
                      dim3(kWsThreads), 0, st, dims_of(p), (const T*)p.u, (const T*)p.u, p.A, prm,
                      prm, p.D, p.bias, p.h_init, p.length, (const T*)p.z, (T*)p.out,
                      (T*)nullptr, (float*)nullptr, p.h_last, p.dummy, p.seg_h, p.seg_dt, dt);
@@ -1597,18 +1598,23 @@ static void launch_ws_dt(const ScanParams& p, const DtProj& dt, hipStream_t st) 
 hipError_t launch_scan_fwd_dt(const ScanParams& p, const DtProj& dt, bool aligned, hipStream_t st) {
   if (p.nseg > 1) {
     ProfScope prof("scan_fwd_segsum", st);
-    if (aligned) launch_ws_dt<0, true, true>(p, dt, st);
-    else launch_ws_dt<0, false, true>(p, dt, st);
+    if (aligned) launch_ws_dt<0, true, true, 1>(p, dt, st);
+    else launch_ws_dt<0, false, true, 1>(p, dt, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   ProfScope prof("scan_fwd", st);
-  if (p.z) {
-    if (aligned) launch_ws_dt<1, true, false>(p, dt, st);
-    else launch_ws_dt<1, false, false>(p, dt, st);
-  } else {
-    if (aligned) launch_ws_dt<0, true, false>(p, dt, st);
-    else launch_ws_dt<0, false, false>(p, dt, st);
+  // with delta_out, the instantiation that stores it
+  const int k = (p.z ? 2 : 0) + (aligned ? 1 : 0) + (dt.delta_out ? 4 : 0);
+  switch (k) {
+    case 0: launch_ws_dt<0, false, false, 1>(p, dt, st); break;
+    case 1: launch_ws_dt<0, true, false, 1>(p, dt, st); break;
+    case 2: launch_ws_dt<1, false, false, 1>(p, dt, st); break;
+    case 3: launch_ws_dt<1, true, false, 1>(p, dt, st); break;
+    case 4: launch_ws_dt<0, false, false, 2>(p, dt, st); break;
+    case 5: launch_ws_dt<0, true, false, 2>(p, dt, st); break;
+    case 6: launch_ws_dt<1, false, false, 2>(p, dt, st); break;
+    default: launch_ws_dt<1, true, false, 2>(p, dt, st); break;
   }
   return hipGetLastError();
 }
