@@ -154,3 +154,30 @@ def test_dt_proj_rejects_unsupported(cuda):
     assert lib.ssm_selective_scan_fwd_dt_proj_supported(2, 64, 64, 16, 60, N.SSM_BF16) == 0
     assert lib.ssm_selective_scan_fwd_dt_proj_supported(2, 64, 64, 32, 64, N.SSM_BF16) == 0
     assert lib.ssm_selective_scan_fwd_dt_proj_supported(2, 64, 64, 6, 64, N.SSM_BF16) == 0
+
+
+def _sweep_config(seed):
+    import random
+    g = random.Random(seed)
+    batch = g.choice([1, 2, 3])
+    seqlen = g.choice([1, 2, 7, 16, 33, 64, 100, 128, 250, 256, 300, 513, 600])
+    length = None
+    if g.random() < 0.5:
+        length = torch.tensor([g.randint(0, seqlen) for _ in range(batch)], dtype=torch.int64)
+    return dict(batch=batch, dim=g.choice([64, 80, 130, 256]), seqlen=seqlen,
+                nstate=g.choice([4, 8, 12, 16, 16]), rank=g.choice([8, 16, 24, 32, 40, 48, 56, 64]),
+                with_z=g.random() < 0.8, h_init=g.random() < 0.5, length=length,
+                padding_side=g.choice(["left", "right"]), pstride_pad=g.choice([0, 0, 8, 40]),
+                z_strided=g.random() < 0.3)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_dt_proj_sweep(cuda, seed):
+    """Seeded irregular shapes: part-filled channel blocks, ragged and aligned
+    lengths, 4-16 states, ranks 8-64, gate or none, h_init, lengths on either
+    side, padded ssm_params rows and a batch-strided gate."""
+    c = _sweep_config(500 + seed)
+    run_dt_case(cuda, c["batch"], c["dim"], c["seqlen"], c["nstate"], c["rank"], seed=900 + seed,
+                with_z=c["with_z"], h_init=c["h_init"], length=c["length"],
+                padding_side=c["padding_side"], pstride_pad=c["pstride_pad"],
+                z_strided=c["z_strided"])
