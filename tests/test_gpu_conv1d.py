@@ -146,3 +146,22 @@ def test_forward_batch_strided(cuda, dtype, seqlen):
     assert torch.equal(got, ref) and torch.equal(win_a, win_b)
     assert_close(got, _ref(x[:, 8:48].to(dtype).double(), w[:40].to(dtype).double(),
                            b[:40].to(dtype).double(), True), dtype, "out strided")
+
+
+def test_backward_batch_strided_input(cuda):
+    """Autograd through a batch-strided x (a channel slice): the gradients
+    equal those of a contiguous copy bit for bit."""
+    from ssm_mamba_amd.causal_conv1d import causal_conv1d_fn
+    x, w, b = _case(2, 64, 96, 4, seed=77)
+    big = x.repeat(1, 2, 1).to(cuda)                 # (2, 128, 96); use channels 32..95
+    dy = torch.randn(2, 64, 96, generator=torch.Generator().manual_seed(78)).to(cuda)
+    grads = []
+    for strided in (True, False):
+        xb = big.clone().requires_grad_(True)
+        xs = xb[:, 32:96] if strided else xb[:, 32:96].contiguous()
+        wd = w.to(cuda).requires_grad_(True)
+        bd = b.to(cuda).requires_grad_(True)
+        causal_conv1d_fn(xs, wd, bd).backward(dy)
+        grads.append((xb.grad.clone(), wd.grad.clone(), bd.grad.clone()))
+    for g1, g2 in zip(*grads):
+        assert torch.equal(g1, g2)
